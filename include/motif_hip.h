@@ -1,0 +1,199 @@
+/*
+ * motif_hip.h — C ABI of the MI355X (gfx950) decode-attention hot path of
+ * junhoyeo/mlx-motif.
+ *
+ * One ABI serves every host binding: Python (ctypes, mlx-motif_amd/mlx_motif)
+ * and a Swift C-module (module map in mlx-motif_amd/swift/).  The signatures
+ * hold only plain pointers, integers and floats: no HIP, torch or MLX types.
+ *
+ * Conventions
+ *  - Every device pointer is caller-owned device memory on the current HIP
+ *    device; tensors are dense row-major ("row-contiguous") in the shapes
+ *    given per function.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Calls only enqueue work; they never synchronise the stream.
+ *  - Return value: MOTIF_OK, or a negative status.  motif_last_error() then
+ *    returns a message (thread-local, valid until the next call on the same
+ *    thread).  Contract checks run before any HIP call, so a rejected call
+ *    touches no device state.
+ *  - dtype codes name the element type of q / k / v / y and of quantisation
+ *    scales and biases: MOTIF_F16 (IEEE half), MOTIF_BF16, MOTIF_F32.
+ *  - Split-KV attention needs a workspace: size it with
+ *    motif_sdpa_workspace_bytes().  Its first motif_sdpa_counter_bytes()
+ *    bytes are arrival counters that must be zero before the first call;
+ *    every call leaves them zero again.  Calls that share one workspace must
+ *    be ordered (same stream); concurrent calls need separate workspaces.
+ */
+#ifndef MOTIF_HIP_H
+#define MOTIF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOTIF_ABI_VERSION 1
+
+#define MOTIF_OK 0
+#define MOTIF_ERR_CONTRACT (-1)    /* violates the reference kernel contract   */
+#define MOTIF_ERR_UNSUPPORTED (-2) /* legal shape with no compiled variant     */
+#define MOTIF_ERR_WORKSPACE (-3)   /* workspace missing or too small           */
+#define MOTIF_ERR_HIP (-4)         /* HIP runtime error (launch, device query) */
+
+#define MOTIF_F16 0
+#define MOTIF_BF16 1
+#define MOTIF_F32 2
+
+/* Version of this ABI (MOTIF_ABI_VERSION of the build). */
+int motif_abi_version(void);
+
+/* Message for the last non-OK status on this thread ("" if none). */
+const char* motif_last_error(void);
+
+/* ------------------------------------------------------------------------ *
+ * Workspace sizing for the split-KV attention entry points.
+ * S_q = query rows per head (1 for decode), kv_len = live KV rows,
+ * D = head dim.  Counters come first, then partial results.
+ * ------------------------------------------------------------------------ */
+size_t motif_sdpa_counter_bytes(int B, int Hq, int Hkv, int S_q);
+size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
+
+/* ------------------------------------------------------------------------ *
+ * Shared-QK dual-V SDPA over an fp16/bf16/fp32 4-slot cache.
+ * Replaces sdpa_dual_v (src/mlx_motif/kernels/attention.py:190-260) and its
+ * Metal kernel motif_sdpa_dual_v (attention.py:53-166).
+ *
+ *   q      (B, Hq, 1, D)          dtype
+ *   k,v1,v2 (B, Hkv, kv_cap, D)   dtype, rows >= kv_len never read
+ *   y      (B, Hq, 1, 2D)         dtype = [softmax(scale q K^T) V1 || ... V2]
+ * Query head h reads KV head h / (Hq/Hkv) (repeat-interleave GQA).
+ * kv_len == 0 writes zeros.
+ * Contract (reference asserts attention.py:237-243): D % 32 == 0,
+ * Hq % Hkv == 0, 0 <= kv_len <= kv_cap.
+ * ------------------------------------------------------------------------ */
+int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
+                      int dtype, int B, int Hq, int Hkv, int D, int kv_cap, int kv_len,
+                      float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Same, reading the packed MLX-affine q4/q8 cache directly.
+ * Replaces sdpa_dual_v_q4 (attention.py:510-645) and its Metal kernel
+ * motif_sdpa_dual_v_q4 (attention.py:293-445).
+ *
+ *   *_data   (B, Hkv, kv_cap, D*bits/32) uint32, value i of a row at bits
+ *            [(i % (32/bits))*bits, +bits) of word i / (32/bits)
+ *   *_scales (B, Hkv, kv_cap, D/group_size) dtype
+ *   *_biases (B, Hkv, kv_cap, D/group_size) dtype
+ *   dequantised value = scale * u + bias (u unsigned, no zero point).
+ * Contract (attention.py:556-608): bits in {4,8}, D % 32 == 0,
+ * D % group_size == 0, (32/bits) % (D/32) == 0, group_size % (D/32) == 0,
+ * Hq % Hkv == 0, 0 <= kv_len <= kv_cap.
+ * ------------------------------------------------------------------------ */
+int motif_sdpa_dual_v_q(const void* q,
+                        const uint32_t* k_data, const void* k_scales, const void* k_biases,
+                        const uint32_t* v1_data, const void* v1_scales, const void* v1_biases,
+                        const uint32_t* v2_data, const void* v2_scales, const void* v2_biases,
+                        void* y, int dtype, int B, int Hq, int Hkv, int D, int kv_cap,
+                        int kv_len, int bits, int group_size, float scale, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Multi-row (speculative-verify / chunked-prefill) dual-V SDPA, S_q query
+ * rows per head, bottom-right-aligned causal mask when causal != 0: row i of
+ * S_q attends keys [0, kv_len - S_q + i].  q (B,Hq,S_q,D), y (B,Hq,S_q,2D).
+ * Replaces the FALLBACK composition model.py:769-807 (4 masked
+ * mx.fast.scaled_dot_product_attention calls + concat) for the 4-slot cache;
+ * the reference has no kernel for it.
+ * The _q variant reads the packed cache like motif_sdpa_dual_v_q (the
+ * reference dequantises through cache.py:448-465 first).
+ * ------------------------------------------------------------------------ */
+int motif_sdpa_dual_v_rows(const void* q, const void* k, const void* v1, const void* v2, void* y,
+                           int dtype, int B, int Hq, int Hkv, int S_q, int D, int kv_cap,
+                           int kv_len, int causal, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+int motif_sdpa_dual_v_q_rows(const void* q,
+                             const uint32_t* k_data, const void* k_scales, const void* k_biases,
+                             const uint32_t* v1_data, const void* v1_scales,
+                             const void* v1_biases, const uint32_t* v2_data,
+                             const void* v2_scales, const void* v2_biases, void* y, int dtype,
+                             int B, int Hq, int Hkv, int S_q, int D, int kv_cap, int kv_len,
+                             int causal, int bits, int group_size, float scale,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * MLX affine quantisation (mx.quantize, mode "affine") of `rows` rows of D
+ * values: data (rows, D*bits/32) uint32, scales/biases (rows, D/group_size)
+ * in dtype.  The reference calls mx.quantize at cache.py:498 and
+ * cache.py:399-402.  bits in {4,8}, group_size in {32,64,128},
+ * D % group_size == 0.
+ * ------------------------------------------------------------------------ */
+int motif_quantize(const void* x, uint32_t* data, void* scales, void* biases, int dtype,
+                   int64_t rows, int D, int bits, int group_size, void* stream);
+
+/* Dequantisation y = dtype(float(scale) * u + float(bias)); replaces the
+ * _dequant_probe kernel (src/mlx_motif/kernels/mlp.py:176-255) and serves the
+ * dequant bridge (cache.py:448-465). */
+int motif_dequantize(const uint32_t* data, const void* scales, const void* biases, void* y,
+                     int dtype, int64_t rows, int D, int bits, int group_size, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Batched 4-slot quantised cache write in ONE dispatch: quantise rows
+ * [0,S) of k1,k2,v1,v2 (each (B,H,S,D) dtype) and store them at rows
+ * [offset, offset+S) of the four cache triples, each of capacity kv_cap:
+ *   data[i] (B,H,kv_cap,D*bits/32) uint32, scales[i]/biases[i]
+ *   (B,H,kv_cap,D/group_size) dtype; i = 0..3 for k1,k2,v1,v2.
+ * Replaces MotifGroupedQuantizedKVCache._update_4 (cache.py:485-512:
+ * concat + one mx.quantize + 12 slice writes).  Requires
+ * offset + S <= kv_cap (the host grows capacity first, cache.py:245-265).
+ * ------------------------------------------------------------------------ */
+int motif_quant_write4(const void* k1, const void* k2, const void* v1, const void* v2,
+                       uint32_t* const data[4], void* const scales[4], void* const biases[4],
+                       int dtype, int B, int H, int S, int D, int kv_cap, int offset, int bits,
+                       int group_size, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Fused GDA epilogue on split inputs (gda_post_split, gda.py:223-282):
+ *   d = o[b,h,s,:] - lambda * n[b,h/gr,s,:]
+ *   y = dtype(d * rsqrt(mean(d^2) + eps) * w * one_minus_lambda_init)
+ * o (B,q_origin,S,C), n (B,q_groups,S,C), w (C) dtype, y like o.
+ * lambda_full: device pointer to ONE fp32 value (no host sync).
+ * Contract (gda.py:248): q_origin == q_groups * gr.
+ * ------------------------------------------------------------------------ */
+int motif_gda_post_split(const void* attn_o, const void* attn_n, const void* subln_w, void* y,
+                         int dtype, int B, int q_origin, int q_groups, int gr, int S, int C,
+                         const float* lambda_full, float one_minus_lambda_init, float eps,
+                         void* stream);
+
+/* Same epilogue on the merged layout (gda_post, gda.py:285-341): merged is
+ * (B, q_groups*gr + q_groups, S, C); noise head of origin head h is
+ * q_groups*gr + h/gr. */
+int motif_gda_post(const void* merged, const void* subln_w, void* y, int dtype, int B,
+                   int q_groups, int gr, int S, int C, const float* lambda_full,
+                   float one_minus_lambda_init, float eps, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Fused PolyNorm (polynorm, src/mlx_motif/kernels/mlp.py:119-157):
+ *   y = w0*x^3*rsqrt(mean(x^6)+eps) + w1*x^2*rsqrt(mean(x^4)+eps)
+ *     + w2*x*rsqrt(mean(x^2)+eps) + b
+ * over the last axis of x (rows, D); weight (3) and bias (1) are dtype device
+ * arrays.  x is read from HBM once.
+ * ------------------------------------------------------------------------ */
+int motif_polynorm(const void* x, const void* weight, const void* bias, void* y, int dtype,
+                   int64_t rows, int D, float eps, void* stream);
+
+/* ------------------------------------------------------------------------ *
+ * Tuning knobs of the split-KV kernels (process-wide; for benchmarks and
+ * sweeps, not needed for correct use).  key: "rows_per_split",
+ * "waves_per_wg", "min_wgs".  value 0 restores the default.  Returns
+ * MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key.
+ * ------------------------------------------------------------------------ */
+int motif_set_tuning(const char* key, int value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOTIF_HIP_H */

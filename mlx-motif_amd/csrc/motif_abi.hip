@@ -1,0 +1,147 @@
+// C-ABI plumbing shared by every entry point: thread-local error messages,
+// tuning knobs, device queries and the split-KV launch plan.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "motif_common.hpp"
+#include "sdpa_plan.hpp"
+
+namespace motif {
+
+static thread_local char g_err[512] = {0};
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return MOTIF_ERR_HIP;
+  }
+  return MOTIF_OK;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+Tuning& tuning() {
+  static Tuning t;
+  return t;
+}
+
+static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max) {
+  SdpaPlan p{};
+  const int G = Hkv > 0 ? Hq / Hkv : 1;
+  const int GV = G * S_q;
+  int gc = 1;
+  while (gc < GV && gc < gc_max) gc *= 2;
+  p.gc = gc;
+  p.nchunk = (GV + gc - 1) / gc;
+  p.waves = tuning().waves_per_wg == 8 ? 8 : 4;
+
+  const int units = B * Hkv * p.nchunk;
+  // Rows one block iteration of a workgroup consumes: waves x rows per wave
+  // load (4 for 16 lanes per row) x unroll 4.  Splits are whole iterations.
+  const int step = p.waves * 4 * 4;
+  int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : 2 * device_cu_count();
+  int rows = kv_len > 0 ? kv_len : 1;
+  int rps;
+  if (tuning().rows_per_split > 0) {
+    rps = tuning().rows_per_split;
+  } else {
+    int nsplit = (min_wgs + units - 1) / units;
+    int max_split = (rows + step - 1) / step;  // at least one iteration each
+    if (nsplit > max_split) nsplit = max_split;
+    if (nsplit < 1) nsplit = 1;
+    rps = (rows + nsplit - 1) / nsplit;
+  }
+  rps = (int)round_up((size_t)rps, (size_t)step);
+  p.rows_per_split = rps;
+  p.nsplit = (rows + rps - 1) / rps;
+  if (p.nsplit < 1) p.nsplit = 1;
+
+  const size_t vrows = (size_t)B * Hq * S_q;
+  p.counter_bytes = round_up(vrows * sizeof(unsigned), 256);
+  size_t part = 0;
+  if (p.nsplit > 1) {
+    part = round_up(vrows * p.nsplit * 2 * D * sizeof(float), 256) +
+           round_up(vrows * p.nsplit * 2 * sizeof(float), 256);
+  }
+  p.workspace_bytes = p.counter_bytes + part;
+  return p;
+}
+
+}  // namespace motif
+
+using namespace motif;
+
+extern "C" {
+
+int motif_abi_version(void) { return MOTIF_ABI_VERSION; }
+
+const char* motif_last_error(void) { return g_err; }
+
+size_t motif_sdpa_counter_bytes(int B, int Hq, int Hkv, int S_q) {
+  (void)Hkv;
+  if (B <= 0 || Hq <= 0 || S_q <= 0) return 0;
+  return round_up((size_t)B * Hq * S_q * sizeof(unsigned), 256);
+}
+
+size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || S_q <= 0 || D <= 0 || kv_len < 0) return 0;
+  return plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D)).workspace_bytes;
+}
+
+int motif_set_tuning(const char* key, int value) {
+  clear_error();
+  if (!key) {
+    set_error("motif_set_tuning: null key");
+    return MOTIF_ERR_CONTRACT;
+  }
+  if (value < 0) {
+    set_error("motif_set_tuning: negative value %d", value);
+    return MOTIF_ERR_CONTRACT;
+  }
+  if (!strcmp(key, "rows_per_split")) {
+    tuning().rows_per_split = value;
+  } else if (!strcmp(key, "waves_per_wg")) {
+    if (value != 0 && value != 4 && value != 8) {
+      set_error("motif_set_tuning: waves_per_wg must be 0, 4 or 8");
+      return MOTIF_ERR_CONTRACT;
+    }
+    tuning().waves_per_wg = value;
+  } else if (!strcmp(key, "min_wgs")) {
+    tuning().min_wgs = value;
+  } else {
+    set_error("motif_set_tuning: unknown key '%s'", key);
+    return MOTIF_ERR_CONTRACT;
+  }
+  return MOTIF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,241 @@
+// Fused PolyNorm on gfx950 (src/mlx_motif/kernels/mlp.py:21-93):
+//   rs_k = rsqrt(mean(x^(2k)) + eps), k = 1..3
+//   y    = T(w0*(x^3*rs3) + w1*(x^2*rs2) + w2*(x*rs1) + b), fp32 math.
+// The reference kernel reads each row twice (sums, then outputs).  Here a
+// row is held in registers between the reduction and the store, so x is read
+// from HBM once: LPR lanes per row, NCH chunks of 8 values per lane.
+//   LPR = 16  : rows of <= 128 values, 16 rows per 256-thread workgroup
+//   LPR = 64  : rows of <= 2048 values, one wave per row
+//   LPR = 256 : rows of <= 32768 values, one workgroup per row (LDS merge)
+// Rows whose length is not a multiple of 8, or longer, take a strided
+// scalar path that reads x twice.
+#include "motif_common.hpp"
+
+namespace motif {
+
+struct PolyArgs {
+  const void* x;
+  const void* w;  // (3)
+  const void* b;  // (1)
+  void* y;
+  long rows;
+  int D;
+  float eps;
+};
+
+template <typename T>
+__device__ inline void load8v(const void* base, long idx, float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    uint4 q = *reinterpret_cast<const uint4*>((const uint16_t*)base + idx);
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = Elem<T>::get(w, i);
+  } else {
+    const float4* p = reinterpret_cast<const float4*>((const float*)base + idx);
+    float4 a = p[0], c = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+  }
+}
+
+template <typename T>
+__device__ inline void store8v(void* base, long idx, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)Elem<T>::from_f32(v[2 * i]) |
+             ((uint32_t)Elem<T>::from_f32(v[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>((uint16_t*)base + idx) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    float4* p = reinterpret_cast<float4*>((float*)base + idx);
+    p[0] = make_float4(v[0], v[1], v[2], v[3]);
+    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+__device__ inline float poly_out(float v, float rs2, float rs4, float rs6, float w0, float w1,
+                                 float w2, float b) {
+  const float v2 = v * v;
+  const float v3 = v2 * v;
+  return w0 * (v3 * rs6) + w1 * (v2 * rs4) + w2 * (v * rs2) + b;
+}
+
+template <typename T, int LPR, int NCH>
+__global__ void __launch_bounds__(256) polynorm_vec_kernel(PolyArgs a) {
+  constexpr int RPB = 256 / LPR;  // rows per block
+  const int tid = threadIdx.x;
+  const int sub = tid % LPR;
+  const long row = (long)blockIdx.x * RPB + tid / LPR;
+  const bool active = row < a.rows;
+  const int nchunks = a.D / 8;
+  const long base = (active ? row : 0) * (long)a.D;
+
+  float v[NCH][8];
+  float s2 = 0.f, s4 = 0.f, s6 = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = sub + LPR * j;
+    if (active && c < nchunks) {
+      load8v<T>(a.x, base + (long)c * 8, v[j]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x2 = v[j][e] * v[j][e];
+      const float x4 = x2 * x2;
+      s2 += x2;
+      s4 += x4;
+      s6 += x4 * x2;
+    }
+  }
+  if constexpr (LPR <= 64) {
+    s2 = group_sum<LPR>(s2);
+    s4 = group_sum<LPR>(s4);
+    s6 = group_sum<LPR>(s6);
+  } else {
+    __shared__ float red[3][4];
+    s2 = group_sum<64>(s2);
+    s4 = group_sum<64>(s4);
+    s6 = group_sum<64>(s6);
+    const int wave = tid >> 6;
+    if ((tid & 63) == 0) {
+      red[0][wave] = s2;
+      red[1][wave] = s4;
+      red[2][wave] = s6;
+    }
+    __syncthreads();
+    s2 = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    s4 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    s6 = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+  }
+  if (!active) return;
+  const float inv_d = 1.0f / (float)a.D;
+  const float rs2 = rsqrtf(s2 * inv_d + a.eps);
+  const float rs4 = rsqrtf(s4 * inv_d + a.eps);
+  const float rs6 = rsqrtf(s6 * inv_d + a.eps);
+  const float w0 = Elem<T>::load(a.w, 0), w1 = Elem<T>::load(a.w, 1), w2 = Elem<T>::load(a.w, 2);
+  const float bb = Elem<T>::load(a.b, 0);
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = sub + LPR * j;
+    if (c < nchunks) {
+      float out[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = poly_out(v[j][e], rs2, rs4, rs6, w0, w1, w2, bb);
+      store8v<T>(a.y, base + (long)c * 8, out);
+    }
+  }
+}
+
+// Any D: one workgroup per row, two passes over x.
+template <typename T>
+__global__ void __launch_bounds__(256) polynorm_scalar_kernel(PolyArgs a) {
+  const long row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const long base = row * (long)a.D;
+  float s2 = 0.f, s4 = 0.f, s6 = 0.f;
+  for (int i = tid; i < a.D; i += 256) {
+    const float v = Elem<T>::load(a.x, base + i);
+    const float x2 = v * v, x4 = x2 * x2;
+    s2 += x2;
+    s4 += x4;
+    s6 += x4 * x2;
+  }
+  __shared__ float red[3][4];
+  s2 = group_sum<64>(s2);
+  s4 = group_sum<64>(s4);
+  s6 = group_sum<64>(s6);
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) {
+    red[0][wave] = s2;
+    red[1][wave] = s4;
+    red[2][wave] = s6;
+  }
+  __syncthreads();
+  s2 = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+  s4 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+  s6 = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+  const float inv_d = 1.0f / (float)a.D;
+  const float rs2 = rsqrtf(s2 * inv_d + a.eps);
+  const float rs4 = rsqrtf(s4 * inv_d + a.eps);
+  const float rs6 = rsqrtf(s6 * inv_d + a.eps);
+  const float w0 = Elem<T>::load(a.w, 0), w1 = Elem<T>::load(a.w, 1), w2 = Elem<T>::load(a.w, 2);
+  const float bb = Elem<T>::load(a.b, 0);
+  for (int i = tid; i < a.D; i += 256)
+    Elem<T>::store(a.y, base + i,
+                   poly_out(Elem<T>::load(a.x, base + i), rs2, rs4, rs6, w0, w1, w2, bb));
+}
+
+template <typename T, int LPR>
+static void launch_poly_lpr(const PolyArgs& a, int nch, hipStream_t st) {
+  const unsigned blocks = (unsigned)((a.rows + 256 / LPR - 1) / (256 / LPR));
+  switch (nch) {
+#define MOTIF_POLY_CASE(N)                                                               \
+  case N:                                                                                \
+    hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, N>), blocks, 256, 0, st, a); break;
+    MOTIF_POLY_CASE(1)
+    MOTIF_POLY_CASE(2)
+    MOTIF_POLY_CASE(3)
+    MOTIF_POLY_CASE(4)
+    MOTIF_POLY_CASE(5)
+    MOTIF_POLY_CASE(6)
+    MOTIF_POLY_CASE(7)
+    MOTIF_POLY_CASE(8)
+    MOTIF_POLY_CASE(9)
+    MOTIF_POLY_CASE(10)
+    MOTIF_POLY_CASE(11)
+    MOTIF_POLY_CASE(12)
+    MOTIF_POLY_CASE(13)
+    MOTIF_POLY_CASE(14)
+    MOTIF_POLY_CASE(15)
+    MOTIF_POLY_CASE(16)
+#undef MOTIF_POLY_CASE
+    default: break;
+  }
+}
+
+template <typename T>
+static int launch_poly(const PolyArgs& a, bool vec_ok, hipStream_t st) {
+  const int nchunks = a.D / 8;
+  if (vec_ok && a.D % 8 == 0) {
+    if (nchunks <= 16) {
+      launch_poly_lpr<T, 16>(a, 1, st);
+      return check_launch("polynorm");
+    }
+    if (nchunks <= 64 * 4) {
+      launch_poly_lpr<T, 64>(a, (nchunks + 63) / 64, st);
+      return check_launch("polynorm");
+    }
+    if (nchunks <= 256 * 16) {
+      launch_poly_lpr<T, 256>(a, (nchunks + 255) / 256, st);
+      return check_launch("polynorm");
+    }
+  }
+  hipLaunchKernelGGL((polynorm_scalar_kernel<T>), (unsigned)a.rows, 256, 0, st, a);
+  return check_launch("polynorm");
+}
+
+}  // namespace motif
+
+using namespace motif;
+
+extern "C" int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
+                              int dtype, int64_t rows, int D, float eps, void* stream) {
+  clear_error();
+  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
+                "polynorm: unknown dtype code %d", dtype);
+  MOTIF_REQUIRE(rows >= 0 && D >= 0, "polynorm: negative extent");
+  if (rows == 0 || D == 0) return MOTIF_OK;
+  MOTIF_REQUIRE(x && weight && bias && y, "polynorm: null pointer");
+  PolyArgs a{x, weight, bias, y, (long)rows, D, eps};
+  const bool vec_ok = (((uintptr_t)x | (uintptr_t)y) & 15u) == 0;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case MOTIF_F16: return launch_poly<half_t>(a, vec_ok, st);
+    case MOTIF_BF16: return launch_poly<bf16_t>(a, vec_ok, st);
+    default: return launch_poly<float>(a, vec_ok, st);
+  }
+}

@@ -1,0 +1,26 @@
+// Per-format dispatch of the split-KV attention kernel.  Each dispatch
+// function is defined in its own translation unit (one per element type) so
+// the variants compile in parallel.
+#pragma once
+
+#include "motif_common.hpp"
+#include "sdpa_plan.hpp"
+
+namespace motif {
+
+// fp16 / bf16 / fp32 cache.  Returns MOTIF_ERR_UNSUPPORTED for a head dim
+// with no compiled variant.
+int dispatch_sdpa_fp_f16(const SdpaArgs& a, const SdpaPlan& p, int D, hipStream_t s);
+int dispatch_sdpa_fp_bf16(const SdpaArgs& a, const SdpaPlan& p, int D, hipStream_t s);
+int dispatch_sdpa_fp_f32(const SdpaArgs& a, const SdpaPlan& p, int D, hipStream_t s);
+
+// Packed q4 / q8 cache with scales/biases of the given element type.
+int dispatch_sdpa_q_f16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
+int dispatch_sdpa_q_bf16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
+int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
+
+// Pointer alignment (bytes) the kernels need for head dim D.
+int sdpa_fp_align(int dtype, int D);
+int sdpa_q_align(int D, int bits);
+
+}  // namespace motif

@@ -1,0 +1,187 @@
+// extern "C" entry points of the dual-V attention path: contract checks,
+// launch plan, workspace carving, dispatch by element type.
+#include "sdpa_dispatch.hpp"
+
+namespace motif {
+
+int sdpa_fp_align(int dtype, int D) {
+  const int bytes = dtype == MOTIF_F32 ? 4 : 2;
+  const int lane_bytes = (D / 16) * bytes;
+  return lane_bytes % 16 == 0 ? 16 : lane_bytes % 8 == 0 ? 8 : 4;
+}
+
+int sdpa_q_align(int D, int bits) {
+  const int el = 32 / bits;
+  const int cpl = (D / 16 > el) ? D / 16 : el;
+  const int wpl = cpl / el;
+  return wpl % 4 == 0 ? 16 : wpl % 2 == 0 ? 8 : 4;
+}
+
+static bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
+
+// Shared shape checks (the reference asserts of attention.py:237-243, 556-564)
+// and plan/workspace set-up.
+static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, int B, int Hq,
+                       int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal, float scale,
+                       void* ws, size_t ws_bytes) {
+  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
+                "%s: unknown dtype code %d", name, dtype);
+  MOTIF_REQUIRE(B >= 1 && Hq >= 1 && Hkv >= 1 && S_q >= 1, "%s: B, H_q, H_kv, S_q must be >= 1",
+                name);
+  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
+  MOTIF_REQUIRE(Hq % Hkv == 0, "%s: H_q=%d must be a multiple of H_kv=%d", name, Hq, Hkv);
+  MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
+                "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
+  MOTIF_REQUIRE((long)B * Hkv * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
+  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D));
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.S_q = S_q;
+  a.G = Hq / Hkv;
+  a.GV = a.G * S_q;
+  a.nchunk = p.nchunk;
+  a.kv_cap = kv_cap;
+  a.kv_len = kv_len;
+  a.causal = causal ? 1 : 0;
+  a.nsplit = p.nsplit;
+  a.rows_per_split = p.rows_per_split;
+  a.qscale = scale * 1.4426950408889634f;  // log2(e): the kernels use exp2
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  a.counters = nullptr;
+  if (p.nsplit > 1) {
+    if (ws == nullptr || ws_bytes < p.workspace_bytes) {
+      set_error("%s: workspace of %zu bytes needed, %zu given", name, p.workspace_bytes,
+                ws == nullptr ? (size_t)0 : ws_bytes);
+      return MOTIF_ERR_WORKSPACE;
+    }
+    MOTIF_REQUIRE(aligned(ws, 256), "%s: workspace must be 256-byte aligned", name);
+    char* w = (char*)ws;
+    a.counters = (unsigned*)w;
+    const size_t vrows = (size_t)B * Hq * S_q;
+    const size_t o_bytes = (vrows * p.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
+    a.part_o = (float*)(w + p.counter_bytes);
+    a.part_ml = (float*)(w + p.counter_bytes + o_bytes);
+  }
+  return MOTIF_OK;
+}
+
+static int sdpa_fp_run(const char* name, const void* q, const void* k, const void* v1,
+                       const void* v2, void* y, int dtype, int B, int Hq, int Hkv, int S_q, int D,
+                       int kv_cap, int kv_len, int causal, float scale, void* ws,
+                       size_t ws_bytes, void* stream) {
+  clear_error();
+  SdpaArgs a{};
+  SdpaPlan p{};
+  int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
+                       ws_bytes);
+  if (rc != MOTIF_OK) return rc;
+  MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
+  const int al = sdpa_fp_align(dtype, D);
+  MOTIF_REQUIRE(aligned(k, al) && aligned(v1, al) && aligned(v2, al),
+                "%s: k/v1/v2 must be %d-byte aligned", name, al);
+  a.q = q;
+  a.k = k;
+  a.v1 = v1;
+  a.v2 = v2;
+  a.y = y;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MOTIF_F16: return dispatch_sdpa_fp_f16(a, p, D, s);
+    case MOTIF_BF16: return dispatch_sdpa_fp_bf16(a, p, D, s);
+    default: return dispatch_sdpa_fp_f32(a, p, D, s);
+  }
+}
+
+static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const void* ks,
+                      const void* kb, const uint32_t* v1d, const void* v1s, const void* v1b,
+                      const uint32_t* v2d, const void* v2s, const void* v2b, void* y, int dtype,
+                      int B, int Hq, int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal,
+                      int bits, int gs, float scale, void* ws, size_t ws_bytes, void* stream) {
+  clear_error();
+  // Packed-layout contract, attention.py:556-608.
+  MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
+  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
+  MOTIF_REQUIRE(gs > 0 && D % gs == 0, "%s: D=%d must be a multiple of group_size=%d", name, D,
+                gs);
+  MOTIF_REQUIRE((32 / bits) % (D / 32) == 0,
+                "%s requires qk_per_thread | EL_PER_INT so each lane's D/32 channels come from "
+                "ONE packed uint32 (implies D/32 <= 32/bits); got D=%d, bits=%d",
+                name, D, bits);
+  MOTIF_REQUIRE(gs % (D / 32) == 0,
+                "%s requires qk_per_thread | group_size; got D=%d, group_size=%d", name, D, gs);
+  MOTIF_REQUIRE(gs == 32 || gs == 64 || gs == 128, "%s: group_size=%d must be 32, 64 or 128",
+                name, gs);
+  SdpaArgs a{};
+  SdpaPlan p{};
+  int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
+                       ws_bytes);
+  if (rc != MOTIF_OK) return rc;
+  MOTIF_REQUIRE(q && y && (kv_cap == 0 || (kd && ks && kb && v1d && v1s && v1b && v2d && v2s &&
+                                           v2b)),
+                "%s: null tensor pointer", name);
+  const int al = sdpa_q_align(D, bits);
+  MOTIF_REQUIRE(aligned(kd, al) && aligned(v1d, al) && aligned(v2d, al),
+                "%s: packed data must be %d-byte aligned", name, al);
+  a.q = q;
+  a.kd = kd; a.ks = ks; a.kb = kb;
+  a.v1d = v1d; a.v1s = v1s; a.v1b = v1b;
+  a.v2d = v2d; a.v2s = v2s; a.v2b = v2b;
+  a.y = y;
+  a.group_size = gs;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MOTIF_F16: return dispatch_sdpa_q_f16(a, p, D, bits, s);
+    case MOTIF_BF16: return dispatch_sdpa_q_bf16(a, p, D, bits, s);
+    default: return dispatch_sdpa_q_f32(a, p, D, bits, s);
+  }
+}
+
+}  // namespace motif
+
+using namespace motif;
+
+extern "C" {
+
+int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
+                      int dtype, int B, int Hq, int Hkv, int D, int kv_cap, int kv_len,
+                      float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  return sdpa_fp_run("sdpa_dual_v", q, k, v1, v2, y, dtype, B, Hq, Hkv, 1, D, kv_cap, kv_len, 0,
+                     scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_rows(const void* q, const void* k, const void* v1, const void* v2, void* y,
+                           int dtype, int B, int Hq, int Hkv, int S_q, int D, int kv_cap,
+                           int kv_len, int causal, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return sdpa_fp_run("sdpa_dual_v_rows", q, k, v1, v2, y, dtype, B, Hq, Hkv, S_q, D, kv_cap,
+                     kv_len, causal, scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_q(const void* q, const uint32_t* k_data, const void* k_scales,
+                        const void* k_biases, const uint32_t* v1_data, const void* v1_scales,
+                        const void* v1_biases, const uint32_t* v2_data, const void* v2_scales,
+                        const void* v2_biases, void* y, int dtype, int B, int Hq, int Hkv, int D,
+                        int kv_cap, int kv_len, int bits, int group_size, float scale,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  return sdpa_q_run("sdpa_dual_v_q4", q, k_data, k_scales, k_biases, v1_data, v1_scales,
+                    v1_biases, v2_data, v2_scales, v2_biases, y, dtype, B, Hq, Hkv, 1, D, kv_cap,
+                    kv_len, 0, bits, group_size, scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_q_rows(const void* q, const uint32_t* k_data, const void* k_scales,
+                             const void* k_biases, const uint32_t* v1_data,
+                             const void* v1_scales, const void* v1_biases,
+                             const uint32_t* v2_data, const void* v2_scales,
+                             const void* v2_biases, void* y, int dtype, int B, int Hq, int Hkv,
+                             int S_q, int D, int kv_cap, int kv_len, int causal, int bits,
+                             int group_size, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return sdpa_q_run("sdpa_dual_v_q_rows", q, k_data, k_scales, k_biases, v1_data, v1_scales,
+                    v1_biases, v2_data, v2_scales, v2_biases, y, dtype, B, Hq, Hkv, S_q, D,
+                    kv_cap, kv_len, causal, bits, group_size, scale, workspace, workspace_bytes,
+                    stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Instantiation bodies for one element type; included by sdpa_{f16,bf16,f32}.hip
+// with MOTIF_ELEM and MOTIF_SUFFIX defined.
+#include "sdpa_dispatch.hpp"
+#include "sdpa_impl.hpp"
+
+namespace motif {
+
+#define MOTIF_CAT2(a, b) a##b
+#define MOTIF_CAT(a, b) MOTIF_CAT2(a, b)
+
+int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
+                                              hipStream_t s) {
+  const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  switch (D) {
+    case 32: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 32>>(a, p.gc, p.waves, nblocks, s);
+    case 64: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 64>>(a, p.gc, p.waves, nblocks, s);
+    case 96: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 96>>(a, p.gc, p.waves, nblocks, s);
+    case 128: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 128>>(a, p.gc, p.waves, nblocks, s);
+    case 160: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 160>>(a, p.gc, p.waves, nblocks, s);
+    case 192: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 192>>(a, p.gc, p.waves, nblocks, s);
+    case 224: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 224>>(a, p.gc, p.waves, nblocks, s);
+    case 256: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 256>>(a, p.gc, p.waves, nblocks, s);
+    default: break;
+  }
+  set_error("sdpa_dual_v: head dim D=%d has no compiled variant (supported: 32..256 step 32)", D);
+  return MOTIF_ERR_UNSUPPORTED;
+}
+
+int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
+                                             int bits, hipStream_t s) {
+  const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  if (bits == 4) {
+    switch (D) {
+      case 32: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 32, 4>>(a, p.gc, p.waves, nblocks, s);
+      case 64: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 64, 4>>(a, p.gc, p.waves, nblocks, s);
+      case 128: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 128, 4>>(a, p.gc, p.waves, nblocks, s);
+      case 256: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 256, 4>>(a, p.gc, p.waves, nblocks, s);
+      default: break;
+    }
+  } else if (bits == 8) {
+    switch (D) {
+      case 32: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 32, 8>>(a, p.gc, p.waves, nblocks, s);
+      case 64: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 64, 8>>(a, p.gc, p.waves, nblocks, s);
+      case 128: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 128, 8>>(a, p.gc, p.waves, nblocks, s);
+      default: break;
+    }
+  }
+  set_error("sdpa_dual_v_q: no compiled variant for D=%d bits=%d", D, bits);
+  return MOTIF_ERR_UNSUPPORTED;
+}
+
+}  // namespace motif

@@ -1,0 +1,58 @@
+// Host-side launch plan of the split-KV dual-V attention kernels: how the
+// query heads of one KV head are chunked, how the live KV rows are split
+// across workgroups, and where counters and partials sit in the workspace.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace motif {
+
+// Everything a split-KV launch needs, shared by every cache format.
+struct SdpaArgs {
+  const void* q;  // (B, Hq, S_q, D)
+  // fp16/bf16/fp32 cache (B, Hkv, kv_cap, D)
+  const void* k;
+  const void* v1;
+  const void* v2;
+  // packed cache: data u32 (B,Hkv,kv_cap,D*bits/32), scales/biases (B,Hkv,kv_cap,D/gs)
+  const uint32_t* kd;
+  const void* ks;
+  const void* kb;
+  const uint32_t* v1d;
+  const void* v1s;
+  const void* v1b;
+  const uint32_t* v2d;
+  const void* v2s;
+  const void* v2b;
+  void* y;             // (B, Hq, S_q, 2D)
+  float* part_o;       // [B*Hq*S_q][nsplit][2D]
+  float* part_ml;      // [B*Hq*S_q][nsplit][2]  (running max in log2 units, sum)
+  unsigned* counters;  // [B*Hkv*nchunk] arrival counters, zero between calls
+  int B, Hq, Hkv, S_q;
+  int G;       // Hq / Hkv
+  int GV;      // virtual heads per KV head = G * S_q (one per (head, query row))
+  int nchunk;  // ceil(GV / GC): workgroups per KV head and split
+  int kv_cap, kv_len, causal;
+  int nsplit, rows_per_split;
+  int group_size;
+  float qscale;  // softmax scale * log2(e)
+};
+
+struct SdpaPlan {
+  int gc;              // virtual heads per workgroup (1, 2, 4 or 8)
+  int nchunk;
+  int nsplit;
+  int rows_per_split;
+  int waves;           // waves per workgroup
+  size_t counter_bytes;
+  size_t workspace_bytes;
+};
+
+// gc_max: the largest per-workgroup head count compiled for this head dim.
+SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max);
+
+// Largest head chunk compiled for head dim D (register budget).
+inline int sdpa_gc_max(int D) { return D <= 128 ? 8 : 4; }
+
+}  // namespace motif

@@ -1,0 +1,52 @@
+"""HIP kernels of the Motif decode-attention hot path (gfx950).
+
+Mirror of ``src/mlx_motif/kernels/__init__.py``: the same public names with
+the same signatures, each backed by ``libmotif_hip`` and paired with a
+``*_reference`` in torch ops.  ``MLX_MOTIF_DISABLE_KERNELS=1`` (read once at
+import) routes every wrapper to its reference.
+
+    attention.py — sdpa_dual_v, sdpa_dual_v_q4 (+ multi-row *_rows variants)
+    gda.py       — gda_post, gda_post_split
+    mlp.py       — polynorm, _dequant_probe (test helper)
+    quant.py     — quantize / dequantize (MLX affine format of the KV cache)
+"""
+
+from .attention import (
+    sdpa_dual_v,
+    sdpa_dual_v_q4,
+    sdpa_dual_v_q4_reference,
+    sdpa_dual_v_q4_rows,
+    sdpa_dual_v_reference,
+    sdpa_dual_v_rows,
+)
+from .gda import (
+    gda_post,
+    gda_post_reference,
+    gda_post_split,
+    gda_post_split_reference,
+)
+from .mlp import (
+    _dequant_probe,  # noqa: F401  — test helper, deliberately not in __all__
+    polynorm,
+    polynorm_reference,
+)
+from .quant import dequantize, dequantize_reference, quantize, quantize_reference
+
+__all__ = [
+    "polynorm",
+    "polynorm_reference",
+    "gda_post",
+    "gda_post_reference",
+    "gda_post_split",
+    "gda_post_split_reference",
+    "sdpa_dual_v",
+    "sdpa_dual_v_reference",
+    "sdpa_dual_v_q4",
+    "sdpa_dual_v_q4_reference",
+    "sdpa_dual_v_rows",
+    "sdpa_dual_v_q4_rows",
+    "quantize",
+    "quantize_reference",
+    "dequantize",
+    "dequantize_reference",
+]

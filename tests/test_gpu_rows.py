@@ -1,0 +1,82 @@
+"""Parity of the multi-row dual-V path (speculative verify / chunked prefill):
+``motif_sdpa_dual_v_rows`` and ``motif_sdpa_dual_v_q_rows`` against the
+oracle's bottom-right causal attention (the FALLBACK composition of
+model.py:769-807 with mask "causal").
+
+Includes the verify slab of the 12.7B layer: K+1 = 5 query rows per head, 32
+q-heads over 8 KV heads, head_dim 128, over a q8 cache of 32768 rows.
+Tolerance: fp16 max |gpu - oracle| <= 2e-3.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import np_to_torch, randn, torch_dtype, torch_to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,cap,kv_len,d,causal", [
+    (1, 32, 8, 5, 512, 300, 128, True),
+    (1, 32, 8, 5, 512, 5, 128, True),
+    (2, 8, 8, 3, 256, 200, 64, True),
+    (1, 40, 8, 4, 1024, 1000, 128, False),
+    (1, 16, 4, 7, 256, 256, 128, True),
+])
+def test_rows_fp16(gpu, rng, B, Hq, Hkv, S, cap, kv_len, d, causal):
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    q = randn(rng, (B, Hq, S, d), "f16")
+    k, v1, v2 = (randn(rng, (B, Hkv, cap, d), "f16") for _ in range(3))
+    for t in (k, v1, v2):
+        t[:, :, kv_len:] = 1e4
+    T = lambda a: np_to_torch(a, torch_dtype("f16"), gpu)  # noqa: E731
+    y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(d), kv_len=kv_len, causal=causal)
+    assert y.shape == (B, Hq, S, 2 * d)
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(d), kv_len, causal=causal)
+    assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
+
+
+def test_rows_single_row_equals_decode(gpu, rng):
+    """S_q = 1 with the causal mask is the decode kernel's computation."""
+    from mlx_motif.kernels import sdpa_dual_v, sdpa_dual_v_rows
+
+    q = randn(rng, (1, 32, 1, 128), "f16")
+    k, v1, v2 = (randn(rng, (1, 8, 700, 128), "f16") for _ in range(3))
+    T = lambda a: np_to_torch(a, torch_dtype("f16"), gpu)  # noqa: E731
+    a = torch_to_np(sdpa_dual_v(T(q), T(k), T(v1), T(v2), 0.088, kv_len=650))
+    b = torch_to_np(sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 0.088, kv_len=650, causal=True))
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("S,cap,kv_len", [(5, 512, 400), (3, 256, 3)])
+def test_rows_packed(gpu, rng, bits, S, cap, kv_len):
+    from mlx_motif.kernels import sdpa_dual_v_q4_rows
+
+    q = randn(rng, (1, 32, S, 128), "f16")
+    trips = [O.quantize(randn(rng, (1, 8, cap, 128), "f16"), 64, bits) for _ in range(3)]
+    G = lambda t: (np_to_torch(t[0], None, gpu), np_to_torch(t[1], torch_dtype("f16"), gpu),  # noqa: E731
+                   np_to_torch(t[2], torch_dtype("f16"), gpu))
+    y = sdpa_dual_v_q4_rows(np_to_torch(q, torch_dtype("f16"), gpu), *(G(t) for t in trips),
+                            1 / np.sqrt(128), group_size=64, bits=bits, kv_len=kv_len)
+    ref = O.sdpa_dual_v_q(q, *trips, 1 / np.sqrt(128), 64, bits, kv_len, causal=True)
+    assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
+
+
+def test_verify_slab_q8_32k(gpu, rng):
+    """5 query rows, q8 cache of 32768 rows (all live, the 5 new rows included)."""
+    from mlx_motif.kernels import sdpa_dual_v_q4_rows
+
+    S, cap = 5, 32768
+    q = randn(rng, (1, 32, S, 128), "f16")
+    trips = [O.quantize(randn(rng, (1, 8, cap, 128), "f16"), 64, 8) for _ in range(3)]
+    G = lambda t: (np_to_torch(t[0], None, gpu), np_to_torch(t[1], torch_dtype("f16"), gpu),  # noqa: E731
+                   np_to_torch(t[2], torch_dtype("f16"), gpu))
+    y = sdpa_dual_v_q4_rows(np_to_torch(q, torch_dtype("f16"), gpu), *(G(t) for t in trips),
+                            1 / np.sqrt(128), group_size=64, bits=8, kv_len=cap)
+    ref = O.sdpa_dual_v_q(q, *trips, 1 / np.sqrt(128), 64, 8, cap, causal=True)
+    assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3

@@ -1,0 +1,182 @@
+"""Parity of the split-KV dual-V attention kernel (fp16/bf16/fp32 cache)
+against the oracle, through the C ABI (``motif_sdpa_dual_v``).
+
+Shapes follow the reference's tests/test_kernels_sdpa_dual_v.py (MHA, GQA,
+runtime kv_len over poisoned padding, growing kv_len), plus head dims
+32..256, kv_len = 0, forced multi-split merges and the full-size workloads:
+32 q-heads over 8 KV heads, head_dim 128, KV 3204 (cap 3328) and 16000
+(cap 16128).  Tolerances (max |gpu - oracle|): fp16 2e-3 (fp32 accumulation),
+bf16 1e-2 (output rounding alone is up to 3.9e-3 at |y| ~ 1), fp32 1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import np_to_torch, randn, torch_dtype, torch_to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f16": 2e-3, "bf16": 1e-2, "f32": 1e-5}
+
+
+def _run(gpu, rng, B, Hq, Hkv, cap, kv_len, D, tag, *, poison=False, qs=1.0, ks=1.0, vs=1.0):
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v
+
+    q = randn(rng, (B, Hq, 1, D), tag, qs)
+    k = randn(rng, (B, Hkv, cap, D), tag, ks)
+    v1 = randn(rng, (B, Hkv, cap, D), tag, vs)
+    v2 = randn(rng, (B, Hkv, cap, D), tag, vs)
+    if poison and kv_len < cap:
+        for t in (k, v1, v2):
+            t[:, :, kv_len:] = 1e4
+    dt = torch_dtype(tag)
+    tq, tk, tv1, tv2 = (np_to_torch(a, dt, gpu) for a in (q, k, v1, v2))
+    scale = 1.0 / np.sqrt(D)
+    y = sdpa_dual_v(tq, tk, tv1, tv2, scale, kv_len=kv_len)
+    torch.cuda.synchronize()
+    assert y.shape == (B, Hq, 1, 2 * D) and y.dtype == dt
+    ref = O.sdpa_dual_v(q, k, v1, v2, scale, kv_len)
+    err = float(np.max(np.abs(torch_to_np(y) - ref))) if ref.size else 0.0
+    return err, y, ref
+
+
+@pytest.mark.parametrize("B,H,KV,d", [
+    (1, 8, 1, 128), (1, 8, 16, 128), (1, 40, 64, 128), (1, 40, 256, 128), (1, 8, 17, 128),
+    (2, 16, 64, 64),
+])
+@pytest.mark.parametrize("tag", ["f16", "bf16", "f32"])
+def test_mha_matches_oracle(gpu, rng, B, H, KV, d, tag):
+    err, _, _ = _run(gpu, rng, B, H, H, KV, KV, d, tag, qs=0.1, ks=0.1, vs=0.5)
+    assert err <= TOL[tag], f"B={B} H={H} KV={KV} d={d} {tag}: max err {err:.3e}"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,KV,d", [
+    (1, 32, 8, 64, 128), (1, 16, 8, 32, 128), (1, 32, 4, 100, 128), (2, 32, 8, 17, 128),
+    (1, 40, 8, 300, 128),
+])
+@pytest.mark.parametrize("tag", ["f16", "bf16", "f32"])
+def test_gqa_matches_oracle(gpu, rng, B, Hq, Hkv, KV, d, tag):
+    err, _, _ = _run(gpu, rng, B, Hq, Hkv, KV, KV, d, tag)
+    assert err <= TOL[tag], f"GQA {Hq}/{Hkv} KV={KV} {tag}: max err {err:.3e}"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,cap,kv_len,d", [
+    (1, 8, 8, 256, 1, 128), (1, 8, 8, 256, 17, 128), (1, 32, 8, 256, 100, 128),
+    (1, 40, 8, 512, 385, 128), (2, 16, 8, 256, 200, 64),
+])
+@pytest.mark.parametrize("tag", ["f16", "bf16"])
+def test_runtime_kv_len_ignores_poisoned_padding(gpu, rng, B, Hq, Hkv, cap, kv_len, d, tag):
+    err, y, _ = _run(gpu, rng, B, Hq, Hkv, cap, kv_len, d, tag, poison=True)
+    assert np.isfinite(torch_to_np(y)).all()
+    assert err <= TOL[tag], f"cap={cap} kv_len={kv_len}: max err {err:.3e}"
+
+
+def test_growing_kv_len_one_buffer(gpu, rng):
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v
+
+    B, Hq, Hkv, cap, d = 1, 32, 8, 256, 128
+    q = randn(rng, (B, Hq, 1, d), "f16")
+    k, v1, v2 = (randn(rng, (B, Hkv, cap, d), "f16") for _ in range(3))
+    tq, tk, tv1, tv2 = (np_to_torch(a, torch.float16, gpu) for a in (q, k, v1, v2))
+    for kv_len in (1, 2, 31, 32, 33, 100, 255, 256):
+        y = sdpa_dual_v(tq, tk, tv1, tv2, 1 / np.sqrt(d), kv_len=kv_len)
+        err = np.max(np.abs(torch_to_np(y) - O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(d), kv_len)))
+        assert err <= 2e-3, f"kv_len={kv_len}: {err:.3e}"
+
+
+@pytest.mark.parametrize("d", [32, 96, 160, 192, 224, 256])
+def test_head_dims(gpu, rng, d):
+    err, _, _ = _run(gpu, rng, 1, 8, 2, 300, 300, d, "f16")
+    assert err <= 2e-3, f"d={d}: {err:.3e}"
+
+
+def test_kv_len_zero_gives_zeros(gpu, rng):
+    err, y, _ = _run(gpu, rng, 1, 8, 8, 256, 0, 128, "f16")
+    assert float(torch_to_np(y).max()) == 0.0 and float(torch_to_np(y).min()) == 0.0
+
+
+def test_v1_equals_v2_gives_identical_halves(gpu, rng):
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v
+
+    q = randn(rng, (1, 32, 1, 128), "f16")
+    k, v = (randn(rng, (1, 8, 2000, 128), "f16") for _ in range(2))
+    tq, tk, tv = (np_to_torch(a, torch.float16, gpu) for a in (q, k, v))
+    y = torch_to_np(sdpa_dual_v(tq, tk, tv, tv, 1 / np.sqrt(128)))
+    assert np.array_equal(y[..., :128], y[..., 128:])
+
+
+@pytest.mark.parametrize("rows_per_split", [16, 64, 208])
+def test_forced_split_merges(gpu, rng, rows_per_split):
+    """Many splits per KV head exercise the last-arriving-workgroup merge."""
+    from mlx_motif import _native
+
+    _native.set_tuning("rows_per_split", rows_per_split)
+    try:
+        err, _, _ = _run(gpu, rng, 2, 32, 8, 3328, 3204, 128, "f16")
+        err2, _, _ = _run(gpu, rng, 1, 8, 8, 1024, 1000, 64, "bf16")
+    finally:
+        _native.set_tuning("rows_per_split", 0)
+    assert err <= 2e-3 and err2 <= 1e-2, (err, err2)
+
+
+def test_repeated_calls_rearm_counters(gpu, rng):
+    """Back-to-back multi-split calls on one workspace stay correct (the last
+    workgroup of each call re-arms the arrival counters)."""
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v
+
+    q = randn(rng, (1, 32, 1, 128), "f16")
+    k, v1, v2 = (randn(rng, (1, 8, 4096, 128), "f16") for _ in range(3))
+    tq, tk, tv1, tv2 = (np_to_torch(a, torch.float16, gpu) for a in (q, k, v1, v2))
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128))
+    outs = [sdpa_dual_v(tq, tk, tv1, tv2, 1 / np.sqrt(128)) for _ in range(20)]
+    for y in outs:
+        assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
+    assert all(torch.equal(outs[0], y) for y in outs[1:])
+
+
+@pytest.mark.parametrize("kv_len,cap", [(3204, 3328), (16000, 16128)])
+def test_full_size_12p7b_layer(gpu, rng, kv_len, cap):
+    """32 q-heads over 8 KV heads, head_dim 128, fp16 N(0,1) inputs."""
+    err, _, _ = _run(gpu, rng, 1, 32, 8, cap, kv_len, 128, "f16")
+    assert err <= 2e-3, f"kv_len={kv_len}: {err:.3e}"
+
+
+def test_gda_decode_step_cfg1(gpu, rng):
+    """One GDA decode step: 8 signal + 8 noise q-heads over 4 KV heads
+    (GQA 2 each), head_dim 128, fp16 KV 1024, then gda_post_split (gr = 1)."""
+    import torch
+
+    from mlx_motif.kernels import gda_post_split, sdpa_dual_v
+
+    D, kv = 128, 1024
+    q1 = randn(rng, (1, 8, 1, D), "f16")
+    q2 = randn(rng, (1, 8, 1, D), "f16")
+    k1, k2, v1, v2 = (randn(rng, (1, 4, kv, D), "f16") for _ in range(4))
+    lam = np.float32(rng.uniform(0.1, 0.9))
+    lam_init = float(rng.uniform(0.1, 0.9))
+    w = O.round_to(rng.uniform(0.5, 1.5, 2 * D), "f16")
+    T = lambda a: np_to_torch(a, torch.float16, gpu)  # noqa: E731
+    a_o = sdpa_dual_v(T(q1), T(k1), T(v1), T(v2), 1 / np.sqrt(D))
+    a_n = sdpa_dual_v(T(q2), T(k2), T(v1), T(v2), 1 / np.sqrt(D))
+    y = gda_post_split(a_o, a_n, T(w), torch.tensor([lam], device=gpu), lam_init, 1, 1e-6)
+    r_o = O.round_to(O.sdpa_dual_v(q1, k1, v1, v2, 1 / np.sqrt(D)), "f16")
+    r_n = O.round_to(O.sdpa_dual_v(q2, k2, v1, v2, 1 / np.sqrt(D)), "f16")
+    assert np.max(np.abs(torch_to_np(a_o) - r_o)) <= 2e-3
+    assert np.max(np.abs(torch_to_np(a_n) - r_n)) <= 2e-3
+    # the epilogue is checked on the GPU's own attention outputs (fp16-rounded
+    # once); its outputs reach |y| ~ 3-4 where the fp16 ulp is 2e-3 to 3.9e-3
+    ref = O.gda_post_split(torch_to_np(a_o), torch_to_np(a_n), w, lam, lam_init, 1, 1e-6)
+    assert y.shape == (1, 8, 1, 2 * D)
+    err = np.abs(torch_to_np(y) - ref)
+    assert np.max(err / np.maximum(1.0, np.abs(ref))) <= 2e-3

@@ -1,0 +1,138 @@
+"""Parity of dual-V attention reading the packed q4/q8 cache
+(``motif_sdpa_dual_v_q`` via ``sdpa_dual_v_q4``) against the oracle.
+
+Shapes follow the reference's tests/test_kernels_sdpa_dual_v_q4.py (sizes,
+GQA 1..5, poisoned padding, growing kv_len, V1=V2 halves, group sizes
+32/64/128 at D=128) plus the 16k workloads (32 q-heads over 8 KV heads, cap
+16128).  The cache is quantised by the oracle so this file tests attention
+alone; tests/test_gpu_quant.py checks the quantizer bit for bit.
+Tolerance: fp16 max |gpu - oracle| <= 2e-3 against the oracle with exact
+(fp32-style, unrounded) dequantised values; bf16 1e-2.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import np_to_torch, randn, torch_dtype, torch_to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f16": 2e-3, "bf16": 1e-2}
+
+
+def _quant(x, gs, bits, tag):
+    return O.quantize(x, gs, bits, out_dtype=tag)
+
+
+def _to_gpu(trip, tag, gpu):
+    d, s, b = trip
+    dt = torch_dtype(tag)
+    return (np_to_torch(d, None, gpu), np_to_torch(s, dt, gpu), np_to_torch(b, dt, gpu))
+
+
+def _run(gpu, rng, B, Hq, Hkv, cap, kv_len, D, bits, gs, tag, *, poison=False, v_same=False):
+    from mlx_motif.kernels import sdpa_dual_v_q4
+
+    q = randn(rng, (B, Hq, 1, D), tag)
+    k = randn(rng, (B, Hkv, cap, D), tag)
+    v1 = randn(rng, (B, Hkv, cap, D), tag)
+    v2 = v1 if v_same else randn(rng, (B, Hkv, cap, D), tag)
+    if poison and kv_len < cap:
+        for t in {id(k): k, id(v1): v1, id(v2): v2}.values():
+            t[:, :, kv_len:] = 1e3
+    kq, v1q, v2q = (_quant(t, gs, bits, tag) for t in (k, v1, v2))
+    scale = 1.0 / np.sqrt(D)
+    y = sdpa_dual_v_q4(np_to_torch(q, torch_dtype(tag), gpu), _to_gpu(kq, tag, gpu),
+                       _to_gpu(v1q, tag, gpu), _to_gpu(v2q, tag, gpu), scale,
+                       group_size=gs, bits=bits, kv_len=kv_len)
+    assert y.shape == (B, Hq, 1, 2 * D) and y.dtype == torch_dtype(tag)
+    ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, scale, gs, bits, kv_len)
+    return float(np.max(np.abs(torch_to_np(y) - ref))), y, ref
+
+
+_SHAPES = [
+    (1, 4, 4, 16, 128), (1, 4, 4, 128, 128), (1, 4, 4, 300, 128), (1, 4, 4, 1024, 128),
+    (2, 4, 4, 64, 128), (1, 8, 4, 64, 128), (1, 16, 4, 64, 128), (1, 40, 8, 256, 128),
+    (1, 40, 8, 1024, 128),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,KV,d", _SHAPES)
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("tag", ["f16", "bf16"])
+def test_matches_oracle(gpu, rng, B, Hq, Hkv, KV, d, bits, tag):
+    err, _, _ = _run(gpu, rng, B, Hq, Hkv, KV, KV, d, bits, 64, tag)
+    assert err <= TOL[tag], f"{(B, Hq, Hkv, KV, d)} bits={bits} {tag}: {err:.3e}"
+
+
+def test_dequant_rounding_point_is_inside_tolerance(gpu, rng):
+    """The reference's reference path rounds dequantised values to fp16
+    (mx.dequantize) before attention; the kernel keeps them in fp32.  Both
+    stay within tolerance of each other."""
+    err, y, _ = _run(gpu, rng, 1, 32, 8, 2048, 2048, 128, 4, 64, "f16")
+    assert err <= 2e-3
+
+
+def test_v1_equals_v2_halves_identical_and_distinct_differ(gpu, rng):
+    _, y, _ = _run(gpu, rng, 1, 4, 4, 64, 64, 128, 4, 64, "f16", v_same=True)
+    y = torch_to_np(y)
+    assert np.array_equal(y[..., :128], y[..., 128:])
+    _, y2, _ = _run(gpu, rng, 1, 4, 4, 64, 64, 128, 4, 64, "f16")
+    y2 = torch_to_np(y2)
+    assert not np.allclose(y2[..., :128], y2[..., 128:], atol=1e-3)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,cap,kv_len,d", [
+    (1, 8, 8, 256, 1, 128), (1, 8, 8, 256, 100, 128), (1, 32, 8, 256, 100, 128),
+    (1, 40, 8, 512, 385, 128),
+])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("tag", ["f16", "bf16"])
+def test_runtime_kv_len_poisoned(gpu, rng, B, Hq, Hkv, cap, kv_len, d, bits, tag):
+    err, y, _ = _run(gpu, rng, B, Hq, Hkv, cap, kv_len, d, bits, 64, tag, poison=True)
+    assert np.isfinite(torch_to_np(y)).all()
+    assert err <= TOL[tag], f"cap={cap} kv_len={kv_len} bits={bits}: {err:.3e}"
+
+
+def test_growing_kv_len(gpu, rng):
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v_q4
+
+    B, Hq, Hkv, cap, d, gs, bits = 1, 32, 8, 256, 128, 64, 4
+    q = randn(rng, (B, Hq, 1, d), "f16")
+    full = randn(rng, (B, Hkv, cap, d), "f16")
+    kq = _quant(full, gs, bits, "f16")
+    v1q = _quant(O.round_to(full.astype(np.float32) * 0.5, "f16"), gs, bits, "f16")
+    v2q = _quant(O.round_to(full.astype(np.float32) * -0.25, "f16"), gs, bits, "f16")
+    tq = np_to_torch(q, torch.float16, gpu)
+    gk, g1, g2 = (_to_gpu(t, "f16", gpu) for t in (kq, v1q, v2q))
+    for kv_len in (1, 31, 32, 33, 100, 255, 256):
+        y = sdpa_dual_v_q4(tq, gk, g1, g2, 1 / np.sqrt(d), group_size=gs, bits=bits,
+                           kv_len=kv_len)
+        ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, 1 / np.sqrt(d), gs, bits, kv_len)
+        assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3, kv_len
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_group_sizes_at_d128(gpu, rng, gs, bits):
+    err, _, _ = _run(gpu, rng, 1, 4, 4, 64, 64, 128, bits, gs, "f16")
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("d,bits", [(32, 4), (64, 4), (256, 4), (32, 8), (64, 8)])
+def test_other_head_dims(gpu, rng, d, bits):
+    gs = 32 if d == 32 else 64
+    err, _, _ = _run(gpu, rng, 1, 8, 2, 300, 300, d, bits, gs, "f16")
+    assert err <= 2e-3, f"d={d} bits={bits}: {err:.3e}"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_full_size_16k(gpu, rng, bits):
+    """32 q-heads over 8 KV heads, head_dim 128, gs 64, kv_len 16000, cap 16128."""
+    err, _, _ = _run(gpu, rng, 1, 32, 8, 16128, 16000, 128, bits, 64, "f16")
+    assert err <= 2e-3, f"bits={bits}: {err:.3e}"
