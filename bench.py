@@ -1,0 +1,341 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X.
+
+Metric: decode-attn µs/call and achieved HBM GB/s (% of peak) at KV = 16k for
+the fp16 4-slot cache (the headline ``value``) and the packed q4 / q8 caches.
+
+Workload (one "step" = one call of the hot path over one layer's cache):
+  shared-QK dual-V decode, batch 1, 32 query heads over 8 KV heads,
+  head_dim 128, kv_len 16000 live rows of a 16128-row cache, scale 1/sqrt(128),
+  synthetic N(0,1) fp16 from a fixed seed; q4/q8 caches quantised MLX-affine
+  with group size 64.
+Each call reads a different layer's buffers (fp16: 8 sets = 0.79 GB, q4: 24
+sets = 0.67 GB, q8: 16 sets = 0.84 GB), so the 256 MB Infinity Cache cannot
+serve them.  The K timed calls are replayed from one HIP graph (captured after
+W eager warm-up calls), bracketed by HIP events on the launch stream.
+
+Algorithmic bytes per call count each live K/V1/V2 row once (plus scales and
+biases for packed caches) and q and y:
+  fp16 98,328,576 B, q4 27,672,576 B, q8 52,248,576 B.
+
+cpu_baseline: the oracle's C/OpenMP port (oracle/motif_oracle.c) on the host
+cores, one full fp16 call (32 heads x 16000 rows), median of 5 after 2
+warm-ups.  It is a reported baseline, not the target.
+
+stdout carries exactly one JSON line.  --extra adds µs/call lines for the
+other workloads of the path on stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "mlx-motif_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "decode-attn µs/call + achieved HBM GB/s (% peak) at KV=16k, fp16 & q4 cache"
+
+B, HQ, HKV, D = 1, 32, 8, 128
+KV_LEN, CAP = 16000, 16128
+GS = 64
+
+
+def alg_bytes(kind: str, kv_len: int = KV_LEN, hq: int = HQ, hkv: int = HKV, s_q: int = 1) -> int:
+    qy = hq * s_q * D * 2 + hq * s_q * 2 * D * 2
+    if kind == "f16":
+        return 3 * B * hkv * kv_len * D * 2 + qy
+    bits = 4 if kind == "q4" else 8
+    return 3 * B * hkv * kv_len * (D * bits // 8 + 2 * (D // GS) * 2) + qy
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_calls(torch, calls, steps: int, warmup: int, use_graph: bool = True):
+    """Average µs per call over `steps` calls cycling through `calls`."""
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    if use_graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                calls[i % len(calls)]()
+        g.replay()  # warm replay
+        torch.cuda.synchronize()
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+    else:
+        start.record(stream)
+        for i in range(steps):
+            calls[i % len(calls)]()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
+    from mlx_motif import _native
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).half()
+    sets = []
+    for _ in range(nsets):
+        k, v1, v2 = (torch.randn((B, hkv, cap, D), generator=g, device=dev).half()
+                     for _ in range(3))
+        sets.append((k, v1, v2, torch.empty((B, hq, s_q, 2 * D), dtype=torch.float16,
+                                            device=dev)))
+    nbytes = lib.motif_sdpa_workspace_bytes(B, hq, hkv, s_q, kv_len, D)
+    ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
+    scale = 1.0 / D ** 0.5
+
+    def mk(k, v1, v2, y):
+        def call():
+            stream = torch.cuda.current_stream().cuda_stream
+            if s_q == 1:
+                st = lib.motif_sdpa_dual_v(q.data_ptr(), k.data_ptr(), v1.data_ptr(),
+                                           v2.data_ptr(), y.data_ptr(), 0, B, hq, hkv, D, cap,
+                                           kv_len, scale, ws.data_ptr(), ws.numel(), stream)
+            else:
+                st = lib.motif_sdpa_dual_v_rows(q.data_ptr(), k.data_ptr(), v1.data_ptr(),
+                                                v2.data_ptr(), y.data_ptr(), 0, B, hq, hkv, s_q,
+                                                D, cap, kv_len, 1, scale, ws.data_ptr(),
+                                                ws.numel(), stream)
+            _native.check(st)
+        return call
+
+    return [mk(*s) for s in sets], (q, sets)
+
+
+def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
+    from mlx_motif import _native
+    from mlx_motif.kernels import quantize
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(4321 + bits)
+    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).half()
+    sets = []
+    for _ in range(nsets):
+        trips = []
+        for _ in range(3):
+            x = torch.randn((B, hkv, cap, D), generator=g, device=dev).half()
+            trips.append(quantize(x, group_size=GS, bits=bits))
+            del x
+        sets.append((trips, torch.empty((B, hq, s_q, 2 * D), dtype=torch.float16, device=dev)))
+    nbytes = lib.motif_sdpa_workspace_bytes(B, hq, hkv, s_q, kv_len, D)
+    ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
+    scale = 1.0 / D ** 0.5
+
+    def mk(trips, y):
+        ptrs = [t.data_ptr() for trip in trips for t in trip]
+
+        def call():
+            stream = torch.cuda.current_stream().cuda_stream
+            if s_q == 1:
+                st = lib.motif_sdpa_dual_v_q(q.data_ptr(), *ptrs, y.data_ptr(), 0, B, hq, hkv, D,
+                                             cap, kv_len, bits, GS, scale, ws.data_ptr(),
+                                             ws.numel(), stream)
+            else:
+                st = lib.motif_sdpa_dual_v_q_rows(q.data_ptr(), *ptrs, y.data_ptr(), 0, B, hq,
+                                                  hkv, s_q, D, cap, kv_len, 1, bits, GS, scale,
+                                                  ws.data_ptr(), ws.numel(), stream)
+            _native.check(st)
+        return call
+
+    return [mk(*s) for s in sets], (q, sets)
+
+
+def cpu_baseline():
+    """The oracle's C/OpenMP port timed on the host: one full fp16 call."""
+    import numpy as np
+
+    from oracle import c_oracle
+
+    rng = np.random.default_rng(99)
+    q = rng.standard_normal((B, HQ, 1, D)).astype(np.float16)
+    k, v1, v2 = (rng.standard_normal((B, HKV, CAP, D)).astype(np.float16) for _ in range(3))
+    threads = c_oracle.max_threads()
+    times = []
+    for i in range(7):
+        t0 = time.perf_counter()
+        c_oracle.sdpa_dual_v_f16(q, k, v1, v2, 1 / np.sqrt(D), KV_LEN, nthreads=threads)
+        t1 = time.perf_counter()
+        if i >= 2:
+            times.append((t1 - t0) * 1e6)
+    us = statistics.median(times)
+    return {
+        "value": round(us, 1),
+        "unit": "us/call",
+        "cores": threads,
+        "kind": "port",
+        "sample": "one full fp16 sdpa_dual_v call (32 heads x 16000 rows, D 128) of the "
+                  "C/OpenMP port oracle/motif_oracle.c, median of 5 after 2 warm-ups",
+        "gbps": round(alg_bytes("f16") / us / 1e3, 2),
+    }
+
+
+def load_traffic(name: str):
+    p = ROOT / "profiles" / f"traffic_{name}.json"
+    if p.is_file():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time eager launches")
+    ap.add_argument("--extra", action="store_true", help="also time the other workloads")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE {world}).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from mlx_motif import _native
+
+    lib = _native.lib()
+    dev = torch.device("cuda:0")
+    graph = not args.no_graph
+    res = {}
+    for kind, nsets in (("f16", 8), ("q4", 24), ("q8", 16)):
+        if kind == "f16":
+            calls, keep = make_fp16_calls(torch, lib, dev, nsets)
+        else:
+            calls, keep = make_q_calls(torch, lib, dev, nsets, 4 if kind == "q4" else 8)
+        us = time_calls(torch, calls, args.steps, args.warmup, graph)
+        gbps = alg_bytes(kind) / us / 1e3
+        res[kind] = {"us_per_call": round(us, 3), "gbps": round(gbps, 1),
+                     "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 1),
+                     "alg_bytes": alg_bytes(kind), "buffer_sets": nsets}
+        log(f"{kind}: {us:.3f} us/call  {gbps:.1f} GB/s  ({100 * gbps / PEAK_HBM_GBPS:.1f}% of "
+            f"{PEAK_HBM_GBPS:.0f})")
+        del calls, keep
+        torch.cuda.empty_cache()
+
+    if args.extra:
+        run_extra(torch, lib, dev, args)
+
+    f16 = res["f16"]
+    out = {
+        "metric": METRIC,
+        "value": f16["us_per_call"],
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(f16["us_per_call"] / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: N(0,1) fp16 K/V/q from a fixed seed (random cache, no checkpoint)",
+        "config": {
+            "workload": "sdpa_dual_v decode on the fp16 4-slot cache: B=1, 32 q-heads over 8 "
+                        "KV heads, head_dim 128, kv_len 16000 (cap 16128); q4/q8 at the same "
+                        "shape, group_size 64",
+            "cache_dtype": "f16", "kv_len": KV_LEN, "kv_cap": CAP, "heads_q": HQ,
+            "heads_kv": HKV, "head_dim": D, "timing": "hip graph replay" if graph else "eager",
+        },
+        "gbps": f16["gbps"],
+        "pct_peak": f16["pct_peak"],
+        "q4": res["q4"],
+        "q8": res["q8"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": f16["gbps"],
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(f16["gbps"] / PEAK_HBM_GBPS, 4),
+            "traffic": load_traffic("sdpa_dual_v_f16_kv16000"),
+        },
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def run_extra(torch, lib, dev, args):
+    """µs/call of the other workloads of the path (stderr, one JSON per line)."""
+    from mlx_motif.cache import MotifGroupedQuantizedKVCache
+    from mlx_motif.kernels import gda_post_split, polynorm
+
+    steps, warm = max(20, args.steps // 4), 5
+
+    def report(name, us, nbytes):
+        gbps = nbytes / us / 1e3
+        log("EXTRA " + json.dumps({"workload": name, "us_per_call": round(us, 3),
+                                   "gbps": round(gbps, 1),
+                                   "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 1)}))
+
+    # 48 back-to-back layer calls at kv_len 3204 over 48 distinct layer buffers
+    calls, keep = make_fp16_calls(torch, lib, dev, 48, kv_len=3204, cap=3328)
+    report("sdpa_dual_v f16 kv3204 x48 layers", time_calls(torch, calls, 48 * 4, warm),
+           alg_bytes("f16", 3204))
+    del calls, keep
+    # verify slab: 5 rows over a q8 cache of 32768 rows
+    calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
+    report("verify slab q8 5 rows kv32768", time_calls(torch, calls, steps, warm),
+           alg_bytes("q8", 32768, s_q=5))
+    del calls, keep
+    torch.cuda.empty_cache()
+    # gda_post_split prefill [1,16,3204,128]
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    o = [torch.randn((1, 16, 3204, 128), generator=g, device=dev).half() for _ in range(8)]
+    n = [torch.randn((1, 16, 3204, 128), generator=g, device=dev).half() for _ in range(8)]
+    w = torch.rand(128, generator=g, device=dev).half()
+    lam = torch.tensor([0.37], device=dev)
+    calls = [lambda i=i: gda_post_split(o[i], n[i], w, lam, 0.2, 1, 1e-6) for i in range(8)]
+    report("gda_post_split [1,16,3204,128]", time_calls(torch, calls, steps, warm),
+           3 * 16 * 3204 * 128 * 2)
+    del o, n, calls
+    # PolyNorm [3204, 13824]
+    xs = [torch.randn((3204, 13824), generator=g, device=dev).half() for _ in range(4)]
+    pw = torch.rand(3, generator=g, device=dev).half()
+    pb = torch.zeros(1, device=dev).half()
+    calls = [lambda i=i: polynorm(xs[i], pw, pb, 1e-6) for i in range(4)]
+    report("polynorm [3204,13824]", time_calls(torch, calls, steps, warm),
+           2 * 3204 * 13824 * 2)
+    del xs, calls
+    # decode write of one token into four q4 slots at row 15999
+    cache = MotifGroupedQuantizedKVCache(group_size=64, bits=4)
+    big = torch.randn((1, 8, 15999, 128), device=dev).half()
+    cache.update_and_fetch_4_quantized(big, big, big, big)
+    tok = torch.randn((1, 8, 1, 128), device=dev).half()
+
+    def write():
+        cache.offset = 15999
+        cache.update_and_fetch_4_quantized(tok, tok, tok, tok)
+
+    report("quant_write4 q4 1 token", time_calls(torch, [write], steps, warm),
+           4 * 8 * 128 * 2 + 4 * 8 * (64 + 8))
+
+
+if __name__ == "__main__":
+    sys.exit(main())

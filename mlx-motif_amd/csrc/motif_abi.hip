@@ -62,13 +62,19 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   while (gc < GV && gc < gc_max) gc *= 2;
   p.gc = gc;
   p.nchunk = (GV + gc - 1) / gc;
-  p.waves = tuning().waves_per_wg == 8 ? 8 : 4;
+  // 8-wave workgroups when their cross-wave LDS merge fits (D * gc <= 512
+  // floats per wave per slab), else 4.
+  const int max_waves = (D * gc <= 512) ? 8 : 4;
+  p.waves = tuning().waves_per_wg ? tuning().waves_per_wg : max_waves;
+  if (p.waves > max_waves) p.waves = max_waves;
 
   const int units = B * Hkv * p.nchunk;
   // Rows one block iteration of a workgroup consumes: waves x rows per wave
   // load (4 for 16 lanes per row) x unroll 4.  Splits are whole iterations.
   const int step = p.waves * 4 * 4;
-  int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : 2 * device_cu_count();
+  // Default: one round of workgroups over the CUs (an 8-wave workgroup
+  // fills a CU at this kernel's register use; a 4-wave one fills half).
+  int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count() * (8 / p.waves);
   int rows = kv_len > 0 ? kv_len : 1;
   int rps;
   if (tuning().rows_per_split > 0) {
@@ -78,9 +84,11 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
     int max_split = (rows + step - 1) / step;  // at least one iteration each
     if (nsplit > max_split) nsplit = max_split;
     if (nsplit < 1) nsplit = 1;
-    rps = (rows + nsplit - 1) / nsplit;
+    rps = (int)round_up((size_t)((rows + nsplit - 1) / nsplit), (size_t)step);
   }
-  rps = (int)round_up((size_t)rps, (size_t)step);
+  // The merge holds every split's (m, l) in LDS: at most kMaxSplits splits.
+  const int min_rps = (rows + kMaxSplits - 1) / kMaxSplits;
+  if (rps < min_rps) rps = (int)round_up((size_t)min_rps, (size_t)step);
   p.rows_per_split = rps;
   p.nsplit = (rows + rps - 1) / rps;
   if (p.nsplit < 1) p.nsplit = 1;

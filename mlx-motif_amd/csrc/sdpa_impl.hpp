@@ -27,6 +27,26 @@ namespace motif {
 
 constexpr float kNegSentinel = -1e30f;
 
+// Cross-workgroup hand-off of split partials without whole-cache maintenance.
+// Partials are stored and re-loaded with system-scope relaxed atomics, which
+// gfx950 issues with sc0 sc1: stores are written through the XCD's L2 to
+// memory, loads miss in L1/L2 and read memory.  A writer waits for all its
+// stores to complete (s_waitcnt 0) before it takes an arrival ticket, so
+// the workgroup that takes the last ticket reads complete partials.  (An
+// agent-scope __threadfence() here costs a buffer_wbl2 + buffer_inv of the
+// whole L2 per workgroup, which serialises per XCD.)
+__device__ inline void store_through(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ inline float load_through(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ inline void wait_stores_done() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the compiler from moving memory ops
+  __builtin_amdgcn_s_waitcnt(0);             // vmcnt = expcnt = lgkmcnt = 0
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // --------------------------------------------------------------- formats --
 // fp16 / bf16 / fp32 cache rows of D elements.  16 lanes per row.
 template <typename T_, int D_>
@@ -135,6 +155,114 @@ struct QFmt {
     }
   }
 };
+
+// ------------------------------------------------------- split merge ---
+// Combine the nsplit partials (m, l, o1, o2) of virtual heads qrow0 ..
+// qrow0+nvh-1 and write y.  Every load of a phase is independent of the
+// others so they are in flight together: (m, l) pairs go to LDS, one wave
+// per head turns them into factors exp2(m_s - M) and the total L, then each
+// output float4 is summed over its splits by P threads with 16 loads in
+// flight each, and the P partial sums meet in LDS.
+template <typename T, int D, int GC, int NW>
+__device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
+  constexpr int NT = NW * 64;
+  constexpr int C4 = 2 * D / 4;
+  constexpr int UNR = 16;
+  __shared__ float lds_f[GC][kMaxSplits];  // m_s, then exp2(m_s - M)
+  __shared__ float lds_l[GC][kMaxSplits];
+  __shared__ float lds_L[GC];
+  __shared__ float4 lds_acc[NT];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int ns = a.nsplit;
+
+  for (int i = tid; i < nvh * ns; i += NT) {
+    const int g = i / ns, s = i % ns;
+    const float* ml = a.part_ml + ((qrow0 + g) * ns + s) * 2;
+    lds_f[g][s] = load_through(ml);
+    lds_l[g][s] = load_through(ml + 1);
+  }
+  __syncthreads();
+  for (int g = wave; g < nvh; g += NW) {
+    float M = kNegSentinel;
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, lds_f[g][s]);
+    M = group_max<64>(M);
+    float L = 0.f;
+    for (int s = lane; s < ns; s += 64) {
+      const float f = fast_exp2(lds_f[g][s] - M);
+      lds_f[g][s] = f;
+      L = fmaf(lds_l[g][s], f, L);
+    }
+    L = group_sum<64>(L);
+    if (lane == 0) lds_L[g] = L;
+  }
+  __syncthreads();
+
+  const int items = nvh * C4;
+  const int P = items >= NT ? 1 : NT / items;  // threads per output float4
+  for (int base = 0; base < items; base += NT) {
+    const int idx = base + tid;
+    const int item = P == 1 ? idx : tid % items;
+    const int part = P == 1 ? 0 : tid / items;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool active = item < items && part < P;
+    if (active) {
+      const int g = item / C4;
+      const int c = (item % C4) * 4;
+      const float* po = a.part_o + (qrow0 + g) * ns * 2 * D + c;
+      for (int s0 = part; s0 < ns; s0 += P * UNR) {
+        float4 v[UNR];
+        float f[UNR];
+#pragma unroll
+        for (int j = 0; j < UNR; ++j) {
+          const int s = s0 + j * P;
+          if (s < ns) {
+            const float* src = po + (long)s * 2 * D;
+            v[j] = make_float4(load_through(src), load_through(src + 1), load_through(src + 2),
+                               load_through(src + 3));
+            f[j] = lds_f[g][s];
+          } else {
+            v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            f[j] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < UNR; ++j) {
+          acc.x = fmaf(v[j].x, f[j], acc.x);
+          acc.y = fmaf(v[j].y, f[j], acc.y);
+          acc.z = fmaf(v[j].z, f[j], acc.z);
+          acc.w = fmaf(v[j].w, f[j], acc.w);
+        }
+      }
+    }
+    if (P > 1) {
+      lds_acc[tid] = acc;
+      __syncthreads();
+      if (tid < items) {
+        float4 t = lds_acc[tid];
+        for (int p = 1; p < P; ++p) {
+          const float4 u = lds_acc[p * items + tid];
+          t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        acc = t;
+      }
+    }
+    const int out_item = P == 1 ? idx : tid;
+    if (out_item < items && (P == 1 || tid < items)) {
+      const int g = out_item / C4;
+      const int c = (out_item % C4) * 4;
+      const float L = lds_L[g];
+      const bool zero_l = L == 0.f;
+      const long yo = (qrow0 + g) * 2 * D + c;
+      Elem<T>::store(a.y, yo + 0, zero_l ? acc.x : acc.x / L);
+      Elem<T>::store(a.y, yo + 1, zero_l ? acc.y : acc.y / L);
+      Elem<T>::store(a.y, yo + 2, zero_l ? acc.z : acc.z / L);
+      Elem<T>::store(a.y, yo + 3, zero_l ? acc.w : acc.w / L);
+    }
+    if (P > 1) break;  // items < NT: a single pass covers every item
+  }
+}
 
 // ---------------------------------------------------------------- kernel --
 template <class Fmt, int GC, int NW, int U>
@@ -331,10 +459,10 @@ __global__ void __launch_bounds__(NW * 64) sdpa_dual_v_kernel(SdpaArgs a) {
     if (single) {
       Elem<T>::store(a.y, r * 2 * D + c, L == 0.f ? O : O / L);
     } else {
-      a.part_o[(r * a.nsplit + split) * 2 * D + c] = O;
+      store_through(a.part_o + (r * a.nsplit + split) * 2 * D + c, O);
       if (c == 0) {
-        a.part_ml[(r * a.nsplit + split) * 2] = M;
-        a.part_ml[(r * a.nsplit + split) * 2 + 1] = L;
+        store_through(a.part_ml + (r * a.nsplit + split) * 2, M);
+        store_through(a.part_ml + (r * a.nsplit + split) * 2 + 1, L);
       }
     }
   }
@@ -342,44 +470,18 @@ __global__ void __launch_bounds__(NW * 64) sdpa_dual_v_kernel(SdpaArgs a) {
 
   // ---- last workgroup of this (b, KV head, chunk) combines all splits.
   __shared__ int is_last;
-  __threadfence();
+  wait_stores_done();
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned t = atomicAdd(&a.counters[unit], 1u);
+    unsigned t = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_SYSTEM);
     is_last = (t == (unsigned)(a.nsplit - 1));
-    if (is_last) a.counters[unit] = 0u;  // re-arm for the next call
+    if (is_last)  // re-arm for the next call
+      __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   __syncthreads();
   if (!is_last) return;
-  __threadfence();
-
-  constexpr int C4 = 2 * D / 4;
-  for (int idx = threadIdx.x; idx < nvh * C4; idx += NW * 64) {
-    const int g = idx / C4;
-    const int c = (idx % C4) * 4;
-    const long r = qrow0 + g;
-    const float* ml = a.part_ml + r * a.nsplit * 2;
-    const float* po = a.part_o + r * a.nsplit * 2 * D + c;
-    float M = kNegSentinel;
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, ml[2 * s]);
-    float L = 0.f;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < a.nsplit; ++s) {
-      float f = fast_exp2(ml[2 * s] - M);
-      L = fmaf(ml[2 * s + 1], f, L);
-      float4 v = *reinterpret_cast<const float4*>(po + (long)s * 2 * D);
-      O.x = fmaf(v.x, f, O.x);
-      O.y = fmaf(v.y, f, O.y);
-      O.z = fmaf(v.z, f, O.z);
-      O.w = fmaf(v.w, f, O.w);
-    }
-    const bool zero_l = L == 0.f;
-    long yo = r * 2 * D + c;
-    Elem<T>::store(a.y, yo + 0, zero_l ? O.x : O.x / L);
-    Elem<T>::store(a.y, yo + 1, zero_l ? O.y : O.y / L);
-    Elem<T>::store(a.y, yo + 2, zero_l ? O.z : O.z / L);
-    Elem<T>::store(a.y, yo + 3, zero_l ? O.w : O.w / L);
-  }
+  merge_splits<T, D, GC, NW>(a, qrow0, nvh);
 }
 
 // Host launcher for one format.

@@ -49,6 +49,10 @@ struct SdpaPlan {
   size_t workspace_bytes;
 };
 
+// Upper bound on splits per (b, KV head, chunk): the final merge keeps every
+// split's (m, l) pair in LDS.
+constexpr int kMaxSplits = 256;
+
 // gc_max: the largest per-workgroup head count compiled for this head dim.
 SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max);
 

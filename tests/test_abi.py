@@ -1,0 +1,115 @@
+"""The C ABI surface on the CPU: the library loads, exports exactly what
+include/motif_hip.h declares (and what the ctypes binding binds), and
+rejects out-of-contract arguments before touching the GPU.  No kernel runs.
+"""
+
+from __future__ import annotations
+
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+from mlx_motif import _native
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "motif_hip.h"
+
+
+def _declared() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(motif_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_symbols_are_exported_and_bound():
+    lib = _native.lib()
+    declared = _declared()
+    assert declared == set(_native.exported_names()), declared ^ set(_native.exported_names())
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (motif_[a-z0-9_]+)$", out, flags=re.M))
+    assert declared <= exported, declared - exported
+    for name in declared:
+        assert getattr(lib, name) is not None
+
+
+def test_abi_version():
+    assert _native.lib().motif_abi_version() == 1
+
+
+def _err():
+    return _native.lib().motif_last_error().decode()
+
+
+def test_sdpa_contract_rejections_need_no_gpu():
+    lib = _native.lib()
+    st = lib.motif_sdpa_dual_v(None, None, None, None, None, 0, 1, 32, 8, 100, 256, 10, 0.1,
+                               None, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "multiple of 32" in _err()
+    st = lib.motif_sdpa_dual_v(None, None, None, None, None, 0, 1, 30, 8, 128, 256, 10, 0.1,
+                               None, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "multiple of H_kv" in _err()
+    st = lib.motif_sdpa_dual_v(None, None, None, None, None, 0, 1, 32, 8, 128, 256, 300, 0.1,
+                               None, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "kv_len=300" in _err()
+    st = lib.motif_sdpa_dual_v(None, None, None, None, None, 7, 1, 32, 8, 128, 256, 3, 0.1,
+                               None, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "dtype" in _err()
+
+
+@pytest.mark.parametrize("D,bits,fragment", [
+    (256, 8, "D/32 <= 32/bits"), (512, 4, "qk_per_thread | EL_PER_INT"),
+    (96, 8, "qk_per_thread | EL_PER_INT"), (160, 4, "qk_per_thread | EL_PER_INT"),
+])
+def test_packed_layout_contract_rejections(D, bits, fragment):
+    lib = _native.lib()
+    st = lib.motif_sdpa_dual_v_q(None, *[None] * 9, None, 0, 1, 4, 4, D, 64, 64, bits, 32, 0.1,
+                                 None, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and fragment in _err()
+
+
+def test_quant_and_epilogue_rejections():
+    lib = _native.lib()
+    assert lib.motif_quantize(None, None, None, None, 0, 4, 128, 3, 64, None) == -1
+    assert "bits" in _err()
+    assert lib.motif_quantize(None, None, None, None, 0, 4, 100, 4, 64, None) == -1
+    assert lib.motif_quantize(None, None, None, None, 0, 4, 128, 4, 16, None) == -1
+    vp4 = _native._VP4(None, None, None, None)
+    st = lib.motif_quant_write4(None, None, None, None, vp4, vp4, vp4, 0, 1, 8, 2, 128, 256, 255,
+                                4, 64, None)
+    assert st == -1 and "exceed capacity" in _err()
+    st = lib.motif_gda_post_split(None, None, None, None, 0, 1, 30, 8, 4, 1, 256, None, 0.8,
+                                  1e-5, None)
+    assert st == -1 and "q_origin=30 != q_groups(8) * gr(4)" in _err()
+    assert lib.motif_polynorm(None, None, None, None, 5, 3, 16, 1e-6, None) == -1
+
+
+def test_empty_work_is_a_no_op():
+    lib = _native.lib()
+    assert lib.motif_polynorm(None, None, None, None, 0, 0, 16, 1e-6, None) == 0
+    assert lib.motif_quantize(None, None, None, None, 0, 0, 128, 4, 64, None) == 0
+    assert lib.motif_gda_post_split(None, None, None, None, 0, 1, 0, 0, 4, 1, 256, None, 0.8,
+                                    1e-5, None) == 0
+
+
+def test_workspace_sizing_and_tuning():
+    lib = _native.lib()
+    counters = lib.motif_sdpa_counter_bytes(1, 32, 8, 1)
+    assert counters == 256
+    small = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16, 128)
+    big = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128)
+    assert counters <= small <= big
+    # the split count is capped (256 per KV head), so the partials are bounded
+    assert big <= counters + 32 * 256 * (2 * 128 + 2) * 4 + 512
+    with pytest.raises(_native.MotifNativeError):
+        _native.set_tuning("no_such_knob", 1)
+    _native.set_tuning("rows_per_split", 64)
+    forced = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128)
+    _native.set_tuning("rows_per_split", 0)
+    assert forced > big
+    assert lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128) == big
+    # too-small workspace for a multi-split plan is refused before any launch
+    st = lib.motif_sdpa_dual_v(1, 1, 1, 1, 1, 0, 1, 32, 8, 128, 16128, 16000, 0.1, None, 0, None)
+    assert st == _native.MOTIF_ERR_WORKSPACE and "workspace" in _err()

@@ -1,0 +1,228 @@
+"""Host-side logic on the CPU: the Python mirror of the reference kernel API
+(assertion messages, reference paths behind MLX_MOTIF_DISABLE_KERNELS, no
+silent CPU fallback) and the 4-slot caches' buffer contract (growth, trim,
+state), checked against the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_motif import cache as C
+from mlx_motif import kernels as K
+from mlx_motif.kernels import _common
+from oracle import oracle as O
+
+
+@pytest.fixture
+def disabled(monkeypatch):
+    monkeypatch.setattr(_common, "_DISABLE", True)
+
+
+@pytest.fixture
+def enabled(monkeypatch):
+    monkeypatch.setattr(_common, "_DISABLE", False)
+
+
+def _t(rng, shape, dtype=torch.float16, s=1.0):
+    return torch.from_numpy((rng.standard_normal(shape) * s).astype(np.float32)).to(dtype)
+
+
+# -------------------------------------------------- contract assertions ---
+
+def test_sdpa_dual_v_assertions(enabled, rng):
+    q = _t(rng, (1, 32, 2, 128))
+    k = _t(rng, (1, 8, 16, 128))
+    with pytest.raises(AssertionError, match="decode-only"):
+        K.sdpa_dual_v(q, k, k, k, 0.1)
+    with pytest.raises(AssertionError, match="multiple of 32"):
+        K.sdpa_dual_v(_t(rng, (1, 4, 1, 48)), _t(rng, (1, 4, 8, 48)), *[_t(rng, (1, 4, 8, 48))] * 2,
+                      0.1)
+    with pytest.raises(AssertionError, match=r"kv_len=17 must be in \[0, 16\]"):
+        K.sdpa_dual_v(q[:, :, :1], k, k, k, 0.1, kv_len=17)
+    with pytest.raises(AssertionError, match="v1,v2 must match"):
+        K.sdpa_dual_v(q[:, :, :1], k, k[:, :, :8], k, 0.1)
+
+
+@pytest.mark.parametrize("D,bits,gs,pattern", [
+    (256, 8, 128, r"D/32 <= 32/bits"),
+    (512, 4, 128, r"qk_per_thread \| EL_PER_INT"),
+    (96, 8, 32, r"qk_per_thread \| EL_PER_INT"),
+    (96, 4, 32, r"qk_per_thread \| EL_PER_INT"),
+    (160, 4, 32, r"qk_per_thread \| EL_PER_INT"),
+])
+def test_sdpa_q4_rejects_out_of_contract_shapes(enabled, rng, D, bits, gs, pattern):
+    """Reference tests/test_kernels_sdpa_dual_v_q4.py:162-232."""
+    q = _t(rng, (1, 4, 1, D))
+    data = torch.zeros((1, 4, 64, D * bits // 32), dtype=torch.uint32)
+    sc = torch.zeros((1, 4, 64, D // gs), dtype=torch.float16)
+    trip = (data, sc, sc)
+    with pytest.raises(AssertionError, match=pattern):
+        K.sdpa_dual_v_q4(q, trip, trip, trip, 0.1, group_size=gs, bits=bits)
+
+
+def test_gda_assertion(enabled, rng):
+    with pytest.raises(AssertionError, match=r"q_origin=30 != q_groups\(8\) \* gr\(4\)"):
+        K.gda_post_split(_t(rng, (1, 30, 1, 256)), _t(rng, (1, 8, 1, 256)), _t(rng, (256,)),
+                         torch.tensor([0.3]), 0.5, 4)
+
+
+def test_kernels_refuse_cpu_tensors(enabled, rng):
+    """No silent CPU fallback: valid shapes on CPU tensors raise."""
+    q, k = _t(rng, (1, 8, 1, 64)), _t(rng, (1, 8, 16, 64))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.sdpa_dual_v(q, k, k, k, 0.1)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.polynorm(_t(rng, (4, 16)), torch.ones(3), torch.zeros(1))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        K.quantize(_t(rng, (4, 64)), 64, 4)
+
+
+# ------------------------------------------------------ reference paths ---
+
+def test_disabled_sdpa_reference_matches_oracle(disabled, rng):
+    q, k, v1, v2 = _t(rng, (1, 32, 1, 128)), *(_t(rng, (1, 8, 300, 128)) for _ in range(3))
+    y = K.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128), kv_len=257)
+    ref = O.sdpa_dual_v(q.numpy(), k.numpy(), v1.numpy(), v2.numpy(), 1 / np.sqrt(128), 257)
+    assert y.dtype == torch.float16 and y.shape == (1, 32, 1, 256)
+    assert np.max(np.abs(y.float().numpy() - ref)) <= 2e-3
+
+
+def test_disabled_rows_reference_matches_oracle(disabled, rng):
+    q, k, v1, v2 = _t(rng, (1, 8, 5, 64)), *(_t(rng, (1, 4, 64, 64)) for _ in range(3))
+    y = K.sdpa_dual_v_rows(q, k, v1, v2, 0.125, kv_len=40, causal=True)
+    ref = O.sdpa_dual_v(q.numpy(), k.numpy(), v1.numpy(), v2.numpy(), 0.125, 40, causal=True)
+    assert np.max(np.abs(y.float().numpy() - ref)) <= 2e-3
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_disabled_q4_reference_matches_oracle(disabled, rng, bits):
+    q = _t(rng, (1, 8, 1, 128))
+    raw = [_t(rng, (1, 4, 100, 128)) for _ in range(3)]
+    trips = [K.quantize(x, 64, bits) for x in raw]
+    y = K.sdpa_dual_v_q4(q, *trips, 0.09, 64, bits, kv_len=90)
+    np_trips = [O.quantize(x.numpy(), 64, bits) for x in raw]
+    ref = O.sdpa_dual_v_q(q.numpy(), *np_trips, 0.09, 64, bits, 90, dequant_dtype="f16")
+    assert np.max(np.abs(y.float().numpy() - ref)) <= 2e-3
+
+
+@pytest.mark.parametrize("dtype,tag", [(torch.float16, "f16"), (torch.bfloat16, "bf16"),
+                                       (torch.float32, "f32")])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_torch_reference_quantizer_bit_identical_to_oracle(rng, dtype, tag, bits):
+    x = _t(rng, (3, 5, 128), dtype, 2.0)
+    d, s, b = K.quantize_reference(x, 64, bits)
+    rd, rs, rb = O.quantize(x.float().numpy(), 64, bits, out_dtype=tag)
+    assert d.dtype == torch.uint32
+    np.testing.assert_array_equal(d.view(torch.int32).numpy().view(np.uint32), rd)
+    np.testing.assert_array_equal(s.float().numpy(), np.asarray(rs, np.float32))
+    np.testing.assert_array_equal(b.float().numpy(), np.asarray(rb, np.float32))
+    y = K.dequantize_reference(d, s, b, 64, bits)
+    np.testing.assert_array_equal(y.float().numpy(),
+                                  np.asarray(O.dequantize(rd, rs, rb, 64, bits, tag), np.float32))
+
+
+def test_disabled_epilogues_match_oracle(disabled, rng):
+    o, n, w = _t(rng, (1, 8, 3, 256)), _t(rng, (1, 2, 3, 256)), _t(rng, (256,))
+    lam = torch.tensor([0.4321], dtype=torch.float32)
+    y = K.gda_post_split(o, n, w, lam, 0.65, 4, 1e-5)
+    assert y.dtype == torch.float32  # fp32 lambda promotes, as in the reference
+    ref = O.gda_post_split(o.numpy(), n.numpy(), w.numpy(), 0.4321, 0.65, 4, 1e-5)
+    np.testing.assert_allclose(y.numpy(), ref, rtol=1e-4, atol=1e-4)
+    m = torch.cat([o, n], dim=1)
+    np.testing.assert_allclose(K.gda_post(m, w, lam, 0.65, 2, 4, 1e-5).numpy(), ref, rtol=1e-4,
+                               atol=1e-4)
+    x = _t(rng, (3, 7, 256), torch.float32)
+    pw, pb = torch.tensor([0.4, 0.3, 0.3]), torch.tensor([0.05])
+    np.testing.assert_allclose(K.polynorm(x, pw, pb, 1e-6).numpy(),
+                               O.polynorm(x.numpy(), pw.numpy(), pb.numpy(), 1e-6),
+                               rtol=1e-4, atol=1e-4)
+
+
+def test_polynorm_zero_rows_returns_zeros(enabled):
+    x = torch.zeros((0, 16))
+    assert K.polynorm(x, torch.ones(3), torch.zeros(1)).shape == (0, 16)
+
+
+# ------------------------------------------------------------ caches ---
+
+def test_fp_cache_growth_and_fetch_contract(rng):
+    cache = C.MotifGroupedKVCache()
+    cache.step = 4
+    B, H, D = 1, 4, 32
+    rows = []
+    for S in (3, 1, 1, 5, 1):
+        new = [_t(rng, (B, H, S, D)) for _ in range(4)]
+        rows.append(new)
+        k1, k2, v1, v2 = cache.update_and_fetch_4(*new)
+    assert cache.offset == 11
+    assert k1.shape[2] >= 11 and k1.is_contiguous()
+    o = cache.offset
+    for i, t in enumerate((k1, k2, v1, v2)):
+        np.testing.assert_array_equal(t[:, :, :o].numpy(),
+                                      torch.cat([r[i] for r in rows], dim=2).numpy())
+    st = cache.state
+    assert all(s.shape[2] == o for s in st)
+    assert cache.meta_state == ("11",)
+    assert cache.trim(3) == 3 and cache.offset == 8
+    assert cache.trim(100) == 8 and cache.offset == 0
+
+
+def test_cache_rejects_mismatched_slot_heads(rng):
+    cache = C.MotifGroupedKVCache()
+    with pytest.raises(ValueError, match="share a head count"):
+        cache.update_and_fetch_4(_t(rng, (1, 8, 1, 32)), *[_t(rng, (1, 4, 1, 32))] * 3)
+    qc = C.MotifGroupedQuantizedKVCache(64, 4)
+    with pytest.raises(ValueError, match="share a head count"):
+        qc.update_and_fetch_4_quantized(_t(rng, (1, 8, 1, 64)), *[_t(rng, (1, 4, 1, 64))] * 3)
+
+
+def test_update_and_fetch_single_slot_unsupported():
+    with pytest.raises(NotImplementedError):
+        C.MotifGroupedKVCache().update_and_fetch(None, None)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_cache_reference_write_matches_per_slot_oracle(disabled, rng, bits):
+    """Reference path: concat + one quantisation + 12 slice writes, bit-identical
+    to the per-slot oracle write (reference tests/test_grouped_cache.py:168)."""
+    B, H, D, gs = 1, 8, 128, 64
+    cache = C.MotifGroupedQuantizedKVCache(group_size=gs, bits=bits)
+    ref = [(np.zeros((B, H, 256, D * bits // 32), np.uint32), np.zeros((B, H, 256, D // gs)),
+            np.zeros((B, H, 256, D // gs))) for _ in range(4)]
+    off = 0
+    for S in (5, 1, 1, 1):
+        new = [_t(rng, (B, H, S, D)) for _ in range(4)]
+        live = cache.update_and_fetch_4_quantized(*new)
+        O.quant_write4(ref, *[x.numpy() for x in new], off, gs, bits)
+        off += S
+    assert cache.offset == off == 8
+    for slot, r in zip(live, ref):
+        np.testing.assert_array_equal(slot[0].view(torch.int32).numpy().view(np.uint32), r[0])
+        np.testing.assert_array_equal(slot[1].float().numpy(), r[1])
+        np.testing.assert_array_equal(slot[2].float().numpy(), r[2])
+    meta = cache.meta_state
+    assert meta == ("8", str(gs), str(bits))
+    st = cache.state
+    assert all(part.shape[2] == 8 for slot in st for part in slot)
+
+
+@pytest.mark.parametrize("bits,tol", [(4, 0.5), (8, 0.05)])
+def test_quantized_cache_dequant_bridge(disabled, rng, bits, tol):
+    cache = C.MotifGroupedQuantizedKVCache(group_size=64, bits=bits)
+    new = [_t(rng, (1, 8, 5, 128), s=0.1) for _ in range(4)]
+    out = cache.update_and_fetch_4(*new)
+    assert all(t.shape == (1, 8, 5, 128) for t in out)
+    np.testing.assert_allclose(out[0].float().numpy(), new[0].float().numpy(), atol=tol, rtol=tol)
+
+
+def test_to_quantized(disabled, rng):
+    fc = C.MotifGroupedKVCache()
+    new = [_t(rng, (1, 4, 6, 64)) for _ in range(4)]
+    fc.update_and_fetch_4(*new)
+    qc = fc.to_quantized(group_size=64, bits=8)
+    assert qc.offset == 6 and qc.k1[0].shape == (1, 4, 6, 16)
+    rd, _, _ = O.quantize(new[0].numpy(), 64, 8)
+    np.testing.assert_array_equal(qc.k1[0].view(torch.int32).numpy().view(np.uint32), rd)

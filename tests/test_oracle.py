@@ -1,0 +1,264 @@
+"""Pins of the CPU oracle (oracle/oracle.py) — each check is independent of
+the formula it tests: a library routine, a brute-force loop, a closed form,
+an invariant of the format, the reference's own golden vector, or the second
+(C) restatement.  CPU only.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import pathlib
+
+import numpy as np
+import pytest
+
+from oracle import c_oracle
+from oracle import oracle as O
+
+GOLDEN = pathlib.Path(__file__).parent / "golden"
+
+
+def _f16(rng, shape, s=1.0):
+    return (rng.standard_normal(shape) * s).astype(np.float16)
+
+
+# ---------------------------------------------------------------- sdpa ---
+
+def test_sdpa_matches_torch_sdpa_float64(rng):
+    """An independent library routine: torch's scaled_dot_product_attention."""
+    import torch
+
+    B, Hq, Hkv, S, D, kv = 2, 8, 2, 1, 64, 77
+    q, k, v1, v2 = _f16(rng, (B, Hq, S, D)), *(_f16(rng, (B, Hkv, kv, D)) for _ in range(3))
+    y = O.sdpa_dual_v(q, k, v1, v2, 0.125)
+    G = Hq // Hkv
+    t = lambda a: torch.from_numpy(np.repeat(a.astype(np.float64), G, axis=1))  # noqa: E731
+    tq = torch.from_numpy(q.astype(np.float64))
+    a1 = torch.nn.functional.scaled_dot_product_attention(tq, t(k), t(v1), scale=0.125)
+    a2 = torch.nn.functional.scaled_dot_product_attention(tq, t(k), t(v2), scale=0.125)
+    np.testing.assert_allclose(y, torch.cat([a1, a2], -1).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_causal_rows_match_torch_masked_sdpa(rng):
+    import torch
+
+    B, H, S, D, kv = 1, 4, 5, 32, 40
+    q, k, v1, v2 = _f16(rng, (B, H, S, D)), *(_f16(rng, (B, H, kv, D)) for _ in range(3))
+    y = O.sdpa_dual_v(q, k, v1, v2, 0.3, causal=True)
+    mask = torch.ones(S, kv, dtype=torch.bool).tril(diagonal=kv - S)  # bottom-right aligned
+    t = lambda a: torch.from_numpy(a.astype(np.float64))  # noqa: E731
+    a1 = torch.nn.functional.scaled_dot_product_attention(t(q), t(k), t(v1), attn_mask=mask,
+                                                          scale=0.3)
+    np.testing.assert_allclose(y[..., :D], a1.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_sdpa_brute_force_scalar_loop(rng):
+    q, k, v1, v2 = _f16(rng, (1, 2, 1, 8)), *(_f16(rng, (1, 1, 5, 8)) for _ in range(3))
+    y = O.sdpa_dual_v(q, k, v1, v2, 0.5, kv_len=4)
+    for h in range(2):
+        s = [0.5 * sum(float(q[0, h, 0, d]) * float(k[0, 0, j, d]) for d in range(8))
+             for j in range(4)]
+        w = [math.exp(x - max(s)) for x in s]
+        for d in range(8):
+            e1 = sum(w[j] * float(v1[0, 0, j, d]) for j in range(4)) / sum(w)
+            e2 = sum(w[j] * float(v2[0, 0, j, d]) for j in range(4)) / sum(w)
+            assert abs(y[0, h, 0, d] - e1) < 1e-12 and abs(y[0, h, 0, 8 + d] - e2) < 1e-12
+
+
+def test_sdpa_closed_forms(rng):
+    q, k, v1, v2 = _f16(rng, (1, 4, 1, 32)), *(_f16(rng, (1, 4, 9, 32)) for _ in range(3))
+    # one live key -> that key's value rows
+    y = O.sdpa_dual_v(q, k, v1, v2, 0.2, kv_len=1)
+    np.testing.assert_array_equal(y[..., :32], np.broadcast_to(v1[:, :, :1], y[..., :32].shape))
+    np.testing.assert_array_equal(y[..., 32:], np.broadcast_to(v2[:, :, :1], y[..., 32:].shape))
+    # equal keys -> uniform weights -> mean of the values
+    kk = np.broadcast_to(k[:, :, :1], k.shape).copy()
+    y = O.sdpa_dual_v(q, kk, v1, v2, 0.2)
+    np.testing.assert_allclose(y[..., :32], v1.astype(np.float64).mean(axis=2, keepdims=True),
+                               rtol=1e-12, atol=1e-12)
+    # kv_len = 0 -> zeros (the kernel's o = 0 when l = 0)
+    assert not O.sdpa_dual_v(q, k, v1, v2, 0.2, kv_len=0).any()
+
+
+def test_sdpa_invariants(rng):
+    q = _f16(rng, (1, 8, 1, 64))
+    k, v = _f16(rng, (1, 2, 50, 64)), _f16(rng, (1, 2, 50, 64))
+    y = O.sdpa_dual_v(q, k, v, v, 0.1)
+    np.testing.assert_array_equal(y[..., :64], y[..., 64:])  # V1 = V2 -> equal halves
+    # GQA broadcast == explicitly repeated K/V (repeat-interleave of heads)
+    rep = lambda a: np.repeat(a, 4, axis=1)  # noqa: E731
+    np.testing.assert_allclose(y, O.sdpa_dual_v(q, rep(k), rep(v), rep(v), 0.1), atol=0, rtol=0)
+    # rows past kv_len never matter
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, 30:] = 1e4
+    v2[:, :, 30:] = -1e4
+    np.testing.assert_array_equal(O.sdpa_dual_v(q, k, v, v, 0.1, kv_len=30),
+                                  O.sdpa_dual_v(q, k2, v2, v2, 0.1, kv_len=30))
+
+
+def test_c_port_matches_numpy(rng):
+    q, k, v1, v2 = _f16(rng, (1, 16, 1, 128)), *(_f16(rng, (1, 4, 300, 128)) for _ in range(3))
+    y = c_oracle.sdpa_dual_v_f16(q, k, v1, v2, 1 / np.sqrt(128), kv_len=257)
+    np.testing.assert_allclose(y, O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128), 257), atol=2e-6)
+    q5 = _f16(rng, (1, 16, 5, 128))
+    y = c_oracle.sdpa_dual_v_f16(q5, k, v1, v2, 0.09, kv_len=200, causal=True)
+    np.testing.assert_allclose(y, O.sdpa_dual_v(q5, k, v1, v2, 0.09, 200, causal=True),
+                               atol=2e-6)
+    kq, vq1, vq2 = (O.quantize(t, 64, 4) for t in (k, v1, v2))
+    y = c_oracle.sdpa_dual_v_q_f16(q, kq, vq1, vq2, 0.09, 64, 4, kv_len=299)
+    np.testing.assert_allclose(y, O.sdpa_dual_v_q(q, kq, vq1, vq2, 0.09, 64, 4, 299), atol=2e-6)
+
+
+# ------------------------------------------------------------ quantizer ---
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantizer_format_invariants(rng, bits, gs):
+    x = _f16(rng, (3, 5, 256), 2.0)
+    data, scales, biases = O.quantize(x, gs, bits)
+    codes = O.unpack_codes(data, bits).reshape(3, 5, 256 // gs, gs)
+    n_bins = 2 ** bits - 1
+    assert codes.min() >= 0 and codes.max() <= n_bins
+    xg = x.astype(np.float32).reshape(3, 5, 256 // gs, gs)
+    edge_is_min = np.abs(xg.min(-1)) > np.abs(xg.max(-1))
+    edge = np.where(edge_is_min, xg.min(-1), xg.max(-1))
+    # the edge element gets code 0 and the bias is the edge (rounded to fp16)
+    at_edge = np.take_along_axis(codes, np.argmax(xg == edge[..., None], -1)[..., None], -1)
+    assert (at_edge == 0).all()
+    np.testing.assert_array_equal(biases.astype(np.float32),
+                                  edge.astype(np.float16).astype(np.float32))
+    # reconstruction in the format's fp32 arithmetic: codes strictly inside
+    # (0, n_bins) are within half a step of the input; refitting the scale to
+    # make the edge exact can shrink the far end of the range, where codes
+    # clamp at n_bins, by at most one more step.
+    d32, s32, b32 = O.quantize(x, gs, bits, out_dtype="f32")
+    c32 = O.unpack_codes(d32, bits).reshape(xg.shape)
+    recon = (s32.astype(np.float64)[..., None] * c32 + b32.astype(np.float64)[..., None])
+    step = np.abs(s32.astype(np.float64))[..., None]
+    err = np.abs(recon - xg)
+    inner = (c32 > 0) & (c32 < n_bins)
+    # (w - bias) / scale is rounded to fp32 before rint, and exact ties do occur
+    # with fp16 inputs, so allow that rounding on top of half a step
+    slack = 2.0 ** -22 * np.abs(xg - b32.astype(np.float64)[..., None])
+    assert (err[inner] <= (0.5 * step + slack)[inner]).all()
+    assert (err <= 1.5 * step + slack).all()
+
+
+def test_quantizer_zero_reconstructs_when_the_group_straddles_it():
+    """With bias = edge and scale = edge / q0, code -q0 decodes to exactly 0 in
+    the fp32 arithmetic of the format."""
+    w = np.linspace(-3.0, 1.5, 64).astype(np.float16)
+    w[10] = 0.0
+    data, s32, b32 = O.quantize(w[None], 64, 4, out_dtype="f32")
+    code = O.unpack_codes(data, 4)[0, 10]
+    assert np.float32(s32[0, 0]) * np.float32(code) + np.float32(b32[0, 0]) == 0.0
+
+
+def test_quantizer_special_groups():
+    zeros = O.quantize(np.zeros((1, 64), np.float16), 64, 4)
+    assert not zeros[0].any() and zeros[2][0, 0] == 0
+    # all-zero group: scale is -1e-7 (max side, eps floor), rounded to fp16
+    assert zeros[1][0, 0] == np.float16(-1e-7)
+    const = O.quantize(np.full((1, 64), 3.0, np.float16), 64, 8)
+    assert np.all(O.dequantize(*const, 64, 8) == 3.0)
+
+
+def test_quantizer_hand_worked_group():
+    """w = 0..31 (gs 32, 4 bits): max side, scale = 31/-15, bias = 31,
+    code(w) = rint((w - 31) / scale) = rint((31 - w) * 15 / 31)."""
+    w = np.arange(32, dtype=np.float16)[None]
+    data, s, b = O.quantize(w, 32, 4, out_dtype="f32")
+    assert b[0, 0] == np.float32(31.0)
+    assert s[0, 0] == np.float32(31.0) / np.float32(-15.0)
+    codes = O.unpack_codes(data, 4)[0]
+    assert codes[0] == 15 and codes[31] == 0 and codes[16] == 7 and codes[15] == 8
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantizer_batched_equals_per_slot(rng, bits):
+    """Head-axis concat + one quantisation == per-slot quantisation
+    (the invariant of reference tests/test_grouped_cache.py:168)."""
+    slots = [_f16(rng, (1, 8, 5, 128)) for _ in range(4)]
+    d, s, b = O.quantize(np.concatenate(slots, axis=1), 64, bits)
+    for i, x in enumerate(slots):
+        di, si, bi = O.quantize(x, 64, bits)
+        np.testing.assert_array_equal(d[:, 8 * i:8 * (i + 1)], di)
+        np.testing.assert_array_equal(s[:, 8 * i:8 * (i + 1)], si)
+        np.testing.assert_array_equal(b[:, 8 * i:8 * (i + 1)], bi)
+
+
+@pytest.mark.parametrize("bits,tol", [(4, 0.5), (8, 0.05)])
+def test_quantizer_roundtrip_tolerance(rng, bits, tol):
+    """Reference tests/test_grouped_cache.py:112-129 (N(0, 0.1), atol=rtol=tol)."""
+    x = _f16(rng, (1, 8, 5, 128), 0.1)
+    np.testing.assert_allclose(O.dequantize(*O.quantize(x, 64, bits), 64, bits),
+                               x.astype(np.float64), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_quantizer_c_restatement_bit_identical(rng, bits, gs):
+    x = _f16(rng, (4, 7, 256), 3.0)
+    for a, b in zip(O.quantize(x, gs, bits), c_oracle.quantize_f16(x, gs, bits)):
+        np.testing.assert_array_equal(np.asarray(a).view(np.uint16) if a.dtype == np.float16
+                                      else a, np.asarray(b).view(np.uint16)
+                                      if b.dtype == np.float16 else b)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dequantize_bit_extract_loop(rng, bits):
+    """Little-endian code order and s*u+b (probe contract, mlp.py:165-198),
+    checked by a scalar loop over words and bit positions."""
+    x = _f16(rng, (2, 64))
+    data, s, b = O.quantize(x, 32, bits)
+    y = O.dequantize(data, s, b, 32, bits, out_dtype="f16")
+    el = 32 // bits
+    for r in range(2):
+        for i in range(64):
+            word = int(data[r, i // el])
+            u = (word >> ((i % el) * bits)) & ((1 << bits) - 1)
+            ref = np.float16(np.float32(s[r, i // 32]) * np.float32(u) + np.float32(b[r, i // 32]))
+            assert y[r, i] == ref
+
+
+def test_round_to_bf16():
+    x = np.array([1.0, 1.00390625, 1.005859375, -3.14159, 65504.0, 1e-40], np.float32)
+    r = O.round_to(x, "bf16")
+    assert r[0] == 1.0 and r[1] == 1.0  # tie -> even
+    assert r[2] == np.float32(1.0078125)
+    np.testing.assert_allclose(r[:5], x[:5], rtol=2 ** -8)
+    assert abs(r[5] - x[5]) <= 2.0 ** -133  # subnormal: half of bf16's subnormal spacing
+
+
+# ------------------------------------------------------------ epilogues ---
+
+def test_polynorm_reference_golden_vector():
+    case = json.loads((GOLDEN / "polynorm_reference_2x3.json").read_text())
+    y = O.polynorm(np.array(case["input"]), case["weight"], case["bias"], case["eps"])
+    np.testing.assert_allclose(y, np.array(case["expected"]), rtol=1e-13, atol=1e-13)
+
+
+def test_gda_closed_forms(rng):
+    o = rng.standard_normal((1, 8, 3, 64))
+    n = rng.standard_normal((1, 2, 3, 64))
+    w = np.full(64, 1.7)
+    y = O.gda_post_split(o, n, w, 0.3, 0.6, 4, 0.0)
+    # constant weight: each row's RMS is |w * (1 - lambda_init)|
+    np.testing.assert_allclose(np.sqrt((y * y).mean(-1)), 1.7 * 0.4, rtol=1e-12)
+    # lambda = 0: RMSNorm of o
+    y0 = O.gda_post_split(o, n, np.ones(64), 0.0, 0.0, 4, 0.0)
+    np.testing.assert_allclose(y0, o / np.sqrt((o * o).mean(-1, keepdims=True)), rtol=1e-12)
+    # gr broadcast == explicit repeat with gr = 1
+    np.testing.assert_allclose(y, O.gda_post_split(o, np.repeat(n, 4, axis=1), w, 0.3, 0.6, 1,
+                                                   0.0), rtol=0, atol=0)
+    # merged layout == split layout
+    m = np.concatenate([o, n], axis=1)
+    np.testing.assert_array_equal(O.gda_post(m, w, 0.3, 0.6, 2, 4, 0.0), y)
+
+
+def test_lambda_formulas():
+    assert abs(O.lambda_init(1) - 0.2) < 1e-15
+    assert abs(O.lambda_init(1000) - 0.8) < 1e-12
+    lq1, lk1, lq2, lk2 = (np.full(4, 0.1), np.full(4, 0.2), np.zeros(4), np.zeros(4))
+    assert abs(O.lambda_full(lq1, lk1, lq2, lk2, 0.2) - (math.exp(0.08) - 1 + 0.2)) < 1e-15
