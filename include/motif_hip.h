@@ -187,8 +187,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
 /* ------------------------------------------------------------------------ *
  * Tuning knobs of the split-KV kernels (process-wide; for benchmarks and
  * sweeps, not needed for correct use).  key: "rows_per_split",
- * "waves_per_wg", "min_wgs".  value 0 restores the default.  Returns
- * MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key.
+ * "waves_per_wg", "min_wgs" (value 0 restores the default), "mfma" (1, the
+ * default: matrix-core kernels where compiled; 0: VALU kernels only).
+ * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.
  * ------------------------------------------------------------------------ */
 int motif_set_tuning(const char* key, int value);
 

@@ -35,6 +35,7 @@ struct Tuning {
   int rows_per_split = 0;  // 0 = automatic
   int waves_per_wg = 0;    // 0 = automatic
   int min_wgs = 0;         // 0 = automatic
+  int mfma = 1;            // 1 = matrix-core kernels where compiled, 0 = VALU kernels
 };
 Tuning& tuning();
 

@@ -28,18 +28,39 @@ namespace motif {
 constexpr float kNegSentinel = -1e30f;
 
 // Cross-workgroup hand-off of split partials without whole-cache maintenance.
-// Partials are stored and re-loaded with system-scope relaxed atomics, which
-// gfx950 issues with sc0 sc1: stores are written through the XCD's L2 to
-// memory, loads miss in L1/L2 and read memory.  A writer waits for all its
-// stores to complete (s_waitcnt 0) before it takes an arrival ticket, so
+// Partials are stored and re-loaded through raw buffer operations with the
+// sc0|sc1 cache policy: stores are written through the XCD's L2 to memory,
+// loads miss in L1/L2 and read memory, both 16 bytes per lane and without
+// the per-access waits a volatile access would add.  A writer waits for all
+// its stores to complete (s_waitcnt 0) before it takes an arrival ticket, so
 // the workgroup that takes the last ticket reads complete partials.  (An
 // agent-scope __threadfence() here costs a buffer_wbl2 + buffer_inv of the
 // whole L2 per workgroup, which serialises per XCD.)
-__device__ inline void store_through(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kCachePolicyThrough = 1 | 16;  // sc0 | sc1
+
+// Buffer resource over [base, base + bytes); lanes outside it read 0 and
+// drop their stores.
+__device__ inline __amdgpu_buffer_rsrc_t part_rsrc(const float* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), (short)0, (int)bytes,
+                                           0x00020000);
 }
-__device__ inline float load_through(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+__device__ inline void store_through4(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r, byte_off, 0,
+                                         kCachePolicyThrough);
+}
+__device__ inline float4 load_through4(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+  return __builtin_bit_cast(
+      float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicyThrough));
+}
+__device__ inline void store_through2(__amdgpu_buffer_rsrc_t r, unsigned byte_off, float2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, byte_off, 0,
+                                        kCachePolicyThrough);
+}
+__device__ inline float2 load_through2(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+  return __builtin_bit_cast(
+      float2, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kCachePolicyThrough));
 }
 __device__ inline void wait_stores_done() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);  // keep the compiler from moving memory ops
@@ -163,6 +184,25 @@ struct QFmt {
 // per head turns them into factors exp2(m_s - M) and the total L, then each
 // output float4 is summed over its splits by P threads with 16 loads in
 // flight each, and the P partial sums meet in LDS.
+// Floats of padding per LDS head row: keeps the head rows of the
+// cross-wave staging buffer on different LDS banks.
+constexpr int kLdsPad = 4;
+
+template <typename T, int D>
+__device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) {
+  const bool z = L == 0.f;
+  Elem<T>::store(a.y, off + 0, z ? v.x : v.x / L);
+  Elem<T>::store(a.y, off + 1, z ? v.y : v.y / L);
+  Elem<T>::store(a.y, off + 2, z ? v.z : v.z / L);
+  Elem<T>::store(a.y, off + 3, z ? v.w : v.w / L);
+}
+
+// Combine the nsplit partials (m, l, o1, o2) of virtual heads qrow0 ..
+// qrow0+nvh-1 and write y.  One round trip: every thread issues its (m, l)
+// loads (to LDS) and the 16-byte loads of its first UNR partials (to
+// registers) before anything is consumed; one wave per head then turns the
+// maxima into factors exp2(m_s - M) and the total L, and P threads per
+// output float4 sum their splits, meeting in LDS.
 template <typename T, int D, int GC, int NW>
 __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
   constexpr int NT = NW * 64;
@@ -171,19 +211,35 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
   __shared__ float lds_f[GC][kMaxSplits];  // m_s, then exp2(m_s - M)
   __shared__ float lds_l[GC][kMaxSplits];
   __shared__ float lds_L[GC];
-  __shared__ float4 lds_acc[NT];
+  __shared__ __attribute__((aligned(16))) float4 lds_acc[NT];
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
   const int ns = a.nsplit;
+  const auto ro = part_rsrc(a.part_o + qrow0 * ns * 2 * D, (unsigned)(nvh * ns * 2 * D * 4));
+  const auto rml = part_rsrc(a.part_ml + qrow0 * ns * 2, (unsigned)(nvh * ns * 2 * 4));
 
   for (int i = tid; i < nvh * ns; i += NT) {
-    const int g = i / ns, s = i % ns;
-    const float* ml = a.part_ml + ((qrow0 + g) * ns + s) * 2;
-    lds_f[g][s] = load_through(ml);
-    lds_l[g][s] = load_through(ml + 1);
+    const float2 v = load_through2(rml, (unsigned)i * 8u);
+    lds_f[i / ns][i % ns] = v.x;
+    lds_l[i / ns][i % ns] = v.y;
+  }
+  const int items = nvh * C4;
+  const int P = items >= NT ? 1 : NT / items;  // threads per output float4
+  const int passes = P > 1 ? 1 : (items + NT - 1) / NT;
+  // this thread's output float4 of pass 0 and its share of the splits
+  const int item0 = P > 1 ? tid % items : tid;
+  const int part = P > 1 ? tid / items : 0;
+  const bool on0 = item0 < items && part < P;
+  float4 pre[UNR];
+#pragma unroll
+  for (int j = 0; j < UNR; ++j) {
+    const int s = part + j * P;
+    const unsigned off = (unsigned)((((item0 / C4) * ns + s) * 2 * D + (item0 % C4) * 4) * 4);
+    pre[j] = (on0 && s < ns) ? load_through4(ro, off) : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   __syncthreads();
+
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   for (int g = wave; g < nvh; g += NW) {
     float M = kNegSentinel;
     for (int s = lane; s < ns; s += 64) M = fmaxf(M, lds_f[g][s]);
@@ -199,40 +255,32 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
   }
   __syncthreads();
 
-  const int items = nvh * C4;
-  const int P = items >= NT ? 1 : NT / items;  // threads per output float4
-  for (int base = 0; base < items; base += NT) {
-    const int idx = base + tid;
-    const int item = P == 1 ? idx : tid % items;
-    const int part = P == 1 ? 0 : tid / items;
+  for (int ps = 0; ps < passes; ++ps) {
+    const int item = P > 1 ? item0 : ps * NT + tid;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const bool active = item < items && part < P;
-    if (active) {
+    if (item < items && part < P) {
       const int g = item / C4;
       const int c = (item % C4) * 4;
-      const float* po = a.part_o + (qrow0 + g) * ns * 2 * D + c;
       for (int s0 = part; s0 < ns; s0 += P * UNR) {
         float4 v[UNR];
-        float f[UNR];
 #pragma unroll
         for (int j = 0; j < UNR; ++j) {
           const int s = s0 + j * P;
-          if (s < ns) {
-            const float* src = po + (long)s * 2 * D;
-            v[j] = make_float4(load_through(src), load_through(src + 1), load_through(src + 2),
-                               load_through(src + 3));
-            f[j] = lds_f[g][s];
+          if (ps == 0 && s0 == part) {
+            v[j] = pre[j];
           } else {
-            v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-            f[j] = 0.f;
+            const unsigned off = (unsigned)(((g * ns + s) * 2 * D + c) * 4);
+            v[j] = s < ns ? load_through4(ro, off) : make_float4(0.f, 0.f, 0.f, 0.f);
           }
         }
 #pragma unroll
         for (int j = 0; j < UNR; ++j) {
-          acc.x = fmaf(v[j].x, f[j], acc.x);
-          acc.y = fmaf(v[j].y, f[j], acc.y);
-          acc.z = fmaf(v[j].z, f[j], acc.z);
-          acc.w = fmaf(v[j].w, f[j], acc.w);
+          const int s = s0 + j * P;
+          const float f = s < ns ? lds_f[g][s] : 0.f;
+          acc.x = fmaf(v[j].x, f, acc.x);
+          acc.y = fmaf(v[j].y, f, acc.y);
+          acc.z = fmaf(v[j].z, f, acc.z);
+          acc.w = fmaf(v[j].w, f, acc.w);
         }
       }
     }
@@ -245,23 +293,76 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
           const float4 u = lds_acc[p * items + tid];
           t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
         }
-        acc = t;
+        const int g = tid / C4;
+        store_y4<T, D>(a, (qrow0 + g) * 2 * D + (tid % C4) * 4, t, lds_L[g]);
       }
+    } else if (item < items) {
+      const int g = item / C4;
+      store_y4<T, D>(a, (qrow0 + g) * 2 * D + (item % C4) * 4, acc, lds_L[g]);
     }
-    const int out_item = P == 1 ? idx : tid;
-    if (out_item < items && (P == 1 || tid < items)) {
-      const int g = out_item / C4;
-      const int c = (out_item % C4) * 4;
-      const float L = lds_L[g];
-      const bool zero_l = L == 0.f;
-      const long yo = (qrow0 + g) * 2 * D + c;
-      Elem<T>::store(a.y, yo + 0, zero_l ? acc.x : acc.x / L);
-      Elem<T>::store(a.y, yo + 1, zero_l ? acc.y : acc.y / L);
-      Elem<T>::store(a.y, yo + 2, zero_l ? acc.z : acc.z / L);
-      Elem<T>::store(a.y, yo + 3, zero_l ? acc.w : acc.w / L);
-    }
-    if (P > 1) break;  // items < NT: a single pass covers every item
   }
+}
+
+// ------------------------------------------------- workgroup epilogue ---
+// Combine the NW waves' (m, l, o1, o2) staged in LDS (log2-domain running
+// max, sum and unnormalised accumulators per virtual head), then either
+// write y (single split) or publish this split's partial with 16-byte
+// write-through stores and, in the workgroup that arrives last for its
+// (b, KV head, chunk), merge all splits.  Called by every thread of the
+// workgroup after a barrier.
+template <typename T, int D, int GC, int NW>
+__device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * D + kLdsPad],
+                            const float (&lds_m)[NW][GC], const float (&lds_l)[NW][GC],
+                            long qrow0, int nvh, int split, int unit) {
+  constexpr int C4 = 2 * D / 4;
+  const bool single = a.nsplit == 1;
+  const int ns = a.nsplit;
+  // (single split: no workspace, empty resources that are never used)
+  const auto ro = part_rsrc(single ? nullptr : a.part_o + qrow0 * ns * 2 * D,
+                            single ? 0u : (unsigned)(nvh * ns * 2 * D * 4));
+  const auto rml = part_rsrc(single ? nullptr : a.part_ml + qrow0 * ns * 2,
+                             single ? 0u : (unsigned)(nvh * ns * 2 * 4));
+  for (int it = threadIdx.x; it < nvh * C4; it += NW * 64) {
+    const int g = it / C4;
+    const int c = (it % C4) * 4;
+    float M = kNegSentinel;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, lds_m[w][g]);
+    float L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float f = fast_exp2(lds_m[w][g] - M);
+      L = fmaf(lds_l[w][g], f, L);
+      const float4 v = *reinterpret_cast<const float4*>(&lds_o[w][g][c]);
+      O.x = fmaf(v.x, f, O.x);
+      O.y = fmaf(v.y, f, O.y);
+      O.z = fmaf(v.z, f, O.z);
+      O.w = fmaf(v.w, f, O.w);
+    }
+    if (single) {
+      store_y4<T, D>(a, (qrow0 + g) * 2 * D + c, O, L);
+    } else {
+      store_through4(ro, (unsigned)(((g * ns + split) * 2 * D + c) * 4), O);
+      if (c == 0) store_through2(rml, (unsigned)((g * ns + split) * 8), make_float2(M, L));
+    }
+  }
+  if (single) return;
+
+  // ---- last workgroup of this (b, KV head, chunk) combines all splits.
+  __shared__ int is_last;
+  wait_stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned t = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_SYSTEM);
+    is_last = (t == (unsigned)(a.nsplit - 1));
+    if (is_last)  // re-arm for the next call
+      __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  __syncthreads();
+  if (!is_last) return;
+  merge_splits<T, D, GC, NW>(a, qrow0, nvh);
 }
 
 // ---------------------------------------------------------------- kernel --
@@ -421,8 +522,8 @@ __global__ void __launch_bounds__(NW * 64) sdpa_dual_v_kernel(SdpaArgs a) {
     l[g] = L;
   }
 
-  // ---- merge the NW waves through LDS.
-  __shared__ float lds_o[NW][GC][2 * D];
+  // ---- hand the wave results to the shared epilogue through LDS.
+  __shared__ __attribute__((aligned(16))) float lds_o[NW][GC][2 * D + kLdsPad];
   __shared__ float lds_m[NW][GC];
   __shared__ float lds_l[NW][GC];
   if (rg == 0) {
@@ -440,48 +541,7 @@ __global__ void __launch_bounds__(NW * 64) sdpa_dual_v_kernel(SdpaArgs a) {
     }
   }
   __syncthreads();
-
-  const bool single = a.nsplit == 1;
-  for (int idx = threadIdx.x; idx < nvh * 2 * D; idx += NW * 64) {
-    const int g = idx / (2 * D);
-    const int c = idx % (2 * D);
-    float M = kNegSentinel;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, lds_m[w][g]);
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      float f = fast_exp2(lds_m[w][g] - M);
-      L = fmaf(lds_l[w][g], f, L);
-      O = fmaf(lds_o[w][g][c], f, O);
-    }
-    const long r = qrow0 + g;
-    if (single) {
-      Elem<T>::store(a.y, r * 2 * D + c, L == 0.f ? O : O / L);
-    } else {
-      store_through(a.part_o + (r * a.nsplit + split) * 2 * D + c, O);
-      if (c == 0) {
-        store_through(a.part_ml + (r * a.nsplit + split) * 2, M);
-        store_through(a.part_ml + (r * a.nsplit + split) * 2 + 1, L);
-      }
-    }
-  }
-  if (single) return;
-
-  // ---- last workgroup of this (b, KV head, chunk) combines all splits.
-  __shared__ int is_last;
-  wait_stores_done();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned t = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_SYSTEM);
-    is_last = (t == (unsigned)(a.nsplit - 1));
-    if (is_last)  // re-arm for the next call
-      __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  merge_splits<T, D, GC, NW>(a, qrow0, nvh);
+  wg_epilogue<T, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
 // Host launcher for one format.

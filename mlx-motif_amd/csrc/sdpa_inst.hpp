@@ -1,7 +1,10 @@
 // Instantiation bodies for one element type; included by sdpa_{f16,bf16,f32}.hip
 // with MOTIF_ELEM and MOTIF_SUFFIX defined.
+#include <type_traits>
+
 #include "sdpa_dispatch.hpp"
 #include "sdpa_impl.hpp"
+#include "sdpa_mfma.hpp"
 
 namespace motif {
 
@@ -11,6 +14,10 @@ namespace motif {
 int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                               hipStream_t s) {
   const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
+    if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0)
+      return launch_sdpa_mfma_f16(a, p.gc, p.waves, nblocks, s);
+  }
   switch (D) {
     case 32: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 32>>(a, p.gc, p.waves, nblocks, s);
     case 64: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 64>>(a, p.gc, p.waves, nblocks, s);

@@ -1,0 +1,257 @@
+// Matrix-core (MFMA) formulation of split-KV dual-V decode for head_dim 128.
+//
+// The VALU formulation spends ~3k lane-instructions per KV row (dot products,
+// DPP reductions, per-head FMAs into two value slabs), which caps it far
+// below the HBM roofline.  Here one wave processes 16 KV rows per step with
+// matrix instructions, the virtual heads (GQA heads x query rows) riding the
+// 16 columns of the MFMA:
+//
+//   S^T (16 rows x 16 heads) = K (16 x 128) . Q^T (128 x 16)
+//       4 x v_mfma_f32_16x16x32_f16; A = K rows exactly as stored (each lane
+//       reads 16 contiguous bytes of one row per step), B = Q^T held in
+//       registers for the whole split.
+//   O^T (128 ch x 16 heads) += V^T (128 x 16 rows) . P^T (16 rows x 16 heads)
+//       8 x v_mfma_f32_16x16x16_f16 per value slab.  The C layout of S^T
+//       (lane l: rows 4*(l/16)+r, head l%16) is exactly the B layout P^T
+//       needs, so softmax weights never move between lanes.  V^T fragments
+//       (4 rows x 1 channel per lane) come from 16-byte row loads (8
+//       channels of one row per lane, four whole rows per instruction)
+//       paired across rows with one v_perm_b32 per 2 values.
+//   l (16 heads) += ones . P^T: one extra MFMA sums the same fp16-rounded
+//       weights that multiply V, so o/l is consistent.
+//
+// Softmax state per head (column): running max in log2 units, shared by
+// the 4 lanes of the column; accumulators are rescaled only when some
+// column's max grows (wave-uniform branch).  The workgroup epilogue
+// (cross-wave LDS merge, split partials, last-arrival merge) is shared with
+// the VALU kernel.
+#pragma once
+
+#include "sdpa_impl.hpp"
+
+namespace motif {
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Causal row limit of virtual head vh (see sdpa_dual_v_kernel).
+__device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
+  const int s = vh % a.S_q;
+  int L = a.causal ? a.kv_len - a.S_q + s + 1 : a.kv_len;
+  return L < 0 ? 0 : (L > a.kv_len ? a.kv_len : L);
+}
+
+template <int GC, int NW, int U>
+__global__ void __launch_bounds__(NW * 64) sdpa_mfma_f16_kernel(SdpaArgs a) {
+  using T = half_t;
+  constexpr int D = 128;
+  static_assert(GC <= 16, "virtual heads ride the 16 MFMA columns");
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;  // MFMA column: virtual head (S^T, P^T, O^T)
+  const int blk = lane >> 4;  // MFMA k/row block
+
+  const int units = a.B * a.Hkv * a.nchunk;
+  const int unit = blockIdx.x % units;
+  const int split = blockIdx.x / units;
+  const int chunk = unit % a.nchunk;
+  const int bk = unit / a.nchunk;
+  const int b = bk / a.Hkv;
+  const int kvh = bk % a.Hkv;
+  const int vh0 = chunk * GC;
+  const int nvh = min(GC, a.GV - vh0);
+  const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
+
+  int max_lim = 0;
+  for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
+  const bool col_ok = col < nvh;
+  const int lim = col_ok ? vhead_limit(a, vh0 + col) : 0;
+  const int r_begin = split * a.rows_per_split;
+  const int r_end = min(r_begin + a.rows_per_split, max_lim);
+
+  // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds head col,
+  // channels 32*s + 8*blk .. +7 for k-step s.
+  half8_t qb[4];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
+      qb[s] = __builtin_bit_cast(half8_t, w);
+    }
+  }
+
+  const uint16_t* kbase = (const uint16_t*)a.k + (long)bk * a.kv_cap * D;
+  const uint32_t* v1base = (const uint32_t*)a.v1 + (long)bk * a.kv_cap * (D / 2);
+  const uint32_t* v2base = (const uint32_t*)a.v2 + (long)bk * a.kv_cap * (D / 2);
+
+  floatx4 acc1[8], acc2[8], accl;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    acc1[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  accl = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegSentinel;
+  const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+
+  // U tiles of 16 rows per wave per iteration: all of their loads are issued
+  // before any of them is consumed, so a wave keeps U x 12 KB in flight.
+  for (int base = r_begin + wave * 16; base < r_end; base += NW * 16 * U) {
+    half8_t ka[U][4];
+    uint32_t v1w[U][4][4], v2w[U][4][4];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t0 = base + u * NW * 16;
+      // K rows for S^T: row t0 + col (A operand row = lane % 16).
+      const int krow = t0 + col;
+      if (krow < r_end) {
+        const uint16_t* kp = kbase + (long)krow * D + 8 * blk;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          ka[u][s] = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4*>(kp + 32 * s));
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, make_uint4(0, 0, 0, 0));
+      }
+      // V rows t0 + 4*blk + r: 16 bytes per lane, dwords 4*col .. 4*col+3
+      // (dword 4*col + t holds channels 8*col + 2t, +1); one instruction
+      // covers four whole rows.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = t0 + 4 * blk + r;
+        if (row < r_end) {
+          const uint4 w1 = *reinterpret_cast<const uint4*>(v1base + (long)row * (D / 2) + 4 * col);
+          const uint4 w2 = *reinterpret_cast<const uint4*>(v2base + (long)row * (D / 2) + 4 * col);
+          v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
+          v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            v1w[u][r][t] = 0u;
+            v2w[u][r][t] = 0u;
+          }
+        }
+      }
+    }
+
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int t0 = base + u * NW * 16;
+      floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u][s], qb[s], sacc, 0, 0, 0);
+
+      // Scores of rows t0 + 4*blk + r for head col, log2 units.
+      float sc[4];
+      float mx = kNegSentinel;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = t0 + 4 * blk + r;
+        const bool ok = row < r_end && row < lim;
+        sc[r] = ok ? sacc[r] * a.qscale : kNegSentinel;
+        mx = fmaxf(mx, sc[r]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (__ballot(mx > m_run) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float fac = fast_exp2(m_run - m_new);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          acc1[j] *= fac;
+          acc2[j] *= fac;
+        }
+        accl *= fac;
+        m_run = m_new;
+      }
+      half4_t pb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        pb[r] = (_Float16)(sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run) : 0.f);
+
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const uint32_t sel = h ? 0x07060302u : 0x05040100u;  // hi or lo halves, row r in half r%2
+          const half4_t a1 = __builtin_bit_cast(
+              half4_t, make_uint2(__builtin_amdgcn_perm(v1w[u][1][t], v1w[u][0][t], sel),
+                                  __builtin_amdgcn_perm(v1w[u][3][t], v1w[u][2][t], sel)));
+          const half4_t a2 = __builtin_bit_cast(
+              half4_t, make_uint2(__builtin_amdgcn_perm(v2w[u][1][t], v2w[u][0][t], sel),
+                                  __builtin_amdgcn_perm(v2w[u][3][t], v2w[u][2][t], sel)));
+          acc1[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc1[2 * t + h], 0, 0, 0);
+          acc2[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2, pb, acc2[2 * t + h], 0, 0, 0);
+        }
+      }
+      accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pb, accl, 0, 0, 0);
+    }
+  }
+
+  // O^T element (m = 4*blk + r, head col) of MFMA j = 2*t + h is channel
+  // 8*m + j.
+  __shared__ __attribute__((aligned(16))) float lds_o[NW][GC][2 * D + kLdsPad];
+  __shared__ float lds_m[NW][GC];
+  __shared__ float lds_l[NW][GC];
+  if (col < nvh) {
+    // acc[j][r] is channel 8*m + j with m = 4*blk + r: two float4 per row m.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int ch = 8 * (4 * blk + r);
+      *reinterpret_cast<float4*>(&lds_o[wave][col][ch]) =
+          make_float4(acc1[0][r], acc1[1][r], acc1[2][r], acc1[3][r]);
+      *reinterpret_cast<float4*>(&lds_o[wave][col][ch + 4]) =
+          make_float4(acc1[4][r], acc1[5][r], acc1[6][r], acc1[7][r]);
+      *reinterpret_cast<float4*>(&lds_o[wave][col][D + ch]) =
+          make_float4(acc2[0][r], acc2[1][r], acc2[2][r], acc2[3][r]);
+      *reinterpret_cast<float4*>(&lds_o[wave][col][D + ch + 4]) =
+          make_float4(acc2[4][r], acc2[5][r], acc2[6][r], acc2[7][r]);
+    }
+    if (blk == 0) {
+      lds_m[wave][col] = m_run;
+      lds_l[wave][col] = accl[0];
+    }
+  }
+  __syncthreads();
+  wg_epilogue<T, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+}
+
+// fp16 cache, head_dim 128, <= 8 virtual heads per workgroup.
+inline int launch_sdpa_mfma_f16(const SdpaArgs& a, int gc, int waves, int nblocks,
+                                hipStream_t stream) {
+  switch (gc) {
+    case 1:
+      if (waves == 8) {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<1, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<1, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      }
+      break;
+    case 2:
+      if (waves == 8) {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      }
+      break;
+    case 4:
+      if (waves == 8) {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      }
+      break;
+    case 8:
+      hipLaunchKernelGGL((sdpa_mfma_f16_kernel<8, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      break;
+    default:
+      set_error("sdpa_dual_v: no MFMA variant for %d heads per workgroup", gc);
+      return MOTIF_ERR_UNSUPPORTED;
+  }
+  return check_launch("sdpa_dual_v (mfma)");
+}
+
+}  // namespace motif

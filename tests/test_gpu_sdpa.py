@@ -180,3 +180,36 @@ def test_gda_decode_step_cfg1(gpu, rng):
     assert y.shape == (1, 8, 1, 2 * D)
     err = np.abs(torch_to_np(y) - ref)
     assert np.max(err / np.maximum(1.0, np.abs(ref))) <= 2e-3
+
+
+@pytest.fixture
+def valu_only():
+    """Run with the matrix-core kernels switched off (VALU formulation)."""
+    from mlx_motif import _native
+
+    _native.set_tuning("mfma", 0)
+    yield
+    _native.set_tuning("mfma", 1)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,cap,kv_len", [(1, 32, 8, 3328, 3204), (2, 16, 8, 256, 200),
+                                                  (1, 8, 8, 256, 1), (1, 64, 8, 700, 650)])
+def test_valu_formulation_matches_oracle(gpu, rng, valu_only, B, Hq, Hkv, cap, kv_len):
+    err, _, _ = _run(gpu, rng, B, Hq, Hkv, cap, kv_len, 128, "f16", poison=True)
+    assert err <= 2e-3, f"{(B, Hq, Hkv, cap, kv_len)}: {err:.3e}"
+
+
+def test_mfma_and_valu_formulations_agree(gpu, rng):
+    """Same inputs through both formulations (fp16, head_dim 128, GQA 4)."""
+    from mlx_motif import _native
+
+    errs = []
+    for mfma in (1, 0):
+        _native.set_tuning("mfma", mfma)
+        try:
+            errs.append(_run(gpu, np.random.default_rng(5), 1, 32, 8, 4096, 4000, 128, "f16"))
+        finally:
+            _native.set_tuning("mfma", 1)
+    (e1, y1, _), (e0, y0, _) = errs
+    assert e1 <= 2e-3 and e0 <= 2e-3
+    assert np.max(np.abs(torch_to_np(y1) - torch_to_np(y0))) <= 2e-3
