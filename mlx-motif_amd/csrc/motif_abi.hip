@@ -78,7 +78,7 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   int rows = kv_len > 0 ? kv_len : 1;
   int rps;
   if (tuning().rows_per_split > 0) {
-    rps = tuning().rows_per_split;
+    rps = (int)round_up((size_t)tuning().rows_per_split, 16);  // whole 16-row tiles
   } else {
     int nsplit = (min_wgs + units - 1) / units;
     int max_split = (rows + step - 1) / step;  // at least one iteration each

@@ -23,7 +23,7 @@ static bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a)
 // and plan/workspace set-up.
 static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, int B, int Hq,
                        int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal, float scale,
-                       void* ws, size_t ws_bytes) {
+                       void* ws, size_t ws_bytes, int gc_max) {
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "%s: unknown dtype code %d", name, dtype);
   MOTIF_REQUIRE(B >= 1 && Hq >= 1 && Hkv >= 1 && S_q >= 1, "%s: B, H_q, H_kv, S_q must be >= 1",
@@ -33,7 +33,7 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
   MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
                 "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
   MOTIF_REQUIRE((long)B * Hkv * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
-  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D));
+  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, gc_max);
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -75,7 +75,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   SdpaArgs a{};
   SdpaPlan p{};
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes);
+                       ws_bytes, sdpa_gc_max(D));
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
   const int al = sdpa_fp_align(dtype, D);
@@ -115,8 +115,10 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
                 name, gs);
   SdpaArgs a{};
   SdpaPlan p{};
+  // The matrix-core kernel puts (head, scale group) pairs on 16 columns.
+  const int gc_max = (D == 128 && dtype == MOTIF_F16) ? sdpa_gc_max_q(D, gs) : sdpa_gc_max(D);
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes);
+                       ws_bytes, gc_max);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (kd && ks && kb && v1d && v1s && v1b && v2d && v2s &&
                                            v2b)),

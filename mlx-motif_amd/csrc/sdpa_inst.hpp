@@ -5,6 +5,7 @@
 #include "sdpa_dispatch.hpp"
 #include "sdpa_impl.hpp"
 #include "sdpa_mfma.hpp"
+#include "sdpa_mfma_q.hpp"
 
 namespace motif {
 
@@ -36,6 +37,16 @@ int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan
 int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                              int bits, hipStream_t s) {
   const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
+    const int ng = D / a.group_size;
+    const uintptr_t scale_bits = (uintptr_t)a.ks | (uintptr_t)a.kb | (uintptr_t)a.v1s |
+                                 (uintptr_t)a.v1b | (uintptr_t)a.v2s | (uintptr_t)a.v2b;
+    const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;
+    const bool aligned = (data_bits & 15u) == 0 && (scale_bits & (ng == 1 ? 7u : 15u)) == 0 &&
+                         a.kv_cap % 4 == 0 && a.rows_per_split % 16 == 0;
+    if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16)
+      return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
+  }
   if (bits == 4) {
     switch (D) {
       case 32: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 32, 4>>(a, p.gc, p.waves, nblocks, s);

@@ -43,7 +43,8 @@ __device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
 }
 
 template <int GC, int NW, int U>
-__global__ void __launch_bounds__(NW * 64) sdpa_mfma_f16_kernel(SdpaArgs a) {
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+sdpa_mfma_f16_kernel(SdpaArgs a) {
   using T = half_t;
   constexpr int D = 128;
   static_assert(GC <= 16, "virtual heads ride the 16 MFMA columns");

@@ -59,4 +59,13 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
 // Largest head chunk compiled for head dim D (register budget).
 inline int sdpa_gc_max(int D) { return D <= 128 ? 8 : 4; }
 
+// Largest head chunk for the packed cache's matrix-core kernel: heads times
+// scale groups share the 16 MFMA columns.
+inline int sdpa_gc_max_q(int D, int group_size) {
+  const int ng = D / group_size;
+  const int lim = 16 / (ng > 0 ? ng : 1);
+  const int base = sdpa_gc_max(D);
+  return lim < base ? lim : base;
+}
+
 }  // namespace motif

@@ -136,3 +136,69 @@ def test_full_size_16k(gpu, rng, bits):
     """32 q-heads over 8 KV heads, head_dim 128, gs 64, kv_len 16000, cap 16128."""
     err, _, _ = _run(gpu, rng, 1, 32, 8, 16128, 16000, 128, bits, 64, "f16")
     assert err <= 2e-3, f"bits={bits}: {err:.3e}"
+
+
+@pytest.fixture
+def valu_only():
+    """Route the packed cache through the VALU kernel for one test."""
+    from mlx_motif import _native
+
+    _native.set_tuning("mfma", 0)
+    yield
+    _native.set_tuning("mfma", 1)
+
+
+@pytest.fixture
+def tuned_split():
+    from mlx_motif import _native
+
+    yield lambda rows: _native.set_tuning("rows_per_split", rows)
+    _native.set_tuning("rows_per_split", 0)
+
+
+# (Hq, Hkv) pairs that give 1, 2, 4 and 8 heads per workgroup, group sizes
+# that put 1, 2 and 4 scale groups on the matrix-core columns, and lengths
+# with partial 16-row tiles.
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (64, 8), (40, 8)])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("cap,kv_len", [(256, 256), (520, 517), (4096, 3001)])
+def test_head_chunks_groups_and_tails(gpu, rng, Hq, Hkv, gs, bits, cap, kv_len):
+    err, y, _ = _run(gpu, rng, 1, Hq, Hkv, cap, kv_len, 128, bits, gs, "f16", poison=True)
+    assert np.isfinite(torch_to_np(y)).all()
+    assert err <= 2e-3, f"Hq={Hq} Hkv={Hkv} gs={gs} bits={bits} kv_len={kv_len}: {err:.3e}"
+
+
+@pytest.mark.parametrize("rows", [16, 48, 64, 1000])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_forced_splits(gpu, rng, tuned_split, rows, bits):
+    tuned_split(rows)
+    err, _, _ = _run(gpu, rng, 1, 32, 8, 2048, 1999, 128, bits, 64, "f16", poison=True)
+    assert err <= 2e-3, f"rows_per_split={rows} bits={bits}: {err:.3e}"
+
+
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_matrix_core_agrees_with_valu(gpu, gs, bits):
+    """Same inputs through both kernels: both within the oracle bar and
+    within 2e-3 of each other."""
+    from mlx_motif import _native
+
+    errs, ys = [], []
+    for mfma in (1, 0):
+        _native.set_tuning("mfma", mfma)
+        try:
+            err, y, _ = _run(gpu, np.random.default_rng(7), 2, 32, 8, 3000, 2999, 128, bits,
+                             gs, "f16")
+        finally:
+            _native.set_tuning("mfma", 1)
+        errs.append(err)
+        ys.append(torch_to_np(y))
+    assert max(errs) <= 2e-3, errs
+    assert np.max(np.abs(ys[0] - ys[1])) <= 2e-3
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_full_size_16k_valu(gpu, rng, valu_only, bits):
+    err, _, _ = _run(gpu, rng, 1, 32, 8, 16128, 16000, 128, bits, 64, "f16")
+    assert err <= 2e-3, f"bits={bits}: {err:.3e}"
