@@ -207,6 +207,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--extra", action="store_true", help="also time the other workloads")
+    ap.add_argument("--traffic", action="store_true",
+                    help="counter pass: one 256 MiB copy, then eager fp16 decode calls (no "
+                         "timing, no JSON); run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -221,6 +224,8 @@ def main() -> int:
 
     lib = _native.lib()
     dev = torch.device("cuda:0")
+    if args.traffic:
+        return traffic_pass(torch, lib, dev)
     graph = not args.no_graph
     res = {}
     for kind, nsets in (("f16", 8), ("q4", 24), ("q8", 16)):
@@ -253,14 +258,15 @@ def main() -> int:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f16",
         "data": "synthetic: N(0,1) fp16 K/V/q from a fixed seed (random cache, no checkpoint)",
         "config": {
             "workload": "sdpa_dual_v decode on the fp16 4-slot cache: B=1, 32 q-heads over 8 "
                         "KV heads, head_dim 128, kv_len 16000 (cap 16128); q4/q8 at the same "
                         "shape, group_size 64",
             "cache_dtype": "f16", "kv_len": KV_LEN, "kv_cap": CAP, "heads_q": HQ,
-            "heads_kv": HKV, "head_dim": D, "timing": "hip graph replay" if graph else "eager",
+            "heads_kv": HKV, "head_dim": D, "accumulate": "f32",
+            "timing": "hip graph replay" if graph else "eager",
         },
         "gbps": f16["gbps"],
         "pct_peak": f16["pct_peak"],
@@ -277,6 +283,25 @@ def main() -> int:
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
     print(json.dumps(out), flush=True)
+    return 0
+
+
+def traffic_pass(torch, lib, dev) -> int:
+    """Dispatches for the HBM-traffic counters: a plain copy of known size
+    (256 MiB read + 256 MiB written; calibrates FETCH_SIZE / WRITE_SIZE) and
+    16 fp16 decode calls over 8 buffer sets, each 98 MB of algorithmic bytes."""
+    src = torch.empty(128 << 20, dtype=torch.float16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    calls, keep = make_fp16_calls(torch, lib, dev, 8)
+    for i in range(16):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    log(f"traffic pass: copy 268435456 B + 16 decode calls of {alg_bytes('f16')} B")
+    del calls, keep
     return 0
 
 
