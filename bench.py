@@ -207,6 +207,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--extra", action="store_true", help="also time the other workloads")
+    ap.add_argument("--valu", action="store_true",
+                    help="route attention through the VALU kernels (matrix cores off), "
+                         "for comparison")
     ap.add_argument("--traffic", action="store_true",
                     help="counter pass: one 256 MiB copy, then eager fp16 decode calls (no "
                          "timing, no JSON); run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
@@ -226,6 +229,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.traffic:
         return traffic_pass(torch, lib, dev)
+    if args.valu:
+        _native.set_tuning("mfma", 0)
     graph = not args.no_graph
     res = {}
     for kind, nsets in (("f16", 8), ("q4", 24), ("q8", 16)):
@@ -267,6 +272,7 @@ def main() -> int:
             "cache_dtype": "f16", "kv_len": KV_LEN, "kv_cap": CAP, "heads_q": HQ,
             "heads_kv": HKV, "head_dim": D, "accumulate": "f32",
             "timing": "hip graph replay" if graph else "eager",
+            "kernels": "valu" if args.valu else "matrix-core where compiled",
         },
         "gbps": f16["gbps"],
         "pct_peak": f16["pct_peak"],

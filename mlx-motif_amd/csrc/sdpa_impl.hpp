@@ -177,13 +177,6 @@ struct QFmt {
   }
 };
 
-// ------------------------------------------------------- split merge ---
-// Combine the nsplit partials (m, l, o1, o2) of virtual heads qrow0 ..
-// qrow0+nvh-1 and write y.  Every load of a phase is independent of the
-// others so they are in flight together: (m, l) pairs go to LDS, one wave
-// per head turns them into factors exp2(m_s - M) and the total L, then each
-// output float4 is summed over its splits by P threads with 16 loads in
-// flight each, and the P partial sums meet in LDS.
 // Floats of padding per LDS head row: keeps the head rows of the
 // cross-wave staging buffer on different LDS banks.
 constexpr int kLdsPad = 4;
@@ -197,12 +190,13 @@ __device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) 
   Elem<T>::store(a.y, off + 3, z ? v.w : v.w / L);
 }
 
+// ------------------------------------------------------- split merge ---
 // Combine the nsplit partials (m, l, o1, o2) of virtual heads qrow0 ..
-// qrow0+nvh-1 and write y.  One round trip: every thread issues its (m, l)
-// loads (to LDS) and the 16-byte loads of its first UNR partials (to
-// registers) before anything is consumed; one wave per head then turns the
-// maxima into factors exp2(m_s - M) and the total L, and P threads per
-// output float4 sum their splits, meeting in LDS.
+// qrow0+nvh-1 and write y.  One round trip: every thread issues its first
+// (m, l) load and the 16-byte loads of its first UNR partials before
+// anything is consumed; one wave per head then turns the maxima into factors
+// exp2(m_s - M) and the total L, and P threads per output float4 sum their
+// splits, meeting in LDS.
 template <typename T, int D, int GC, int NW>
 __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
   constexpr int NT = NW * 64;
@@ -217,11 +211,8 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
   const auto ro = part_rsrc(a.part_o + qrow0 * ns * 2 * D, (unsigned)(nvh * ns * 2 * D * 4));
   const auto rml = part_rsrc(a.part_ml + qrow0 * ns * 2, (unsigned)(nvh * ns * 2 * 4));
 
-  for (int i = tid; i < nvh * ns; i += NT) {
-    const float2 v = load_through2(rml, (unsigned)i * 8u);
-    lds_f[i / ns][i % ns] = v.x;
-    lds_l[i / ns][i % ns] = v.y;
-  }
+  const int nml = nvh * ns;
+  const float2 ml0 = tid < nml ? load_through2(rml, (unsigned)tid * 8u) : make_float2(0.f, 0.f);
   const int items = nvh * C4;
   const int P = items >= NT ? 1 : NT / items;  // threads per output float4
   const int passes = P > 1 ? 1 : (items + NT - 1) / NT;
@@ -235,6 +226,15 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
     const int s = part + j * P;
     const unsigned off = (unsigned)((((item0 / C4) * ns + s) * 2 * D + (item0 % C4) * 4) * 4);
     pre[j] = (on0 && s < ns) ? load_through4(ro, off) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tid < nml) {
+    lds_f[tid / ns][tid % ns] = ml0.x;
+    lds_l[tid / ns][tid % ns] = ml0.y;
+  }
+  for (int i = tid + NT; i < nml; i += NT) {  // more than NT (head, split) pairs
+    const float2 v = load_through2(rml, (unsigned)i * 8u);
+    lds_f[i / ns][i % ns] = v.x;
+    lds_l[i / ns][i % ns] = v.y;
   }
   __syncthreads();
 

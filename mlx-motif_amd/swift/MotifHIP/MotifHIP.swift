@@ -1,0 +1,139 @@
+// Swift face of the MI355X decode-attention library (libmotif_hip.so) over
+// the CMotifHIP clang module.  It mirrors the entry points of the reference's
+// Swift kernel layer (swift/Sources/MotifKitMLX/MotifMetalKernels.swift:
+// MotifSDPADualV.apply 544-600, MotifSDPADualVQ4.apply 726-810,
+// MotifGDAPostSplit.apply 930-1008, MotifPolynorm.apply 1147-1196) with raw
+// device pointers in place of MLXArray: the caller owns the HIP buffers and
+// the stream.  A non-OK status is returned, never thrown, so a caller keeps
+// the reference's convention of falling back to its reference path and
+// counting the fallback (MotifMetalKernels.swift:562-593).
+
+import CMotifHIP
+
+public enum MotifHIPStatus: Int32 {
+    case ok = 0
+    case contract = -1
+    case unsupported = -2
+    case workspace = -3
+    case hip = -4
+}
+
+public enum MotifHIPDType: Int32 {
+    case float16 = 0
+    case bfloat16 = 1
+    case float32 = 2
+}
+
+/// One packed MLX-affine triple (data uint32, scales, biases) in device memory.
+public struct MotifHIPQuantizedTriple {
+    public var data: UnsafeMutablePointer<UInt32>
+    public var scales: UnsafeMutableRawPointer
+    public var biases: UnsafeMutableRawPointer
+    public init(data: UnsafeMutablePointer<UInt32>, scales: UnsafeMutableRawPointer,
+                biases: UnsafeMutableRawPointer) {
+        self.data = data
+        self.scales = scales
+        self.biases = biases
+    }
+}
+
+public enum MotifHIP {
+    /// Message of the last non-OK status on this thread.
+    public static var lastError: String { String(cString: motif_last_error()) }
+
+    /// Workspace bytes the split-KV attention calls need (counters first; the
+    /// caller zeroes the buffer once).
+    public static func workspaceBytes(batch: Int, queryHeads: Int, kvHeads: Int,
+                                      queryRows: Int = 1, kvLen: Int, headDim: Int) -> Int {
+        Int(motif_sdpa_workspace_bytes(Int32(batch), Int32(queryHeads), Int32(kvHeads),
+                                       Int32(queryRows), Int32(kvLen), Int32(headDim)))
+    }
+
+    /// y (B, Hq, 1, 2D) = [softmax(scale q K^T) V1 || softmax(scale q K^T) V2]
+    /// over rows [0, kvLen) of full-capacity (B, Hkv, cap, D) buffers.
+    public static func sdpaDualV(
+        queries: UnsafeRawPointer, keys: UnsafeRawPointer, value1: UnsafeRawPointer,
+        value2: UnsafeRawPointer, output: UnsafeMutableRawPointer, dtype: MotifHIPDType,
+        batch: Int, queryHeads: Int, kvHeads: Int, headDim: Int, kvCapacity: Int, kvLen: Int,
+        scale: Float, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_sdpa_dual_v(queries, keys, value1, value2, output, dtype.rawValue,
+                                   Int32(batch), Int32(queryHeads), Int32(kvHeads),
+                                   Int32(headDim), Int32(kvCapacity), Int32(kvLen), scale,
+                                   workspace, workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// Same over the packed q4/q8 cache, read directly.
+    public static func sdpaDualVQuantized(
+        queries: UnsafeRawPointer, keys: MotifHIPQuantizedTriple,
+        value1: MotifHIPQuantizedTriple, value2: MotifHIPQuantizedTriple,
+        output: UnsafeMutableRawPointer, dtype: MotifHIPDType, batch: Int, queryHeads: Int,
+        kvHeads: Int, headDim: Int, kvCapacity: Int, kvLen: Int, bits: Int, groupSize: Int,
+        scale: Float, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_sdpa_dual_v_q(queries, keys.data, keys.scales, keys.biases,
+                                     value1.data, value1.scales, value1.biases,
+                                     value2.data, value2.scales, value2.biases,
+                                     output, dtype.rawValue, Int32(batch), Int32(queryHeads),
+                                     Int32(kvHeads), Int32(headDim), Int32(kvCapacity),
+                                     Int32(kvLen), Int32(bits), Int32(groupSize), scale,
+                                     workspace, workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// Quantise S new rows of the four slots into rows [offset, offset+S) of
+    /// the cache triples (k1, k2, v1, v2) in one dispatch.
+    public static func quantizedWrite4(
+        k1: UnsafeRawPointer, k2: UnsafeRawPointer, v1: UnsafeRawPointer,
+        v2: UnsafeRawPointer, slots: [MotifHIPQuantizedTriple], dtype: MotifHIPDType,
+        batch: Int, heads: Int, rows: Int, headDim: Int, kvCapacity: Int, offset: Int,
+        bits: Int, groupSize: Int, stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        guard slots.count == 4 else { return .contract }
+        var data: [UnsafeMutablePointer<UInt32>?] = slots.map { $0.data }
+        var scales: [UnsafeMutableRawPointer?] = slots.map { $0.scales }
+        var biases: [UnsafeMutableRawPointer?] = slots.map { $0.biases }
+        let rc = data.withUnsafeMutableBufferPointer { d in
+            scales.withUnsafeMutableBufferPointer { s in
+                biases.withUnsafeMutableBufferPointer { b in
+                    motif_quant_write4(k1, k2, v1, v2, d.baseAddress, s.baseAddress,
+                                       b.baseAddress, dtype.rawValue, Int32(batch),
+                                       Int32(heads), Int32(rows), Int32(headDim),
+                                       Int32(kvCapacity), Int32(offset), Int32(bits),
+                                       Int32(groupSize), stream)
+                }
+            }
+        }
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// y = RMSNorm(o - lambda * n[h / gr]) * w * (1 - lambda_init); lambdaFull
+    /// is a device pointer to one fp32 value.
+    public static func gdaPostSplit(
+        attnO: UnsafeRawPointer, attnN: UnsafeRawPointer, sublnWeight: UnsafeRawPointer,
+        output: UnsafeMutableRawPointer, dtype: MotifHIPDType, batch: Int, qOrigin: Int,
+        qGroups: Int, gr: Int, rows: Int, channels: Int,
+        lambdaFull: UnsafePointer<Float>, oneMinusLambdaInit: Float, eps: Float,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_post_split(attnO, attnN, sublnWeight, output, dtype.rawValue,
+                                      Int32(batch), Int32(qOrigin), Int32(qGroups), Int32(gr),
+                                      Int32(rows), Int32(channels), lambdaFull,
+                                      oneMinusLambdaInit, eps, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// PolyNorm over the last axis of x (rows, D).
+    public static func polynorm(
+        x: UnsafeRawPointer, weight: UnsafeRawPointer, bias: UnsafeRawPointer,
+        output: UnsafeMutableRawPointer, dtype: MotifHIPDType, rows: Int, dim: Int, eps: Float,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_polynorm(x, weight, bias, output, dtype.rawValue, Int64(rows),
+                                Int32(dim), eps, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+}
