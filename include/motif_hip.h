@@ -11,7 +11,8 @@
  *    device; tensors are dense row-major ("row-contiguous") in the shapes
  *    given per function.
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
- *    Calls only enqueue work; they never synchronise the stream.
+ *    Calls only enqueue work; they never synchronise the stream.  A split-KV
+ *    attention call enqueues two kernels (attention, then the split merge).
  *  - Return value: MOTIF_OK, or a negative status.  motif_last_error() then
  *    returns a message (thread-local, valid until the next call on the same
  *    thread).  Contract checks run before any HIP call, so a rejected call
@@ -188,7 +189,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * Tuning knobs of the split-KV kernels (process-wide; for benchmarks and
  * sweeps, not needed for correct use).  key: "rows_per_split",
  * "waves_per_wg", "min_wgs" (value 0 restores the default), "mfma" (1, the
- * default: matrix-core kernels where compiled; 0: VALU kernels only).
+ * default: matrix-core kernels where compiled; 0: VALU kernels only),
+ * "fused_merge" (0, the default: a second launch combines the splits; 1: the
+ * last workgroup to finish combines them inside the attention launch).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.
  * ------------------------------------------------------------------------ */
 int motif_set_tuning(const char* key, int value);

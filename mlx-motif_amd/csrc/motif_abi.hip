@@ -146,11 +146,17 @@ int motif_set_tuning(const char* key, int value) {
   } else if (!strcmp(key, "min_wgs")) {
     tuning().min_wgs = value;
   } else if (!strcmp(key, "mfma")) {
-    if (value > 1) {
+    if (value != 0 && value != 1) {
       set_error("motif_set_tuning: mfma must be 0 or 1");
       return MOTIF_ERR_CONTRACT;
     }
     tuning().mfma = value;
+  } else if (!strcmp(key, "fused_merge")) {
+    if (value != 0 && value != 1) {
+      set_error("motif_set_tuning: fused_merge must be 0 or 1");
+      return MOTIF_ERR_CONTRACT;
+    }
+    tuning().fused_merge = value;
   } else {
     set_error("motif_set_tuning: unknown key '%s'", key);
     return MOTIF_ERR_CONTRACT;

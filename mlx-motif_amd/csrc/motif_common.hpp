@@ -36,6 +36,7 @@ struct Tuning {
   int waves_per_wg = 0;    // 0 = automatic
   int min_wgs = 0;         // 0 = automatic
   int mfma = 1;            // 1 = matrix-core kernels where compiled, 0 = VALU kernels
+  int fused_merge = 0;     // 1 = last-arriving workgroup merges splits, 0 = merge kernel
 };
 Tuning& tuning();
 
@@ -128,6 +129,44 @@ __device__ inline void load_words(uint32_t (&dst)[NW], const uint32_t* src) {
   } else {
 #pragma unroll
     for (int i = 0; i < NW; ++i) dst[i] = src[i];
+  }
+}
+
+// Streaming loads for data read once per call (the KV cache): the
+// nontemporal hint keeps these lines from displacing reusable ones.  On the
+// 16k decode it saves about 1.5 us per call against plain loads.
+typedef unsigned u32x4_nt_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_nt_t __attribute__((ext_vector_type(2)));
+__device__ inline uint4 ld_stream4(const void* p) {
+  const u32x4_nt_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline uint2 ld_stream2(const void* p) {
+  const u32x2_nt_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_nt_t*>(p));
+  return make_uint2(v.x, v.y);
+}
+__device__ inline uint32_t ld_stream1(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
+// load_words with streaming loads.
+template <int NW>
+__device__ inline void load_words_stream(uint32_t (&dst)[NW], const uint32_t* src) {
+  if constexpr (NW % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW; i += 4) {
+      const uint4 v = ld_stream4(src + i);
+      dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+    }
+  } else if constexpr (NW % 2 == 0) {
+#pragma unroll
+    for (int i = 0; i < NW; i += 2) {
+      const uint2 v = ld_stream2(src + i);
+      dst[i] = v.x; dst[i + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NW; ++i) dst[i] = ld_stream1(src + i);
   }
 }
 

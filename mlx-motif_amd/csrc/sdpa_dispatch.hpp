@@ -19,6 +19,12 @@ int dispatch_sdpa_q_f16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, h
 int dispatch_sdpa_q_bf16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 
+// Split merge (second launch when a.fused_merge == 0 and nsplit > 1) for
+// outputs of the given element type.
+int launch_sdpa_merge_f16(const SdpaArgs& a, int D, hipStream_t s);
+int launch_sdpa_merge_bf16(const SdpaArgs& a, int D, hipStream_t s);
+int launch_sdpa_merge_f32(const SdpaArgs& a, int D, hipStream_t s);
+
 // Pointer alignment (bytes) the kernels need for head dim D.
 int sdpa_fp_align(int dtype, int D);
 int sdpa_q_align(int D, int bits);

@@ -46,6 +46,7 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
   a.causal = causal ? 1 : 0;
   a.nsplit = p.nsplit;
   a.rows_per_split = p.rows_per_split;
+  a.fused_merge = tuning().fused_merge;
   a.qscale = scale * 1.4426950408889634f;  // log2(e): the kernels use exp2
   a.part_o = nullptr;
   a.part_ml = nullptr;
@@ -65,6 +66,16 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
     a.part_ml = (float*)(w + p.counter_bytes + o_bytes);
   }
   return MOTIF_OK;
+}
+
+// Second launch of a split call: combine the partials into y.
+static int sdpa_merge(const SdpaArgs& a, int dtype, int D, hipStream_t s) {
+  if (a.nsplit == 1 || a.fused_merge) return MOTIF_OK;
+  switch (dtype) {
+    case MOTIF_F16: return launch_sdpa_merge_f16(a, D, s);
+    case MOTIF_BF16: return launch_sdpa_merge_bf16(a, D, s);
+    default: return launch_sdpa_merge_f32(a, D, s);
+  }
 }
 
 static int sdpa_fp_run(const char* name, const void* q, const void* k, const void* v1,
@@ -88,10 +99,11 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   a.y = y;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case MOTIF_F16: return dispatch_sdpa_fp_f16(a, p, D, s);
-    case MOTIF_BF16: return dispatch_sdpa_fp_bf16(a, p, D, s);
-    default: return dispatch_sdpa_fp_f32(a, p, D, s);
+    case MOTIF_F16: rc = dispatch_sdpa_fp_f16(a, p, D, s); break;
+    case MOTIF_BF16: rc = dispatch_sdpa_fp_bf16(a, p, D, s); break;
+    default: rc = dispatch_sdpa_fp_f32(a, p, D, s); break;
   }
+  return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
 }
 
 static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const void* ks,
@@ -134,10 +146,11 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   a.group_size = gs;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case MOTIF_F16: return dispatch_sdpa_q_f16(a, p, D, bits, s);
-    case MOTIF_BF16: return dispatch_sdpa_q_bf16(a, p, D, bits, s);
-    default: return dispatch_sdpa_q_f32(a, p, D, bits, s);
+    case MOTIF_F16: rc = dispatch_sdpa_q_f16(a, p, D, bits, s); break;
+    case MOTIF_BF16: rc = dispatch_sdpa_q_bf16(a, p, D, bits, s); break;
+    default: rc = dispatch_sdpa_q_f32(a, p, D, bits, s); break;
   }
+  return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
 }
 
 }  // namespace motif

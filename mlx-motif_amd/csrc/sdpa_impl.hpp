@@ -11,9 +11,10 @@
 //   rows keeping an online softmax (running max m, sum l, two accumulators)
 //   per virtual head in log2 units.
 // Merges: row groups of a wave (lane shuffles), waves of a workgroup (LDS),
-// then splits: every workgroup writes (m, l, o1, o2) to the workspace and the
-// last one to arrive for its (b, KV head, chunk) combines all splits and
-// writes y, then re-arms the arrival counter.
+// then splits: every workgroup writes (m, l, o1, o2) to the workspace, and
+// either sdpa_merge_kernel (a second launch, the default) or the last
+// workgroup to arrive for its (b, KV head, chunk) combines all splits and
+// writes y; the in-kernel merge re-arms its arrival counter.
 //
 // Reference semantics (src/mlx_motif/kernels/attention.py:53-166, 293-445):
 // q scaled once in fp32, fp32 accumulation, running-max sentinel -1e30,
@@ -97,9 +98,9 @@ struct FpFmt {
   }
   __device__ inline void load(int row, Frag& kf, Frag& v1f, Frag& v2f) const {
     long o = (long)row * WPR;
-    load_words<WPL>(kf.w, k + o);
-    load_words<WPL>(v1f.w, v1 + o);
-    load_words<WPL>(v2f.w, v2 + o);
+    load_words_stream<WPL>(kf.w, k + o);
+    load_words_stream<WPL>(v1f.w, v1 + o);
+    load_words_stream<WPL>(v2f.w, v2 + o);
   }
   __device__ static inline void zero(Frag& f) {
 #pragma unroll
@@ -153,9 +154,9 @@ struct QFmt {
   }
   __device__ inline void load(int row, Frag& kf, Frag& v1f, Frag& v2f) const {
     long o = (long)row * WPR;
-    load_words<WPL>(kf.w, kd + o);
-    load_words<WPL>(v1f.w, v1d + o);
-    load_words<WPL>(v2f.w, v2d + o);
+    load_words_stream<WPL>(kf.w, kd + o);
+    load_words_stream<WPL>(v1f.w, v1d + o);
+    load_words_stream<WPL>(v2f.w, v2d + o);
     long si = sbase + (long)row * ngroups;
     kf.s = Elem<T>::load(ks, si);   kf.b = Elem<T>::load(kb, si);
     v1f.s = Elem<T>::load(v1s, si); v1f.b = Elem<T>::load(v1b, si);
@@ -347,7 +348,7 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
       if (c == 0) store_through2(rml, (unsigned)((g * ns + split) * 8), make_float2(M, L));
     }
   }
-  if (single) return;
+  if (single || !a.fused_merge) return;  // sdpa_merge_kernel combines the splits
 
   // ---- last workgroup of this (b, KV head, chunk) combines all splits.
   __shared__ int is_last;
@@ -363,6 +364,105 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
   __syncthreads();
   if (!is_last) return;
   merge_splits<T, D, GC, NW>(a, qrow0, nvh);
+}
+
+// ------------------------------------------------------- merge kernel ---
+// Second launch of a split call: combines the nsplit partials of every
+// virtual-head row.  A workgroup of 256 threads owns one row and a slice of
+// CW float4 output columns; thread (column, group) sums the splits
+// group, group + NG, ...  All partial loads of the first batch and the
+// row's (m, l) pairs are issued before any is consumed.  The kernel boundary
+// makes the main kernel's partials visible, so plain loads suffice.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) sdpa_merge_kernel(SdpaArgs a) {
+  constexpr int C4 = 2 * D / 4;          // float4 columns of one output row
+  constexpr int CW = C4 < 16 ? C4 : 16;  // columns per workgroup
+  constexpr int NSL = C4 / CW;           // workgroups per row
+  constexpr int NG = 256 / CW;           // split groups
+  constexpr int UNR = 4;                 // loads in flight per thread
+  __shared__ float lds_m[kMaxSplits];
+  __shared__ float lds_l[kMaxSplits];
+  __shared__ float lds_ML[2];
+  __shared__ __attribute__((aligned(16))) float4 lds_acc[256];
+  const int tid = threadIdx.x;
+  const long vrow = blockIdx.x / NSL;
+  const int col = (blockIdx.x % NSL) * CW + tid % CW;
+  const int grp = tid / CW;
+  const int ns = a.nsplit;
+  const float* po = a.part_o + vrow * ns * 2 * D + col * 4;
+  const float* pml = a.part_ml + vrow * ns * 2;
+
+  const float2 ml = tid < ns ? *reinterpret_cast<const float2*>(pml + 2 * tid)
+                             : make_float2(kNegSentinel, 0.f);
+  float4 v[UNR];
+#pragma unroll
+  for (int j = 0; j < UNR; ++j) {
+    const int s = grp + j * NG;
+    v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  if (tid < ns) {
+    lds_m[tid] = ml.x;
+    lds_l[tid] = ml.y;
+  }
+  __syncthreads();
+  if (tid < 64) {  // wave 0: row max M and total L = sum_s l_s exp2(m_s - M)
+    float M = kNegSentinel;
+    for (int s = tid; s < ns; s += 64) M = fmaxf(M, lds_m[s]);
+    M = group_max<64>(M);
+    float L = 0.f;
+    for (int s = tid; s < ns; s += 64) L = fmaf(lds_l[s], fast_exp2(lds_m[s] - M), L);
+    L = group_sum<64>(L);
+    if (tid == 0) {
+      lds_ML[0] = M;
+      lds_ML[1] = L;
+    }
+  }
+  __syncthreads();
+  const float M = lds_ML[0];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += NG * UNR) {
+    if (s0 > 0) {
+#pragma unroll
+      for (int j = 0; j < UNR; ++j) {
+        const int s = s0 + grp + j * NG;
+        v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const int s = s0 + grp + j * NG;
+      const float f = s < ns ? fast_exp2(lds_m[s] - M) : 0.f;
+      acc.x = fmaf(v[j].x, f, acc.x);
+      acc.y = fmaf(v[j].y, f, acc.y);
+      acc.z = fmaf(v[j].z, f, acc.z);
+      acc.w = fmaf(v[j].w, f, acc.w);
+    }
+  }
+  lds_acc[tid] = acc;
+  __syncthreads();
+  if (tid < CW) {
+    float4 t = lds_acc[tid];
+#pragma unroll
+    for (int g = 1; g < NG; ++g) {
+      const float4 u = lds_acc[g * CW + tid];
+      t.x += u.x;
+      t.y += u.y;
+      t.z += u.z;
+      t.w += u.w;
+    }
+    store_y4<T, D>(a, vrow * 2 * D + col * 4, t, lds_ML[1]);
+  }
+}
+
+template <typename T, int D>
+int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
+  constexpr int C4 = 2 * D / 4;
+  constexpr int NSL = C4 / (C4 < 16 ? C4 : 16);
+  const long rows = (long)a.B * a.Hq * a.S_q;
+  hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3((unsigned)(rows * NSL)), dim3(256), 0, s, a);
+  return check_launch("sdpa split merge");
 }
 
 // ---------------------------------------------------------------- kernel --

@@ -34,6 +34,22 @@ int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan
   return MOTIF_ERR_UNSUPPORTED;
 }
 
+int MOTIF_CAT(launch_sdpa_merge_, MOTIF_SUFFIX)(const SdpaArgs& a, int D, hipStream_t s) {
+  switch (D) {
+    case 32: return launch_sdpa_merge_d<MOTIF_ELEM, 32>(a, s);
+    case 64: return launch_sdpa_merge_d<MOTIF_ELEM, 64>(a, s);
+    case 96: return launch_sdpa_merge_d<MOTIF_ELEM, 96>(a, s);
+    case 128: return launch_sdpa_merge_d<MOTIF_ELEM, 128>(a, s);
+    case 160: return launch_sdpa_merge_d<MOTIF_ELEM, 160>(a, s);
+    case 192: return launch_sdpa_merge_d<MOTIF_ELEM, 192>(a, s);
+    case 224: return launch_sdpa_merge_d<MOTIF_ELEM, 224>(a, s);
+    case 256: return launch_sdpa_merge_d<MOTIF_ELEM, 256>(a, s);
+    default: break;
+  }
+  set_error("sdpa split merge: head dim D=%d has no compiled variant", D);
+  return MOTIF_ERR_UNSUPPORTED;
+}
+
 int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                              int bits, hipStream_t s) {
   const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;

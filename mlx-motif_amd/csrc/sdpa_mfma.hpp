@@ -111,7 +111,7 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
         const uint16_t* kp = kbase + (long)krow * D + 8 * blk;
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          ka[u][s] = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4*>(kp + 32 * s));
+          ka[u][s] = __builtin_bit_cast(half8_t, ld_stream4(kp + 32 * s));
       } else {
 #pragma unroll
         for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, make_uint4(0, 0, 0, 0));
@@ -123,8 +123,8 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int row = t0 + 4 * blk + r;
         if (row < r_end) {
-          const uint4 w1 = *reinterpret_cast<const uint4*>(v1base + (long)row * (D / 2) + 4 * col);
-          const uint4 w2 = *reinterpret_cast<const uint4*>(v2base + (long)row * (D / 2) + 4 * col);
+          const uint4 w1 = ld_stream4(v1base + (long)row * (D / 2) + 4 * col);
+          const uint4 w2 = ld_stream4(v2base + (long)row * (D / 2) + 4 * col);
           v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
           v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
         } else {

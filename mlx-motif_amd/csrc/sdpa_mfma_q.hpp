@@ -125,15 +125,15 @@ struct LaneScales {
     uint32_t w[2 * NG];
     if (full) {
       if constexpr (NG == 4) {
-        const uint4 x = *reinterpret_cast<const uint4*>(p);
-        const uint4 y = *reinterpret_cast<const uint4*>(p + 8);
+        const uint4 x = ld_stream4(p);
+        const uint4 y = ld_stream4(p + 8);
         w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
         w[4] = y.x; w[5] = y.y; w[6] = y.z; w[7] = y.w;
       } else if constexpr (NG == 2) {
-        const uint4 x = *reinterpret_cast<const uint4*>(p);
+        const uint4 x = ld_stream4(p);
         w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
       } else {
-        const uint2 x = *reinterpret_cast<const uint2*>(p);
+        const uint2 x = ld_stream2(p);
         w[0] = x.x; w[1] = x.y;
       }
     } else {
@@ -249,7 +249,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       const int t0 = base + u * NW * 16;
       const int krow = t0 + col;
       if (krow < r_end) {
-        load_words<KW>(kw[u], kd + (long)krow * WPR + KW * blk);
+        load_words_stream<KW>(kw[u], kd + (long)krow * WPR + KW * blk);
       } else {
 #pragma unroll
         for (int i = 0; i < KW; ++i) kw[u][i] = 0u;
@@ -259,8 +259,8 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int row = row0 + r;
         if (row < r_end) {
-          load_words<VW>(v1w[u][r], v1d + (long)row * WPR + VW * col);
-          load_words<VW>(v2w[u][r], v2d + (long)row * WPR + VW * col);
+          load_words_stream<VW>(v1w[u][r], v1d + (long)row * WPR + VW * col);
+          load_words_stream<VW>(v2w[u][r], v2d + (long)row * WPR + VW * col);
         } else {
 #pragma unroll
           for (int i = 0; i < VW; ++i) { v1w[u][r][i] = 0u; v2w[u][r][i] = 0u; }

@@ -36,7 +36,8 @@ struct SdpaArgs {
   int kv_cap, kv_len, causal;
   int nsplit, rows_per_split;
   int group_size;
-  float qscale;  // softmax scale * log2(e)
+  int fused_merge;  // 1: last-arriving workgroup merges; 0: sdpa_merge_kernel does
+  float qscale;     // softmax scale * log2(e)
 };
 
 struct SdpaPlan {

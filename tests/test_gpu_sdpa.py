@@ -114,23 +114,49 @@ def test_v1_equals_v2_gives_identical_halves(gpu, rng):
     assert np.array_equal(y[..., :128], y[..., 128:])
 
 
+@pytest.fixture(params=[0, 1], ids=["merge_kernel", "fused_merge"])
+def merge_mode(request):
+    """Both ways of combining splits: the second launch (default) and the
+    last-arriving workgroup inside the attention launch."""
+    from mlx_motif import _native
+
+    _native.set_tuning("fused_merge", request.param)
+    yield request.param
+    _native.set_tuning("fused_merge", 0)
+
+
 @pytest.mark.parametrize("rows_per_split", [16, 64, 208])
-def test_forced_split_merges(gpu, rng, rows_per_split):
-    """Many splits per KV head exercise the last-arriving-workgroup merge."""
+def test_forced_split_merges(gpu, rng, merge_mode, rows_per_split):
+    """Many splits per KV head (up to 201) exercise the split merge."""
     from mlx_motif import _native
 
     _native.set_tuning("rows_per_split", rows_per_split)
     try:
         err, _, _ = _run(gpu, rng, 2, 32, 8, 3328, 3204, 128, "f16")
         err2, _, _ = _run(gpu, rng, 1, 8, 8, 1024, 1000, 64, "bf16")
+        err3, _, _ = _run(gpu, rng, 1, 4, 2, 700, 650, 256, "f32")
     finally:
         _native.set_tuning("rows_per_split", 0)
-    assert err <= 2e-3 and err2 <= 1e-2, (err, err2)
+    assert err <= 2e-3 and err2 <= 1e-2 and err3 <= 1e-5, (err, err2, err3)
 
 
-def test_repeated_calls_rearm_counters(gpu, rng):
-    """Back-to-back multi-split calls on one workspace stay correct (the last
-    workgroup of each call re-arms the arrival counters)."""
+def test_merge_kernel_and_fused_merge_agree(gpu):
+    from mlx_motif import _native
+
+    ys = []
+    for fused in (0, 1):
+        _native.set_tuning("fused_merge", fused)
+        try:
+            _, y, _ = _run(gpu, np.random.default_rng(3), 1, 32, 8, 16128, 16000, 128, "f16")
+        finally:
+            _native.set_tuning("fused_merge", 0)
+        ys.append(torch_to_np(y).astype(np.float32))
+    assert np.max(np.abs(ys[0] - ys[1])) <= 1e-3
+
+
+def test_repeated_calls_rearm_counters(gpu, rng, merge_mode):
+    """Back-to-back multi-split calls on one workspace stay correct (with the
+    fused merge, the last workgroup of each call re-arms the counters)."""
     import torch
 
     from mlx_motif.kernels import sdpa_dual_v

@@ -169,11 +169,18 @@ def test_head_chunks_groups_and_tails(gpu, rng, Hq, Hkv, gs, bits, cap, kv_len):
     assert err <= 2e-3, f"Hq={Hq} Hkv={Hkv} gs={gs} bits={bits} kv_len={kv_len}: {err:.3e}"
 
 
+@pytest.mark.parametrize("fused", [0, 1], ids=["merge_kernel", "fused_merge"])
 @pytest.mark.parametrize("rows", [16, 48, 64, 1000])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_forced_splits(gpu, rng, tuned_split, rows, bits):
+def test_forced_splits(gpu, rng, tuned_split, rows, bits, fused):
+    from mlx_motif import _native
+
+    _native.set_tuning("fused_merge", fused)
     tuned_split(rows)
-    err, _, _ = _run(gpu, rng, 1, 32, 8, 2048, 1999, 128, bits, 64, "f16", poison=True)
+    try:
+        err, _, _ = _run(gpu, rng, 1, 32, 8, 2048, 1999, 128, bits, 64, "f16", poison=True)
+    finally:
+        _native.set_tuning("fused_merge", 0)
     assert err <= 2e-3, f"rows_per_split={rows} bits={bits}: {err:.3e}"
 
 
