@@ -44,14 +44,24 @@ __device__ inline half2_t sub1024_hi(uint32_t x) {
 }
 __device__ inline uint32_t h2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
+// The fp16 exponent pattern 0x6400 in both halves, held in a VGPR: with the
+// mask as the one scalar operand, (x & mask) | magic is a single v_and_or_b32
+// (gfx9 VOP3 instructions take at most one scalar or literal operand, so
+// with both constants as literals the compiler emits an and plus an or).
+__device__ inline uint32_t magic_vgpr() {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(0x64006400u));
+  return v;
+}
+
 // 8 channels of one q4 word as exact fp16 codes, in the order
 // [0, 4, 1, 5, 2, 6, 3, 7] (q4_order): k-operand order of the K fragments.
-__device__ inline half8_t q4_word_codes(uint32_t w) {
+__device__ inline half8_t q4_word_codes(uint32_t w, uint32_t magic) {
   const uint32_t w8 = w >> 8;
-  const half2_t y0 = sub1024((w & 0x000F000Fu) | 0x64006400u);
-  const half2_t y1 = sub1024_hi((w & 0x00F000F0u) | 0x64006400u);
-  const half2_t y2 = sub1024((w8 & 0x000F000Fu) | 0x64006400u);
-  const half2_t y3 = sub1024_hi((w8 & 0x00F000F0u) | 0x64006400u);
+  const half2_t y0 = sub1024((w & 0x000F000Fu) | magic);
+  const half2_t y1 = sub1024_hi((w & 0x00F000F0u) | magic);
+  const half2_t y2 = sub1024((w8 & 0x000F000Fu) | magic);
+  const half2_t y3 = sub1024_hi((w8 & 0x00F000F0u) | magic);
   return half8_t{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 __host__ __device__ constexpr int q4_order(int j) { return (j & 1) ? 4 + (j >> 1) : (j >> 1); }
@@ -74,23 +84,23 @@ __device__ inline uint32_t pair_bytes(uint32_t a, uint32_t b, int k) {
 
 // V^T fragment: code i of the lane's word in rows r0..r3, as exact fp16.
 template <int BITS>
-__device__ inline half4_t v_codes(const uint32_t (&w)[4], int i) {
+__device__ inline half4_t v_codes(const uint32_t (&w)[4], int i, uint32_t magic) {
   if constexpr (BITS == 4) {
     const int k = i >> 1;
     const uint32_t x01 = pair_bytes(w[0], w[1], k);
     const uint32_t x23 = pair_bytes(w[2], w[3], k);
     half2_t lo, hi;
     if (i & 1) {
-      lo = sub1024_hi((x01 & 0x00F000F0u) | 0x64006400u);
-      hi = sub1024_hi((x23 & 0x00F000F0u) | 0x64006400u);
+      lo = sub1024_hi((x01 & 0x00F000F0u) | magic);
+      hi = sub1024_hi((x23 & 0x00F000F0u) | magic);
     } else {
-      lo = sub1024((x01 & 0x000F000Fu) | 0x64006400u);
-      hi = sub1024((x23 & 0x000F000Fu) | 0x64006400u);
+      lo = sub1024((x01 & 0x000F000Fu) | magic);
+      hi = sub1024((x23 & 0x000F000Fu) | magic);
     }
     return half4_t{lo.x, lo.y, hi.x, hi.y};
   } else {
-    const half2_t lo = sub1024(pair_bytes(w[0], w[1], i) | 0x64006400u);
-    const half2_t hi = sub1024(pair_bytes(w[2], w[3], i) | 0x64006400u);
+    const half2_t lo = sub1024(pair_bytes(w[0], w[1], i) | magic);
+    const half2_t hi = sub1024(pair_bytes(w[2], w[3], i) | magic);
     return half4_t{lo.x, lo.y, hi.x, hi.y};
   }
 }
@@ -112,63 +122,104 @@ __device__ inline float sum_group_columns(float x) {
   return x;
 }
 
-// fp16 scale/bias of rows row0..row0+3 (row0 % 4 == 0) for the lane's group
-// gsel, NG groups per row.  The 4*NG halves of the four rows are contiguous
-// (8, 16 or 32 bytes) and read with one or two vector loads; the lane's group
-// is then picked with compile-time indexes only (selects, no dynamic register
-// indexing).
+// ------------------------------------------------------------ loads ---
+// Per-split buffer resources: base at the split's first row, range = its
+// rows, so loads past the split's end return 0 with no memory traffic and
+// need no branch.  Cache policy nt: the cache is read once per call.
+constexpr int kCachePolicyStream = 2;  // nt
+
+__device__ inline __amdgpu_buffer_rsrc_t stream_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ inline uint4 bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(uint4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCachePolicyStream));
+}
+__device__ inline uint2 bload2(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(uint2,
+                            __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyStream));
+}
+__device__ inline uint32_t bload1(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCachePolicyStream);
+}
+
+// One 16-row tile of the packed cache as one lane loads it.
+//   k[KW]      K codes of row t0 + col, channels 32*blk .. 32*blk+31
+//   v1/v2[4][] V codes of rows t0 + 4*blk + r, channels 8*col .. 8*col+7
+//   s[6][SW]   raw fp16 (scale, bias) words of K, V1, V2 for rows
+//              t0 + 4*blk .. +3 that hold the lane's scale group
+// Nothing is consumed at load time, so all loads of a tile are in flight
+// together; scale_words() extracts the lane's halves when it is computed.
+template <int BITS, int NG>
+struct QTile {
+  static constexpr int WPR = 128 * BITS / 32;
+  static constexpr int KW = WPR / 4;
+  static constexpr int VW = WPR / 16;
+  static constexpr int SW = NG == 1 ? 2 : 4;
+  uint32_t k[KW];
+  uint32_t v1[4][VW];
+  uint32_t v2[4][VW];
+  uint32_t s[6][SW];
+};
+
+// Raw scale / bias words of one tensor for rows row0 .. row0+3 (NG groups of
+// fp16 per row).  NG = 1: the four halves, one 8-byte load; NG = 2: two
+// 8-byte loads of two rows each; NG = 4: one 4-byte load per row holding
+// groups (gsel & ~1, gsel | 1).  The resource covers whole 4-row groups, so
+// no load straddles its end.
 template <int NG>
-struct LaneScales {
-  float v[4];
-  __device__ inline void load(const uint16_t* base, long row0, bool full, int r_end, int gsel) {
-    const uint16_t* p = base + row0 * NG;
-    uint32_t w[2 * NG];
-    if (full) {
-      if constexpr (NG == 4) {
-        const uint4 x = ld_stream4(p);
-        const uint4 y = ld_stream4(p + 8);
-        w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
-        w[4] = y.x; w[5] = y.y; w[6] = y.z; w[7] = y.w;
-      } else if constexpr (NG == 2) {
-        const uint4 x = ld_stream4(p);
-        w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
-      } else {
-        const uint2 x = ld_stream2(p);
-        w[0] = x.x; w[1] = x.y;
-      }
-    } else {
-      // Tail tile: only rows below r_end exist; the others read as 0.
+__device__ inline void load_scales(uint32_t (&w)[NG == 1 ? 2 : 4], __amdgpu_buffer_rsrc_t r,
+                                   unsigned row0, int gsel) {
+  if constexpr (NG == 1) {
+    const uint2 x = bload2(r, row0 * 2u);
+    w[0] = x.x;
+    w[1] = x.y;
+  } else if constexpr (NG == 2) {
 #pragma unroll
-      for (int i = 0; i < 2 * NG; ++i) {
-        const int r0 = (2 * i) / NG, r1 = (2 * i + 1) / NG;
-        const uint32_t lo = (row0 + r0 < r_end) ? p[2 * i] : 0u;
-        const uint32_t hi = (row0 + r1 < r_end) ? p[2 * i + 1] : 0u;
-        w[i] = lo | (hi << 16);
-      }
+    for (int p = 0; p < 2; ++p) {
+      const uint2 x = bload2(r, (row0 + 2u * p) * 4u);  // rows r, r+1: {g0,g1},{g0,g1}
+      w[2 * p] = x.x;
+      w[2 * p + 1] = x.y;
     }
+  } else {
+    const unsigned off = (row0 * 4u + (unsigned)(gsel & ~1)) * 2u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      uint32_t bits = 0;
+    for (int i = 0; i < 4; ++i) w[i] = bload1(r, off + 8u * i);
+  }
+}
+
+// The lane's halves of rows row0, row0+1 (word 0) and row0+2, row0+3
+// (word 1); sel is the per-lane v_perm selector of half (gsel & 1).  Rows at
+// or past nrows (cache padding, possibly never written) read as 0.
+template <int NG>
+__device__ inline void scale_words(uint32_t (&out)[2], const uint32_t (&w)[NG == 1 ? 2 : 4],
+                                   uint32_t sel, unsigned row0, unsigned nrows) {
+  if constexpr (NG == 1) {
+    out[0] = w[0];
+    out[1] = w[1];
+  } else {
+    out[0] = __builtin_amdgcn_perm(w[1], w[0], sel);
+    out[1] = __builtin_amdgcn_perm(w[3], w[2], sel);
+  }
+  if (row0 + 4u > nrows) {  // last tile of the split: drop rows >= nrows
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const int idx = r * NG + g;
-        const uint32_t hb = (idx & 1) ? (w[idx >> 1] >> 16) : (w[idx >> 1] & 0xFFFFu);
-        bits = (g == gsel) ? hb : bits;
-      }
-      v[r] = Elem<half_t>::to_f32((uint16_t)bits);
+    for (int p = 0; p < 2; ++p) {
+      const unsigned r0 = row0 + 2u * p;
+      out[p] = r0 + 1u < nrows ? out[p] : (r0 < nrows ? (out[p] & 0xFFFFu) : 0u);
     }
   }
-};
+}
 
 template <int BITS, int GS, int GC, int NW, int U>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 sdpa_mfma_q_kernel(SdpaArgs a) {
-  using T = half_t;
   constexpr int D = 128;
-  constexpr int NG = D / GS;                    // scale groups per row
-  constexpr int WPR = D * BITS / 32;            // code words per row
-  constexpr int KW = WPR / 4;                   // K words per lane (32 channels)
-  constexpr int VW = WPR / 16;                  // V words per lane per row (8 channels)
+  constexpr int NG = D / GS;  // scale groups per row
+  using Tile = QTile<BITS, NG>;
+  constexpr int WPR = Tile::WPR;
+  constexpr int KW = Tile::KW;
+  constexpr int VW = Tile::VW;
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -186,15 +237,18 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int nvh = min(GC, a.GV - vh0);
   const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
-  const int h = col % GC;       // head of this column
-  const int grp = col / GC;     // scale group of this column
+  const int h = col % GC;    // head of this column
+  const int grp = col / GC;  // scale group of this column
   const bool col_used = grp < NG && h < nvh;
   const int gsel = grp < NG ? grp : 0;  // group whose scales this lane reads
+  // v_perm selector keeping half (gsel & 1) of two words: low word = row r.
+  const uint32_t sel = (gsel & 1) ? 0x07060302u : 0x05040100u;
   int max_lim = 0;
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
   const int lim = h < nvh ? vhead_limit(a, vh0 + h) : 0;
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
+  const int nrows = max(r_end - r_begin, 0);
 
   // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
   // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
@@ -206,10 +260,10 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     const bool mine = col_used && (32 * blk) / GS == grp;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
+      const half8_t raw = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4*>(qp + 8 * s));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int c = 8 * s + (BITS == 4 ? q4_order(j) : j);
-        const _Float16 v = mine ? __builtin_bit_cast(_Float16, qp[c]) : (_Float16)0.f;
+        const _Float16 v = mine ? raw[BITS == 4 ? q4_order(j) : j] : (_Float16)0.f;
         qb[s][j] = v;
         qsum += (float)v;
       }
@@ -218,16 +272,51 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     qsum += __shfl_xor(qsum, 32);
   }
 
-  const long hbase = (long)bk * a.kv_cap;  // first cache row of this KV head
-  const uint32_t* kd = a.kd + hbase * WPR;
-  const uint32_t* v1d = a.v1d + hbase * WPR;
-  const uint32_t* v2d = a.v2d + hbase * WPR;
-  const uint16_t* ks = (const uint16_t*)a.ks + hbase * NG;
-  const uint16_t* kb = (const uint16_t*)a.kb + hbase * NG;
-  const uint16_t* v1s = (const uint16_t*)a.v1s + hbase * NG;
-  const uint16_t* v1b = (const uint16_t*)a.v1b + hbase * NG;
-  const uint16_t* v2s = (const uint16_t*)a.v2s + hbase * NG;
-  const uint16_t* v2b = (const uint16_t*)a.v2b + hbase * NG;
+  const long hrow0 = (long)bk * a.kv_cap + r_begin;  // first cache row of this split
+  const auto rk = stream_rsrc(a.kd + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
+  const auto rv1 = stream_rsrc(a.v1d + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
+  const auto rv2 = stream_rsrc(a.v2d + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
+  // Scale resources cover whole 4-row groups (kv_cap % 4 == 0 and the split
+  // starts at a multiple of 16 rows, so this stays inside the cache).
+  const unsigned sbytes = (unsigned)(((nrows + 3) & ~3) * NG * 2);
+  const __amdgpu_buffer_rsrc_t rs[6] = {
+      stream_rsrc((const uint16_t*)a.ks + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.kb + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v1s + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v1b + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v2s + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v2b + hrow0 * NG, sbytes)};
+
+  // All loads of U tiles starting at split-relative row t0 (rows past the
+  // split read 0).
+  auto load_tiles = [&](Tile (&T)[U], int t0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const unsigned r0 = (unsigned)(t0 + u * NW * 16);
+      const unsigned koff = ((r0 + col) * WPR + KW * blk) * 4u;
+#pragma unroll
+      for (int i = 0; i < KW; i += 4) {
+        const uint4 x = bload4(rk, koff + 4u * i);
+        T[u].k[i] = x.x; T[u].k[i + 1] = x.y; T[u].k[i + 2] = x.z; T[u].k[i + 3] = x.w;
+      }
+      const unsigned vrow = r0 + 4u * blk;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const unsigned voff = ((vrow + r) * WPR + VW * col) * 4u;
+        if constexpr (VW == 1) {
+          T[u].v1[r][0] = bload1(rv1, voff);
+          T[u].v2[r][0] = bload1(rv2, voff);
+        } else {
+          const uint2 x1 = bload2(rv1, voff);
+          const uint2 x2 = bload2(rv2, voff);
+          T[u].v1[r][0] = x1.x; T[u].v1[r][1] = x1.y;
+          T[u].v2[r][0] = x2.x; T[u].v2[r][1] = x2.y;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 6; ++t) load_scales<NG>(T[u].s[t], rs[t], vrow, gsel);
+    }
+  };
 
   floatx4 acc1[8], acc2[8], accl;
 #pragma unroll
@@ -239,63 +328,40 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   float beta1 = 0.f, beta2 = 0.f;  // sum_r p * b_V over this lane's rows
   float m_run = kNegSentinel;
   const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+  const uint32_t magic = magic_vgpr();
 
-  for (int base = r_begin + wave * 16; base < r_end; base += NW * 16 * U) {
-    uint32_t kw[U][KW];
-    uint32_t v1w[U][4][VW], v2w[U][4][VW];
-    LaneScales<NG> sk[U], bk_[U], s1[U], b1[U], s2[U], b2[U];
+  // Scores, online softmax and both V products of U loaded tiles at
+  // split-relative row t0.
+  auto compute_tiles = [&](const Tile (&T)[U], int t0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t0 = base + u * NW * 16;
-      const int krow = t0 + col;
-      if (krow < r_end) {
-        load_words_stream<KW>(kw[u], kd + (long)krow * WPR + KW * blk);
-      } else {
+      const int row0 = r_begin + t0 + u * NW * 16 + 4 * blk;  // absolute row of r = 0
+      const unsigned rrow0 = (unsigned)(t0 + u * NW * 16 + 4 * blk);  // split-relative
+      uint32_t sw[6][2];
 #pragma unroll
-        for (int i = 0; i < KW; ++i) kw[u][i] = 0u;
-      }
-      const int row0 = t0 + 4 * blk;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = row0 + r;
-        if (row < r_end) {
-          load_words_stream<VW>(v1w[u][r], v1d + (long)row * WPR + VW * col);
-          load_words_stream<VW>(v2w[u][r], v2d + (long)row * WPR + VW * col);
-        } else {
-#pragma unroll
-          for (int i = 0; i < VW; ++i) { v1w[u][r][i] = 0u; v2w[u][r][i] = 0u; }
-        }
-      }
-      const bool full = row0 + 3 < r_end;
-      sk[u].load(ks, row0, full, r_end, gsel);
-      bk_[u].load(kb, row0, full, r_end, gsel);
-      s1[u].load(v1s, row0, full, r_end, gsel);
-      b1[u].load(v1b, row0, full, r_end, gsel);
-      s2[u].load(v2s, row0, full, r_end, gsel);
-      b2[u].load(v2b, row0, full, r_end, gsel);
-    }
-
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t0 = base + u * NW * 16;
+      for (int t = 0; t < 6; ++t) scale_words<NG>(sw[t], T[u].s[t], sel, rrow0, (unsigned)nrows);
       floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         half8_t ka;
         if constexpr (BITS == 4) {
-          ka = q4_word_codes(kw[u][s]);
+          ka = q4_word_codes(T[u].k[s], magic);
         } else {
-          ka = q8_words_codes(kw[u][2 * s], kw[u][2 * s + 1]);
+          ka = q8_words_codes(T[u].k[2 * s], T[u].k[2 * s + 1]);
         }
         sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sacc, 0, 0, 0);
       }
+      const half2_t sk01 = as_h2(sw[0][0]), sk23 = as_h2(sw[0][1]);
+      const half2_t bk01 = as_h2(sw[1][0]), bk23 = as_h2(sw[1][1]);
+      const float skr[4] = {(float)sk01.x, (float)sk01.y, (float)sk23.x, (float)sk23.y};
+      const float bkr[4] = {(float)bk01.x, (float)bk01.y, (float)bk23.x, (float)bk23.y};
       float sc[4];
       float mx = kNegSentinel;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float t = col_used ? fmaf(sk[u].v[r], sacc[r], bk_[u].v[r] * qsum) : 0.f;
+        float t = col_used ? fmaf(skr[r], sacc[r], bkr[r] * qsum) : 0.f;
         t = sum_group_columns<GC>(t);
-        const int row = t0 + 4 * blk + r;
+        const int row = row0 + r;
         const bool ok = row < r_end && row < lim;
         sc[r] = ok ? t * a.qscale : kNegSentinel;
         mx = fmaxf(mx, sc[r]);
@@ -315,31 +381,54 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         beta2 *= fac;
         m_run = m_new;
       }
-      half4_t pb, w1, w2;
+      float p[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = (col_used && sc[r] > kNegSentinel) ? fast_exp2(sc[r] - m_run) : 0.f;
-        pb[r] = (_Float16)p;
-        w1[r] = (_Float16)(p * s1[u].v[r]);
-        w2[r] = (_Float16)(p * s2[u].v[r]);
-        beta1 = fmaf(p, b1[u].v[r], beta1);
-        beta2 = fmaf(p, b2[u].v[r], beta2);
-      }
+      for (int r = 0; r < 4; ++r)
+        p[r] = (col_used && sc[r] > kNegSentinel) ? fast_exp2(sc[r] - m_run) : 0.f;
+      // p rounded to fp16 once; the V weights, the bias terms and l all use
+      // these same values.
+      const half2_t p01 = half2_t{(_Float16)p[0], (_Float16)p[1]};
+      const half2_t p23 = half2_t{(_Float16)p[2], (_Float16)p[3]};
+      const half4_t pb = {p01.x, p01.y, p23.x, p23.y};
+      const half2_t w1a = p01 * as_h2(sw[2][0]), w1b = p23 * as_h2(sw[2][1]);
+      const half2_t w2a = p01 * as_h2(sw[4][0]), w2b = p23 * as_h2(sw[4][1]);
+      const half4_t w1 = {w1a.x, w1a.y, w1b.x, w1b.y};
+      const half4_t w2 = {w2a.x, w2a.y, w2b.x, w2b.y};
+      beta1 = __builtin_amdgcn_fdot2(p01, as_h2(sw[3][0]), beta1, false);
+      beta1 = __builtin_amdgcn_fdot2(p23, as_h2(sw[3][1]), beta1, false);
+      beta2 = __builtin_amdgcn_fdot2(p01, as_h2(sw[5][0]), beta2, false);
+      beta2 = __builtin_amdgcn_fdot2(p23, as_h2(sw[5][1]), beta2, false);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         uint32_t x1[4], x2[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          x1[r] = v1w[u][r][BITS == 4 ? 0 : (i >> 2)];
-          x2[r] = v2w[u][r][BITS == 4 ? 0 : (i >> 2)];
+          x1[r] = T[u].v1[r][BITS == 4 ? 0 : (i >> 2)];
+          x2[r] = T[u].v2[r][BITS == 4 ? 0 : (i >> 2)];
         }
-        const half4_t a1 = v_codes<BITS>(x1, BITS == 4 ? i : (i & 3));
-        const half4_t a2 = v_codes<BITS>(x2, BITS == 4 ? i : (i & 3));
+        const half4_t a1 = v_codes<BITS>(x1, BITS == 4 ? i : (i & 3), magic);
+        const half4_t a2 = v_codes<BITS>(x2, BITS == 4 ? i : (i & 3), magic);
         acc1[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, w1, acc1[i], 0, 0, 0);
         acc2[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2, w2, acc2[i], 0, 0, 0);
       }
       accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pb, accl, 0, 0, 0);
     }
+  };
+
+  // Two register sets in turn: the loads of the next U tiles are in flight
+  // while the current ones are computed.
+  constexpr int kStep = NW * 16 * U;
+  Tile ta[U], tb[U];
+  int t0 = wave * 16;
+  load_tiles(ta, t0);
+  while (t0 < nrows) {
+    load_tiles(tb, t0 + kStep);
+    compute_tiles(ta, t0);
+    t0 += kStep;
+    if (t0 >= nrows) break;
+    load_tiles(ta, t0 + kStep);
+    compute_tiles(tb, t0);
+    t0 += kStep;
   }
 
   // Bias terms: sum the four row blocks of each column.
@@ -377,16 +466,16 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     lds_l[wave][h] = accl[0];
   }
   __syncthreads();
-  wg_epilogue<T, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+  wg_epilogue<half_t, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
 // Packed cache, head_dim 128, fp16 scales: heads x groups <= 16 columns.
-// Two tiles in flight per wave, except q8 with 32-channel groups, whose
-// twelve scale vectors per tile would spill.
+// One tile per register set: with the prefetched set, two tiles' loads are
+// in flight per wave while one is computed.
 template <int BITS, int GS>
 int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;
-  constexpr int U = (BITS == 8 && GS == 32) ? 1 : 2;
+  constexpr int U = 1;
   switch (gc) {
     case 1:
       if (waves == 8) hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 8, U>), dim3(nblocks), dim3(512), 0, st, a);
