@@ -54,7 +54,8 @@ Tuning& tuning() {
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max) {
+SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max,
+                   int waves_pref, int wgs_per_cu) {
   SdpaPlan p{};
   const int G = Hkv > 0 ? Hq / Hkv : 1;
   const int GV = G * S_q;
@@ -65,7 +66,8 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   // 8-wave workgroups when their cross-wave LDS merge fits (D * gc <= 512
   // floats per wave per slab), else 4.
   const int max_waves = (D * gc <= 512) ? 8 : 4;
-  p.waves = tuning().waves_per_wg ? tuning().waves_per_wg : max_waves;
+  p.waves = tuning().waves_per_wg ? tuning().waves_per_wg
+                                  : (waves_pref > 0 && waves_pref < max_waves ? waves_pref : max_waves);
   if (p.waves > max_waves) p.waves = max_waves;
 
   const int units = B * Hkv * p.nchunk;
@@ -73,8 +75,10 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   // load (4 for 16 lanes per row) x unroll 4.  Splits are whole iterations.
   const int step = p.waves * 4 * 4;
   // Default: one round of workgroups over the CUs (an 8-wave workgroup
-  // fills a CU at this kernel's register use; a 4-wave one fills half).
-  int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count() * (8 / p.waves);
+  // fills a CU at two waves per SIMD; a 4-wave one fills half of it, or all
+  // of it for kernels that run one wave per SIMD: wgs_per_cu = 1).
+  const int per_cu = wgs_per_cu > 0 ? wgs_per_cu : 8 / p.waves;
+  int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count() * per_cu;
   int rows = kv_len > 0 ? kv_len : 1;
   int rps;
   if (tuning().rows_per_split > 0) {
@@ -122,7 +126,17 @@ size_t motif_sdpa_counter_bytes(int B, int Hq, int Hkv, int S_q) {
 
 size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S_q <= 0 || D <= 0 || kv_len < 0) return 0;
-  return plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D)).workspace_bytes;
+  // Enough for every kernel family a call may take: the fp16/bf16/fp32 and
+  // VALU plans and the packed-cache matrix-core plans of each group size.
+  size_t ws = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0).workspace_bytes;
+  if (D == kSdpaMfmaQD) {
+    for (int gs = 32; gs <= 128; gs *= 2) {
+      const SdpaPlan p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),
+                                   kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu);
+      if (p.workspace_bytes > ws) ws = p.workspace_bytes;
+    }
+  }
+  return ws;
 }
 
 int motif_set_tuning(const char* key, int value) {

@@ -23,7 +23,7 @@ static bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a)
 // and plan/workspace set-up.
 static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, int B, int Hq,
                        int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal, float scale,
-                       void* ws, size_t ws_bytes, int gc_max) {
+                       void* ws, size_t ws_bytes, int gc_max, int waves_pref, int wgs_per_cu) {
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "%s: unknown dtype code %d", name, dtype);
   MOTIF_REQUIRE(B >= 1 && Hq >= 1 && Hkv >= 1 && S_q >= 1, "%s: B, H_q, H_kv, S_q must be >= 1",
@@ -33,7 +33,7 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
   MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
                 "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
   MOTIF_REQUIRE((long)B * Hkv * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
-  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, gc_max);
+  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, gc_max, waves_pref, wgs_per_cu);
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -86,7 +86,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   SdpaArgs a{};
   SdpaPlan p{};
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes, sdpa_gc_max(D));
+                       ws_bytes, sdpa_gc_max(D), 0, 0);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
   const int al = sdpa_fp_align(dtype, D);
@@ -127,10 +127,12 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
                 name, gs);
   SdpaArgs a{};
   SdpaPlan p{};
-  // The matrix-core kernel puts (head, scale group) pairs on 16 columns.
-  const int gc_max = (D == 128 && dtype == MOTIF_F16) ? sdpa_gc_max_q(D, gs) : sdpa_gc_max(D);
+  // The matrix-core kernel puts (head, scale group) pairs on 16 columns and
+  // runs 4-wave workgroups, one per CU.
+  const bool mfma_q = D == kSdpaMfmaQD && dtype == MOTIF_F16 && tuning().mfma;
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes, gc_max);
+                       ws_bytes, mfma_q ? sdpa_gc_max_q(D, gs) : sdpa_gc_max(D),
+                       mfma_q ? kSdpaMfmaQWaves : 0, mfma_q ? kSdpaMfmaQWgsPerCu : 0);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (kd && ks && kb && v1d && v1s && v1b && v2d && v2s &&
                                            v2b)),

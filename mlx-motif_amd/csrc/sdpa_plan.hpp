@@ -55,7 +55,16 @@ struct SdpaPlan {
 constexpr int kMaxSplits = 256;
 
 // gc_max: the largest per-workgroup head count compiled for this head dim.
-SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max);
+// waves_pref: waves per workgroup (0: 8 where the LDS merge fits, else 4);
+// wgs_per_cu: workgroups one CU holds at once (0: 8 / waves).
+SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max,
+                   int waves_pref, int wgs_per_cu);
+
+// Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
+// workgroups at one wave per SIMD, one per CU.
+constexpr int kSdpaMfmaQD = 128;
+constexpr int kSdpaMfmaQWaves = 4;
+constexpr int kSdpaMfmaQWgsPerCu = 1;
 
 // Largest head chunk compiled for head dim D (register budget).
 inline int sdpa_gc_max(int D) { return D <= 128 ? 8 : 4; }
