@@ -69,6 +69,30 @@ __device__ inline void wait_stores_done() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Workgroup -> (unit = (b, KV head, chunk), split).  With one chunk per KV
+// head, consecutive workgroups take the KV heads of one split.  With several
+// chunks (more virtual heads than one workgroup holds, e.g. a verify slab),
+// the chunks of one (b, KV head, split) go to workgroups 8 apart: the
+// dispatcher deals workgroups round-robin to the 8 XCDs, so those chunks run
+// on one XCD and all but the first find the shared K/V rows in its L2.
+// Placement only affects speed.  Padding workgroups (see sdpa_grid_blocks)
+// return false and exit.
+__device__ inline bool sdpa_block_coords(const SdpaArgs& a, int bid, int& unit, int& split) {
+  const int bh = a.B * a.Hkv;
+  if (a.nchunk == 1) {
+    unit = bid % bh;
+    split = bid / bh;
+    return true;
+  }
+  const int slot = bid >> 3;
+  const int chunk = slot % a.nchunk;
+  const int g = (slot / a.nchunk) * 8 + (bid & 7);  // g = split * bh + (b, KV head)
+  if (g >= bh * a.nsplit) return false;
+  split = g / bh;
+  unit = (g % bh) * a.nchunk + chunk;
+  return true;
+}
+
 // --------------------------------------------------------------- formats --
 // fp16 / bf16 / fp32 cache rows of D elements.  16 lanes per row.
 template <typename T_, int D_>
@@ -483,9 +507,8 @@ __global__ void __launch_bounds__(NW * 64) sdpa_dual_v_kernel(SdpaArgs a) {
   // Consecutive workgroup ids walk (b, KV head, chunk) first, so all splits
   // of one KV head share an id residue (and the XCD round-robin puts them on
   // one XCD, whose L2 then serves the final merge).
-  const int units = a.B * a.Hkv * a.nchunk;
-  const int unit = blockIdx.x % units;
-  const int split = blockIdx.x / units;
+  int unit, split;
+  if (!sdpa_block_coords(a, blockIdx.x, unit, split)) return;  // grid padding
   const int chunk = unit % a.nchunk;
   const int bk = unit / a.nchunk;  // b * Hkv + kv head
   const int b = bk / a.Hkv;

@@ -14,7 +14,7 @@ namespace motif {
 
 int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                               hipStream_t s) {
-  const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
     if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0)
       return launch_sdpa_mfma_f16(a, p.gc, p.waves, nblocks, s);
@@ -52,7 +52,7 @@ int MOTIF_CAT(launch_sdpa_merge_, MOTIF_SUFFIX)(const SdpaArgs& a, int D, hipStr
 
 int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                              int bits, hipStream_t s) {
-  const int nblocks = a.B * a.Hkv * p.nchunk * p.nsplit;
+  const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
     const int ng = D / a.group_size;
     const uintptr_t scale_bits = (uintptr_t)a.ks | (uintptr_t)a.kb | (uintptr_t)a.v1s |

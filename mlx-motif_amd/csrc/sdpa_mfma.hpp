@@ -53,9 +53,8 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   const int col = lane & 15;  // MFMA column: virtual head (S^T, P^T, O^T)
   const int blk = lane >> 4;  // MFMA k/row block
 
-  const int units = a.B * a.Hkv * a.nchunk;
-  const int unit = blockIdx.x % units;
-  const int split = blockIdx.x / units;
+  int unit, split;
+  if (!sdpa_block_coords(a, blockIdx.x, unit, split)) return;  // grid padding
   const int chunk = unit % a.nchunk;
   const int bk = unit / a.nchunk;
   const int b = bk / a.Hkv;

@@ -50,6 +50,14 @@ struct SdpaPlan {
   size_t workspace_bytes;
 };
 
+// Grid of a split-KV launch: one workgroup per (b, KV head, chunk, split).
+// With several chunks, groups of 8 (b, KV head, split) are padded so that
+// sdpa_block_coords() can place the chunks of one group on one XCD.
+inline int sdpa_grid_blocks(int bh, int nchunk, int nsplit) {
+  const int groups = bh * nsplit;
+  return nchunk == 1 ? groups : (groups + 7) / 8 * 8 * nchunk;
+}
+
 // Upper bound on splits per (b, KV head, chunk): the final merge keeps every
 // split's (m, l) pair in LDS.
 constexpr int kMaxSplits = 256;
