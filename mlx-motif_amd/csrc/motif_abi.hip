@@ -77,7 +77,9 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   // Default: one round of workgroups over the CUs (an 8-wave workgroup
   // fills a CU at two waves per SIMD; a 4-wave one fills half of it, or all
   // of it for kernels that run one wave per SIMD: wgs_per_cu = 1).
-  const int per_cu = wgs_per_cu > 0 ? wgs_per_cu : 8 / p.waves;
+  // With several head chunks per KV head (a verify slab), each chunk's
+  // workgroups should still cover the CUs: up to 3x more workgroups.
+  const int per_cu = wgs_per_cu > 0 ? wgs_per_cu * (p.nchunk < 3 ? p.nchunk : 3) : 8 / p.waves;
   int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count() * per_cu;
   int rows = kv_len > 0 ? kv_len : 1;
   int rps;

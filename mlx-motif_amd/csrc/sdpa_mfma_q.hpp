@@ -132,16 +132,19 @@ __device__ inline __amdgpu_buffer_rsrc_t stream_rsrc(const void* base, unsigned 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+// POL: kCachePolicyStream for data read once per call, 0 (cached) where
+// several workgroups read the same rows (head chunks of a verify slab).
+template <int POL = kCachePolicyStream>
 __device__ inline uint4 bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(uint4,
-                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCachePolicyStream));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL));
 }
+template <int POL = kCachePolicyStream>
 __device__ inline uint2 bload2(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(uint2,
-                            __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyStream));
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL));
 }
+template <int POL = kCachePolicyStream>
 __device__ inline uint32_t bload1(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCachePolicyStream);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
 }
 
 // One 16-row tile of the packed cache as one lane loads it.
@@ -168,24 +171,24 @@ struct QTile {
 // 8-byte loads of two rows each; NG = 4: one 4-byte load per row holding
 // groups (gsel & ~1, gsel | 1).  The resource covers whole 4-row groups, so
 // no load straddles its end.
-template <int NG>
+template <int NG, int POL>
 __device__ inline void load_scales(uint32_t (&w)[NG == 1 ? 2 : 4], __amdgpu_buffer_rsrc_t r,
                                    unsigned row0, int gsel) {
   if constexpr (NG == 1) {
-    const uint2 x = bload2(r, row0 * 2u);
+    const uint2 x = bload2<POL>(r, row0 * 2u);
     w[0] = x.x;
     w[1] = x.y;
   } else if constexpr (NG == 2) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const uint2 x = bload2(r, (row0 + 2u * p) * 4u);  // rows r, r+1: {g0,g1},{g0,g1}
+      const uint2 x = bload2<POL>(r, (row0 + 2u * p) * 4u);  // rows r, r+1: {g0,g1},{g0,g1}
       w[2 * p] = x.x;
       w[2 * p + 1] = x.y;
     }
   } else {
     const unsigned off = (row0 * 4u + (unsigned)(gsel & ~1)) * 2u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = bload1(r, off + 8u * i);
+    for (int i = 0; i < 4; ++i) w[i] = bload1<POL>(r, off + 8u * i);
   }
 }
 
@@ -211,7 +214,11 @@ __device__ inline void scale_words(uint32_t (&out)[2], const uint32_t (&w)[NG ==
   }
 }
 
-template <int BITS, int GS, int GC, int NW, int U>
+// POL: cache policy of the K/V/scale loads.  Launches with several head
+// chunks (a.nchunk > 1: more virtual heads than one pass holds, e.g. a
+// verify slab) read each row in several workgroups and use cached loads, so
+// all but the first find the rows in L2 or the Infinity Cache.
+template <int BITS, int GS, int GC, int NW, int U, int POL = kCachePolicyStream>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int D = 128;
@@ -295,7 +302,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       const unsigned koff = ((r0 + col) * WPR + KW * blk) * 4u;
 #pragma unroll
       for (int i = 0; i < KW; i += 4) {
-        const uint4 x = bload4(rk, koff + 4u * i);
+        const uint4 x = bload4<POL>(rk, koff + 4u * i);
         T[u].k[i] = x.x; T[u].k[i + 1] = x.y; T[u].k[i + 2] = x.z; T[u].k[i + 3] = x.w;
       }
       const unsigned vrow = r0 + 4u * blk;
@@ -303,17 +310,17 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       for (int r = 0; r < 4; ++r) {
         const unsigned voff = ((vrow + r) * WPR + VW * col) * 4u;
         if constexpr (VW == 1) {
-          T[u].v1[r][0] = bload1(rv1, voff);
-          T[u].v2[r][0] = bload1(rv2, voff);
+          T[u].v1[r][0] = bload1<POL>(rv1, voff);
+          T[u].v2[r][0] = bload1<POL>(rv2, voff);
         } else {
-          const uint2 x1 = bload2(rv1, voff);
-          const uint2 x2 = bload2(rv2, voff);
+          const uint2 x1 = bload2<POL>(rv1, voff);
+          const uint2 x2 = bload2<POL>(rv2, voff);
           T[u].v1[r][0] = x1.x; T[u].v1[r][1] = x1.y;
           T[u].v2[r][0] = x2.x; T[u].v2[r][1] = x2.y;
         }
       }
 #pragma unroll
-      for (int t = 0; t < 6; ++t) load_scales<NG>(T[u].s[t], rs[t], vrow, gsel);
+      for (int t = 0; t < 6; ++t) load_scales<NG, POL>(T[u].s[t], rs[t], vrow, gsel);
     }
   };
 
@@ -475,6 +482,12 @@ template <int BITS, int GS>
 int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;
   constexpr int U = 1;
+  constexpr int GCM = 16 / NG < 8 ? 16 / NG : 8;  // widest pass
+  if (a.nchunk > 1 && gc == GCM && waves == 4) {
+    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, GCM, 4, U, 0>), dim3(nblocks), dim3(256), 0,
+                       st, a);
+    return check_launch("sdpa_dual_v_q (mfma, chunks)");
+  }
   switch (gc) {
     case 1:
       if (waves == 8) hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 8, U>), dim3(nblocks), dim3(512), 0, st, a);
