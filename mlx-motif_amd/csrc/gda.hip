@@ -54,7 +54,9 @@ __global__ void __launch_bounds__(256) gda_vec_kernel(GdaArgs a) {
   for (int j = 0; j < NCH; ++j) {
     const int c = sub + 16 * j;
     if (active && c < nchunks) {
-      uint4 ov = *reinterpret_cast<const uint4*>((const uint16_t*)a.o + o_off + c * 8);
+      // o is read once (streaming); a noise row serves gr origin rows, so it
+      // stays cacheable.
+      uint4 ov = ld_stream4((const uint16_t*)a.o + o_off + c * 8);
       uint4 nv = *reinterpret_cast<const uint4*>((const uint16_t*)a.n + n_off + c * 8);
       uint32_t ow[4] = {ov.x, ov.y, ov.z, ov.w};
       uint32_t nw[4] = {nv.x, nv.y, nv.z, nv.w};
@@ -84,8 +86,7 @@ __global__ void __launch_bounds__(256) gda_vec_kernel(GdaArgs a) {
         float y1 = d[j][e + 1] * rms_inv * Elem<T>::get(ww, e + 1) * a.scale;
         out[e / 2] = (uint32_t)Elem<T>::from_f32(y0) | ((uint32_t)Elem<T>::from_f32(y1) << 16);
       }
-      *reinterpret_cast<uint4*>((uint16_t*)a.y + y_off + c * 8) =
-          make_uint4(out[0], out[1], out[2], out[3]);
+      st_stream4((uint16_t*)a.y + y_off + c * 8, out[0], out[1], out[2], out[3]);
     }
   }
 }

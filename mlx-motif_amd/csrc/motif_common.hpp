@@ -148,6 +148,10 @@ __device__ inline uint2 ld_stream2(const void* p) {
 __device__ inline uint32_t ld_stream1(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
+// Streaming 16-byte store (output written once).
+__device__ inline void st_stream4(void* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  __builtin_nontemporal_store(u32x4_nt_t{a, b, c, d}, reinterpret_cast<u32x4_nt_t*>(p));
+}
 
 // load_words with streaming loads.
 template <int NW>

@@ -3,10 +3,14 @@
 //   y    = T(w0*(x^3*rs3) + w1*(x^2*rs2) + w2*(x*rs1) + b), fp32 math.
 // The reference kernel reads each row twice (sums, then outputs).  Here a
 // row is held in registers between the reduction and the store, so x is read
-// from HBM once: LPR lanes per row, NCH chunks of 8 values per lane.
-//   LPR = 16  : rows of <= 128 values, 16 rows per 256-thread workgroup
-//   LPR = 64  : rows of <= 2048 values, one wave per row
-//   LPR = 256 : rows of <= 32768 values, one workgroup per row (LDS merge)
+// from HBM once: LPR lanes per row, NCH chunks of 8 values per lane, with
+// nontemporal loads and stores (each byte is touched once).
+//   LPR = 16   : rows of <= 128 values, 16 rows per 256-thread workgroup
+//   LPR = 64   : rows of <= 2048 values, one wave per row
+//   LPR = 512  : rows of <= 16384 values, one 512-thread workgroup per row
+//   LPR = 1024 : rows of <= 32768 values, one 1024-thread workgroup per row
+// (the wide rows merge their wave sums in LDS; 4 loads in flight per lane
+// measured faster than 7 at 256 lanes for 13824-value rows)
 // Rows whose length is not a multiple of 8, or longer, take a strided
 // scalar path that reads x twice.
 #include "motif_common.hpp"
@@ -26,15 +30,16 @@ struct PolyArgs {
 template <typename T>
 __device__ inline void load8v(const void* base, long idx, float (&v)[8]) {
   if constexpr (sizeof(T) == 2) {
-    uint4 q = *reinterpret_cast<const uint4*>((const uint16_t*)base + idx);
+    const uint4 q = ld_stream4((const uint16_t*)base + idx);
     uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = Elem<T>::get(w, i);
   } else {
-    const float4* p = reinterpret_cast<const float4*>((const float*)base + idx);
-    float4 a = p[0], c = p[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+    const uint4 a = ld_stream4((const float*)base + idx);
+    const uint4 c = ld_stream4((const float*)base + idx + 4);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_bit_cast(float, w[i]);
   }
 }
 
@@ -46,11 +51,13 @@ __device__ inline void store8v(void* base, long idx, const float (&v)[8]) {
     for (int i = 0; i < 4; ++i)
       w[i] = (uint32_t)Elem<T>::from_f32(v[2 * i]) |
              ((uint32_t)Elem<T>::from_f32(v[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4*>((uint16_t*)base + idx) = make_uint4(w[0], w[1], w[2], w[3]);
+    st_stream4((uint16_t*)base + idx, w[0], w[1], w[2], w[3]);
   } else {
-    float4* p = reinterpret_cast<float4*>((float*)base + idx);
-    p[0] = make_float4(v[0], v[1], v[2], v[3]);
-    p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __builtin_bit_cast(uint32_t, v[i]);
+    st_stream4((float*)base + idx, w[0], w[1], w[2], w[3]);
+    st_stream4((float*)base + idx + 4, w[4], w[5], w[6], w[7]);
   }
 }
 
@@ -61,9 +68,9 @@ __device__ inline float poly_out(float v, float rs2, float rs4, float rs6, float
   return w0 * (v3 * rs6) + w1 * (v2 * rs4) + w2 * (v * rs2) + b;
 }
 
-template <typename T, int LPR, int NCH>
-__global__ void __launch_bounds__(256) polynorm_vec_kernel(PolyArgs a) {
-  constexpr int RPB = 256 / LPR;  // rows per block
+template <typename T, int LPR, int NCH, int TPB>
+__global__ void __launch_bounds__(TPB) polynorm_vec_kernel(PolyArgs a) {
+  constexpr int RPB = TPB / LPR;  // rows per block
   const int tid = threadIdx.x;
   const int sub = tid % LPR;
   const long row = (long)blockIdx.x * RPB + tid / LPR;
@@ -95,8 +102,10 @@ __global__ void __launch_bounds__(256) polynorm_vec_kernel(PolyArgs a) {
     s2 = group_sum<LPR>(s2);
     s4 = group_sum<LPR>(s4);
     s6 = group_sum<LPR>(s6);
-  } else {
-    __shared__ float red[3][4];
+  } else {  // one row per workgroup: LPR / 64 wave sums meet in LDS
+    constexpr int NWV = LPR / 64;
+    static_assert(RPB == 1, "wide rows take the whole workgroup");
+    __shared__ float red[3][NWV];
     s2 = group_sum<64>(s2);
     s4 = group_sum<64>(s4);
     s6 = group_sum<64>(s6);
@@ -107,9 +116,13 @@ __global__ void __launch_bounds__(256) polynorm_vec_kernel(PolyArgs a) {
       red[2][wave] = s6;
     }
     __syncthreads();
-    s2 = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-    s4 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
-    s6 = (red[2][0] + red[2][1]) + (red[2][2] + red[2][3]);
+    s2 = s4 = s6 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) {
+      s2 += red[0][i];
+      s4 += red[1][i];
+      s6 += red[2][i];
+    }
   }
   if (!active) return;
   const float inv_d = 1.0f / (float)a.D;
@@ -169,30 +182,14 @@ __global__ void __launch_bounds__(256) polynorm_scalar_kernel(PolyArgs a) {
                    poly_out(Elem<T>::load(a.x, base + i), rs2, rs4, rs6, w0, w1, w2, bb));
 }
 
-template <typename T, int LPR>
+template <typename T, int LPR, int TPB>
 static void launch_poly_lpr(const PolyArgs& a, int nch, hipStream_t st) {
-  const unsigned blocks = (unsigned)((a.rows + 256 / LPR - 1) / (256 / LPR));
+  const unsigned blocks = (unsigned)((a.rows + TPB / LPR - 1) / (TPB / LPR));
   switch (nch) {
-#define MOTIF_POLY_CASE(N)                                                               \
-  case N:                                                                                \
-    hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, N>), blocks, 256, 0, st, a); break;
-    MOTIF_POLY_CASE(1)
-    MOTIF_POLY_CASE(2)
-    MOTIF_POLY_CASE(3)
-    MOTIF_POLY_CASE(4)
-    MOTIF_POLY_CASE(5)
-    MOTIF_POLY_CASE(6)
-    MOTIF_POLY_CASE(7)
-    MOTIF_POLY_CASE(8)
-    MOTIF_POLY_CASE(9)
-    MOTIF_POLY_CASE(10)
-    MOTIF_POLY_CASE(11)
-    MOTIF_POLY_CASE(12)
-    MOTIF_POLY_CASE(13)
-    MOTIF_POLY_CASE(14)
-    MOTIF_POLY_CASE(15)
-    MOTIF_POLY_CASE(16)
-#undef MOTIF_POLY_CASE
+    case 1: hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, 1, TPB>), blocks, TPB, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, 2, TPB>), blocks, TPB, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, 3, TPB>), blocks, TPB, 0, st, a); break;
+    case 4: hipLaunchKernelGGL((polynorm_vec_kernel<T, LPR, 4, TPB>), blocks, TPB, 0, st, a); break;
     default: break;
   }
 }
@@ -202,15 +199,19 @@ static int launch_poly(const PolyArgs& a, bool vec_ok, hipStream_t st) {
   const int nchunks = a.D / 8;
   if (vec_ok && a.D % 8 == 0) {
     if (nchunks <= 16) {
-      launch_poly_lpr<T, 16>(a, 1, st);
+      launch_poly_lpr<T, 16, 256>(a, 1, st);
       return check_launch("polynorm");
     }
     if (nchunks <= 64 * 4) {
-      launch_poly_lpr<T, 64>(a, (nchunks + 63) / 64, st);
+      launch_poly_lpr<T, 64, 256>(a, (nchunks + 63) / 64, st);
       return check_launch("polynorm");
     }
-    if (nchunks <= 256 * 16) {
-      launch_poly_lpr<T, 256>(a, (nchunks + 255) / 256, st);
+    if (nchunks <= 512 * 4) {
+      launch_poly_lpr<T, 512, 512>(a, (nchunks + 511) / 512, st);
+      return check_launch("polynorm");
+    }
+    if (nchunks <= 1024 * 4) {
+      launch_poly_lpr<T, 1024, 1024>(a, (nchunks + 1023) / 1024, st);
       return check_launch("polynorm");
     }
   }
