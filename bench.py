@@ -210,9 +210,10 @@ def main() -> int:
     ap.add_argument("--valu", action="store_true",
                     help="route attention through the VALU kernels (matrix cores off), "
                          "for comparison")
-    ap.add_argument("--traffic", action="store_true",
-                    help="counter pass: one 256 MiB copy, then eager fp16 decode calls (no "
-                         "timing, no JSON); run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--traffic", nargs="?", const="f16", choices=("f16", "q4", "q8"),
+                    help="counter pass: one 256 MiB copy, then 16 eager decode calls on the "
+                         "given cache (default f16; no timing, no JSON); run under rocprofv3 "
+                         "--pmc")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -228,7 +229,7 @@ def main() -> int:
     lib = _native.lib()
     dev = torch.device("cuda:0")
     if args.traffic:
-        return traffic_pass(torch, lib, dev)
+        return traffic_pass(torch, lib, dev, args.traffic)
     if args.valu:
         _native.set_tuning("mfma", 0)
     graph = not args.no_graph
@@ -292,21 +293,24 @@ def main() -> int:
     return 0
 
 
-def traffic_pass(torch, lib, dev) -> int:
-    """Dispatches for the HBM-traffic counters: a plain copy of known size
+def traffic_pass(torch, lib, dev, kind: str = "f16") -> int:
+    """Dispatches for the hardware counters: a plain copy of known size
     (256 MiB read + 256 MiB written; calibrates FETCH_SIZE / WRITE_SIZE) and
-    16 fp16 decode calls over 8 buffer sets, each 98 MB of algorithmic bytes."""
+    16 decode calls over 8 buffer sets of the given cache type."""
     src = torch.empty(128 << 20, dtype=torch.float16, device=dev).normal_()
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    calls, keep = make_fp16_calls(torch, lib, dev, 8)
+    if kind == "f16":
+        calls, keep = make_fp16_calls(torch, lib, dev, 8)
+    else:
+        calls, keep = make_q_calls(torch, lib, dev, 8, 4 if kind == "q4" else 8)
     for i in range(16):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
-    log(f"traffic pass: copy 268435456 B + 16 decode calls of {alg_bytes('f16')} B")
+    log(f"traffic pass: copy 268435456 B + 16 {kind} decode calls of {alg_bytes(kind)} B")
     del calls, keep
     return 0
 

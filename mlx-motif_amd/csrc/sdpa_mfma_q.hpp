@@ -193,11 +193,10 @@ __device__ inline void load_scales(uint32_t (&w)[NG == 1 ? 2 : 4], __amdgpu_buff
 }
 
 // The lane's halves of rows row0, row0+1 (word 0) and row0+2, row0+3
-// (word 1); sel is the per-lane v_perm selector of half (gsel & 1).  Rows at
-// or past nrows (cache padding, possibly never written) read as 0.
+// (word 1); sel is the per-lane v_perm selector of half (gsel & 1).
 template <int NG>
 __device__ inline void scale_words(uint32_t (&out)[2], const uint32_t (&w)[NG == 1 ? 2 : 4],
-                                   uint32_t sel, unsigned row0, unsigned nrows) {
+                                   uint32_t sel) {
   if constexpr (NG == 1) {
     out[0] = w[0];
     out[1] = w[1];
@@ -205,12 +204,15 @@ __device__ inline void scale_words(uint32_t (&out)[2], const uint32_t (&w)[NG ==
     out[0] = __builtin_amdgcn_perm(w[1], w[0], sel);
     out[1] = __builtin_amdgcn_perm(w[3], w[2], sel);
   }
-  if (row0 + 4u > nrows) {  // last tile of the split: drop rows >= nrows
+}
+
+// Rows at or past nrows (cache padding, possibly never written, read by a
+// whole 4-row scale load) get zero scale and bias.
+__device__ inline void drop_rows_past(uint32_t (&out)[2], unsigned row0, unsigned nrows) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const unsigned r0 = row0 + 2u * p;
-      out[p] = r0 + 1u < nrows ? out[p] : (r0 < nrows ? (out[p] & 0xFFFFu) : 0u);
-    }
+  for (int p = 0; p < 2; ++p) {
+    const unsigned r0 = row0 + 2u * p;
+    out[p] = r0 + 1u < nrows ? out[p] : (r0 < nrows ? (out[p] & 0xFFFFu) : 0u);
   }
 }
 
@@ -345,7 +347,13 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       const unsigned rrow0 = (unsigned)(t0 + u * NW * 16 + 4 * blk);  // split-relative
       uint32_t sw[6][2];
 #pragma unroll
-      for (int t = 0; t < 6; ++t) scale_words<NG>(sw[t], T[u].s[t], sel, rrow0, (unsigned)nrows);
+      for (int t = 0; t < 6; ++t) scale_words<NG>(sw[t], T[u].s[t], sel);
+      // Only the split's last tile can hold rows past its end; the test is
+      // uniform over the wave, so the others branch around the masking.
+      if (t0 + u * NW * 16 + 16 > nrows) {
+#pragma unroll
+        for (int t = 0; t < 6; ++t) drop_rows_past(sw[t], rrow0, (unsigned)nrows);
+      }
       floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -365,7 +373,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       float mx = kNegSentinel;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float t = col_used ? fmaf(skr[r], sacc[r], bkr[r] * qsum) : 0.f;
+        // Unused columns have Q^T = 0 and qsum = 0, so t = 0 there without
+        // a select (their scale words are finite cache values or 0).
+        float t = fmaf(skr[r], sacc[r], bkr[r] * qsum);
         t = sum_group_columns<GC>(t);
         const int row = row0 + r;
         const bool ok = row < r_end && row < lim;
@@ -390,7 +400,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       float p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        p[r] = (col_used && sc[r] > kNegSentinel) ? fast_exp2(sc[r] - m_run) : 0.f;
+        p[r] = sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run) : 0.f;
       // p rounded to fp16 once; the V weights, the bias terms and l all use
       // these same values.
       const half2_t p01 = half2_t{(_Float16)p[0], (_Float16)p[1]};
