@@ -206,13 +206,21 @@ struct QFmt {
 // cross-wave staging buffer on different LDS banks.
 constexpr int kLdsPad = 4;
 
+// y[off .. off+3] = v / L (v itself where L == 0: no visible key), one
+// 8-byte store for 2-byte types (off is a multiple of 4).
 template <typename T, int D>
 __device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) {
   const bool z = L == 0.f;
-  Elem<T>::store(a.y, off + 0, z ? v.x : v.x / L);
-  Elem<T>::store(a.y, off + 1, z ? v.y : v.y / L);
-  Elem<T>::store(a.y, off + 2, z ? v.z : v.z / L);
-  Elem<T>::store(a.y, off + 3, z ? v.w : v.w / L);
+  const float o[4] = {z ? v.x : v.x / L, z ? v.y : v.y / L, z ? v.z : v.z / L,
+                      z ? v.w : v.w / L};
+  if constexpr (Elem<T>::kBytes == 2) {
+    const uint2 w = make_uint2(
+        (uint32_t)Elem<T>::from_f32(o[0]) | ((uint32_t)Elem<T>::from_f32(o[1]) << 16),
+        (uint32_t)Elem<T>::from_f32(o[2]) | ((uint32_t)Elem<T>::from_f32(o[3]) << 16));
+    *reinterpret_cast<uint2*>((uint16_t*)a.y + off) = w;
+  } else {
+    *reinterpret_cast<float4*>((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 // ------------------------------------------------------- split merge ---
@@ -392,92 +400,78 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
 
 // ------------------------------------------------------- merge kernel ---
 // Second launch of a split call: combines the nsplit partials of every
-// virtual-head row.  A workgroup of 256 threads owns one row and a slice of
-// CW float4 output columns; thread (column, group) sums the splits
-// group, group + NG, ...  All partial loads of the first batch and the
-// row's (m, l) pairs are issued before any is consumed.  The kernel boundary
-// makes the main kernel's partials visible, so plain loads suffice.
+// virtual-head row.  One wave per (row, slice of CW float4 output columns),
+// no LDS and no barrier: lane (column, group) sums the splits group,
+// group + NGR, ...; the row max M and total L come from lane-strided loads
+// of the (m, l) pairs and wave reductions, and each lane reads the m of its
+// own splits to form its factors exp2(m_s - M).  Every load of a batch is
+// issued before any is consumed.  The kernel boundary makes the attention
+// launch's partials visible, so plain loads suffice.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) sdpa_merge_kernel(SdpaArgs a) {
+__global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   constexpr int C4 = 2 * D / 4;          // float4 columns of one output row
-  constexpr int CW = C4 < 16 ? C4 : 16;  // columns per workgroup
-  constexpr int NSL = C4 / CW;           // workgroups per row
-  constexpr int NG = 256 / CW;           // split groups
-  constexpr int UNR = 4;                 // loads in flight per thread
-  __shared__ float lds_m[kMaxSplits];
-  __shared__ float lds_l[kMaxSplits];
-  __shared__ float lds_ML[2];
-  __shared__ __attribute__((aligned(16))) float4 lds_acc[256];
-  const int tid = threadIdx.x;
+  constexpr int CW = C4 < 16 ? C4 : 16;  // columns per wave
+  constexpr int NSL = C4 / CW;           // waves per row
+  constexpr int NGR = 64 / CW;           // split groups
+  constexpr int UNR = 8;                 // partial loads in flight per lane
+  const int lane = threadIdx.x;
   const long vrow = blockIdx.x / NSL;
-  const int col = (blockIdx.x % NSL) * CW + tid % CW;
-  const int grp = tid / CW;
+  const int col = (blockIdx.x % NSL) * CW + lane % CW;
+  const int grp = lane / CW;
   const int ns = a.nsplit;
   const float* po = a.part_o + vrow * ns * 2 * D + col * 4;
   const float* pml = a.part_ml + vrow * ns * 2;
 
-  const float2 ml = tid < ns ? *reinterpret_cast<const float2*>(pml + 2 * tid)
-                             : make_float2(kNegSentinel, 0.f);
   float4 v[UNR];
-#pragma unroll
-  for (int j = 0; j < UNR; ++j) {
-    const int s = grp + j * NG;
-    v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  if (tid < ns) {
-    lds_m[tid] = ml.x;
-    lds_l[tid] = ml.y;
-  }
-  __syncthreads();
-  if (tid < 64) {  // wave 0: row max M and total L = sum_s l_s exp2(m_s - M)
-    float M = kNegSentinel;
-    for (int s = tid; s < ns; s += 64) M = fmaxf(M, lds_m[s]);
-    M = group_max<64>(M);
-    float L = 0.f;
-    for (int s = tid; s < ns; s += 64) L = fmaf(lds_l[s], fast_exp2(lds_m[s] - M), L);
-    L = group_sum<64>(L);
-    if (tid == 0) {
-      lds_ML[0] = M;
-      lds_ML[1] = L;
-    }
-  }
-  __syncthreads();
-  const float M = lds_ML[0];
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < ns; s0 += NG * UNR) {
-    if (s0 > 0) {
-#pragma unroll
-      for (int j = 0; j < UNR; ++j) {
-        const int s = s0 + grp + j * NG;
-        v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+  float mj[UNR];
+  auto load_batch = [&](int s0) {
 #pragma unroll
     for (int j = 0; j < UNR; ++j) {
-      const int s = s0 + grp + j * NG;
-      const float f = s < ns ? fast_exp2(lds_m[s] - M) : 0.f;
+      const int s = s0 + grp + j * NGR;
+      v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      mj[j] = s < ns ? pml[2 * s] : kNegSentinel;
+    }
+  };
+  // (m, l) of splits lane, lane + 64, ... and the first batch together.
+  float2 ml[kMaxSplits / 64];
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / 64; ++i) {
+    const int s = lane + 64 * i;
+    ml[i] = s < ns ? *reinterpret_cast<const float2*>(pml + 2 * s) : make_float2(kNegSentinel, 0.f);
+  }
+  load_batch(0);
+
+  float M = kNegSentinel;
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, ml[i].x);
+  M = group_max<64>(M);
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / 64; ++i) L = fmaf(ml[i].y, fast_exp2(ml[i].x - M), L);
+  L = group_sum<64>(L);
+
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < ns; s0 += NGR * UNR) {
+    if (s0 > 0) load_batch(s0);
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const float f = fast_exp2(mj[j] - M);  // 0 for splits past ns (sentinel m)
       acc.x = fmaf(v[j].x, f, acc.x);
       acc.y = fmaf(v[j].y, f, acc.y);
       acc.z = fmaf(v[j].z, f, acc.z);
       acc.w = fmaf(v[j].w, f, acc.w);
     }
   }
-  lds_acc[tid] = acc;
-  __syncthreads();
-  if (tid < CW) {
-    float4 t = lds_acc[tid];
+  // Sum the NGR split groups of each column (lanes col, col + CW, ...).
 #pragma unroll
-    for (int g = 1; g < NG; ++g) {
-      const float4 u = lds_acc[g * CW + tid];
-      t.x += u.x;
-      t.y += u.y;
-      t.z += u.z;
-      t.w += u.w;
-    }
-    store_y4<T, D>(a, vrow * 2 * D + col * 4, t, lds_ML[1]);
+  for (int off = CW; off < 64; off *= 2) {
+    acc.x += __shfl_xor(acc.x, off);
+    acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off);
+    acc.w += __shfl_xor(acc.w, off);
   }
+  if (grp == 0) store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
 }
 
 template <typename T, int D>
@@ -485,7 +479,7 @@ int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
   constexpr int C4 = 2 * D / 4;
   constexpr int NSL = C4 / (C4 < 16 ? C4 : 16);
   const long rows = (long)a.B * a.Hq * a.S_q;
-  hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3((unsigned)(rows * NSL)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3((unsigned)(rows * NSL)), dim3(64), 0, s, a);
   return check_launch("sdpa split merge");
 }
 
