@@ -82,9 +82,6 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
     }
   }
 
-  const uint16_t* kbase = (const uint16_t*)a.k + (long)bk * a.kv_cap * D;
-  const uint32_t* v1base = (const uint32_t*)a.v1 + (long)bk * a.kv_cap * (D / 2);
-  const uint32_t* v2base = (const uint32_t*)a.v2 + (long)bk * a.kv_cap * (D / 2);
 
   floatx4 acc1[8], acc2[8], accl;
 #pragma unroll
@@ -96,6 +93,14 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   float m_run = kNegSentinel;
   const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
 
+  // Per-split buffer resources: rows past the split's end read 0, and each
+  // address is one 32-bit offset plus an immediate.
+  const long hrow0 = (long)bk * a.kv_cap + r_begin;  // first cache row of this split
+  const unsigned nbytes = (unsigned)(max(r_end - r_begin, 0) * D * 2);
+  const auto rk = stream_rsrc((const uint16_t*)a.k + hrow0 * D, nbytes);
+  const auto rv1 = stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, nbytes);
+  const auto rv2 = stream_rsrc((const uint16_t*)a.v2 + hrow0 * D, nbytes);
+
   // U tiles of 16 rows per wave per iteration: all of their loads are issued
   // before any of them is consumed, so a wave keeps U x 12 KB in flight.
   for (int base = r_begin + wave * 16; base < r_end; base += NW * 16 * U) {
@@ -103,36 +108,21 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
     uint32_t v1w[U][4][4], v2w[U][4][4];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t0 = base + u * NW * 16;
+      const int t0 = base + u * NW * 16 - r_begin;  // split-relative
       // K rows for S^T: row t0 + col (A operand row = lane % 16).
-      const int krow = t0 + col;
-      if (krow < r_end) {
-        const uint16_t* kp = kbase + (long)krow * D + 8 * blk;
+      const unsigned koff = (unsigned)((t0 + col) * D * 2 + 16 * blk);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          ka[u][s] = __builtin_bit_cast(half8_t, ld_stream4(kp + 32 * s));
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, make_uint4(0, 0, 0, 0));
-      }
+      for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, bload4(rk, koff + 64u * s));
       // V rows t0 + 4*blk + r: 16 bytes per lane, dwords 4*col .. 4*col+3
       // (dword 4*col + t holds channels 8*col + 2t, +1); one instruction
       // covers four whole rows.
+      const unsigned voff = (unsigned)((t0 + 4 * blk) * D * 2 + 16 * col);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = t0 + 4 * blk + r;
-        if (row < r_end) {
-          const uint4 w1 = ld_stream4(v1base + (long)row * (D / 2) + 4 * col);
-          const uint4 w2 = ld_stream4(v2base + (long)row * (D / 2) + 4 * col);
-          v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
-          v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
-        } else {
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            v1w[u][r][t] = 0u;
-            v2w[u][r][t] = 0u;
-          }
-        }
+        const uint4 w1 = bload4(rv1, voff + (unsigned)(r * D * 2));
+        const uint4 w2 = bload4(rv2, voff + (unsigned)(r * D * 2));
+        v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
+        v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
       }
     }
 

@@ -122,31 +122,6 @@ __device__ inline float sum_group_columns(float x) {
   return x;
 }
 
-// ------------------------------------------------------------ loads ---
-// Per-split buffer resources: base at the split's first row, range = its
-// rows, so loads past the split's end return 0 with no memory traffic and
-// need no branch.  Cache policy nt: the cache is read once per call.
-constexpr int kCachePolicyStream = 2;  // nt
-
-__device__ inline __amdgpu_buffer_rsrc_t stream_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                           0x00020000);
-}
-// POL: kCachePolicyStream for data read once per call, 0 (cached) where
-// several workgroups read the same rows (head chunks of a verify slab).
-template <int POL = kCachePolicyStream>
-__device__ inline uint4 bload4(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL));
-}
-template <int POL = kCachePolicyStream>
-__device__ inline uint2 bload2(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POL));
-}
-template <int POL = kCachePolicyStream>
-__device__ inline uint32_t bload1(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
-}
-
 // One 16-row tile of the packed cache as one lane loads it.
 //   k[KW]      K codes of row t0 + col, channels 32*blk .. 32*blk+31
 //   v1/v2[4][] V codes of rows t0 + 4*blk + r, channels 8*col .. 8*col+7
