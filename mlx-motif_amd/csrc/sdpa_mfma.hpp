@@ -48,6 +48,7 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   using T = half_t;
   constexpr int D = 128;
   static_assert(GC <= 16, "virtual heads ride the 16 MFMA columns");
+  static_assert(U % 2 == 0, "tiles are computed in pairs");
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;  // MFMA column: virtual head (S^T, P^T, O^T)
@@ -91,7 +92,8 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   }
   accl = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegSentinel;
-  const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+  const half8_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
+                        (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
 
   // Per-split buffer resources: rows past the split's end read 0, and each
   // address is one 32-bit offset plus an immediate.
@@ -126,23 +128,33 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
       }
     }
 
+    // Tiles in pairs: the PV products take both tiles' 32 rows in one
+    // 16x16x32 MFMA (k = 8*blk + j is row 4*blk + j of the pair's first
+    // tile for j < 4, row 4*blk + j - 4 of its second for j >= 4), with one
+    // running-max update per pair.
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t0 = base + u * NW * 16;
-      floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < U; u += 2) {
+      floatx4 sacc[2];
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u][s], qb[s], sacc, 0, 0, 0);
+      for (int v = 0; v < 2; ++v) {
+        sacc[v] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          sacc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u + v][s], qb[s], sacc[v], 0, 0, 0);
+      }
 
-      // Scores of rows t0 + 4*blk + r for head col, log2 units.
-      float sc[4];
+      // Scores of rows t_v + 4*blk + r for head col, log2 units.
+      float sc[8];
       float mx = kNegSentinel;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = t0 + 4 * blk + r;
-        const bool ok = row < r_end && row < lim;
-        sc[r] = ok ? sacc[r] * a.qscale : kNegSentinel;
-        mx = fmaxf(mx, sc[r]);
+      for (int v = 0; v < 2; ++v) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = base + (u + v) * NW * 16 + 4 * blk + r;
+          const bool ok = row < r_end && row < lim;
+          sc[4 * v + r] = ok ? sacc[v][r] * a.qscale : kNegSentinel;
+          mx = fmaxf(mx, sc[4 * v + r]);
+        }
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -157,27 +169,31 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
         accl *= fac;
         m_run = m_new;
       }
-      half4_t pb;
+      half8_t pb;
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        pb[r] = (_Float16)(sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run) : 0.f);
+      for (int j = 0; j < 8; ++j)
+        pb[j] = (_Float16)(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
 
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t sel = h ? 0x07060302u : 0x05040100u;  // hi or lo halves, row r in half r%2
-          const half4_t a1 = __builtin_bit_cast(
-              half4_t, make_uint2(__builtin_amdgcn_perm(v1w[u][1][t], v1w[u][0][t], sel),
-                                  __builtin_amdgcn_perm(v1w[u][3][t], v1w[u][2][t], sel)));
-          const half4_t a2 = __builtin_bit_cast(
-              half4_t, make_uint2(__builtin_amdgcn_perm(v2w[u][1][t], v2w[u][0][t], sel),
-                                  __builtin_amdgcn_perm(v2w[u][3][t], v2w[u][2][t], sel)));
-          acc1[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc1[2 * t + h], 0, 0, 0);
-          acc2[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2, pb, acc2[2 * t + h], 0, 0, 0);
+          const half8_t a1 = __builtin_bit_cast(
+              half8_t, make_uint4(__builtin_amdgcn_perm(v1w[u][1][t], v1w[u][0][t], sel),
+                                  __builtin_amdgcn_perm(v1w[u][3][t], v1w[u][2][t], sel),
+                                  __builtin_amdgcn_perm(v1w[u + 1][1][t], v1w[u + 1][0][t], sel),
+                                  __builtin_amdgcn_perm(v1w[u + 1][3][t], v1w[u + 1][2][t], sel)));
+          const half8_t a2 = __builtin_bit_cast(
+              half8_t, make_uint4(__builtin_amdgcn_perm(v2w[u][1][t], v2w[u][0][t], sel),
+                                  __builtin_amdgcn_perm(v2w[u][3][t], v2w[u][2][t], sel),
+                                  __builtin_amdgcn_perm(v2w[u + 1][1][t], v2w[u + 1][0][t], sel),
+                                  __builtin_amdgcn_perm(v2w[u + 1][3][t], v2w[u + 1][2][t], sel)));
+          acc1[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb, acc1[2 * t + h], 0, 0, 0);
+          acc2[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, pb, acc2[2 * t + h], 0, 0, 0);
         }
       }
-      accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pb, accl, 0, 0, 0);
+      accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, accl, 0, 0, 0);
     }
   }
 
