@@ -35,6 +35,15 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// Lazy rescaling.  The reference point m_run of the online softmax is raised
+// only when a tile's max exceeds it by more than a slack (log2 units); until
+// then p = exp2(s - m_run) may exceed 1, up to 2^slack.  o and l share the
+// reference point, so o / l and the split partials (m_run, l, o) are the
+// same quantities as with an exact running max, and most tiles skip the
+// rescale of the 68 accumulator registers.  The slack only bounds p, which
+// the matrix cores take as fp16: 2^8 leaves fp16 p a wide margin.
+constexpr float kRescaleSlackF16 = 8.f;
+
 // Causal row limit of virtual head vh (see sdpa_dual_v_kernel).
 __device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
   const int s = vh % a.S_q;
@@ -158,7 +167,7 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (__ballot(mx > m_run) != 0) {
+      if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
         const float m_new = fmaxf(m_run, mx);
         const float fac = fast_exp2(m_run - m_new);
 #pragma unroll

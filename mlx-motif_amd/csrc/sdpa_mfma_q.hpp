@@ -22,7 +22,8 @@
 // a byte), and one packed fp16 add or fma recovers u exactly.  V^T fragments
 // (4 rows x 1 channel per lane) come from one code word per row, paired
 // across rows with v_perm_b32.  Everything else (split plan, online softmax
-// in log2 units, workgroup epilogue) matches the fp16-cache kernel.
+// in log2 units with lazy rescaling, workgroup epilogue) matches the
+// fp16-cache kernel.
 #pragma once
 
 #include "sdpa_mfma.hpp"
@@ -205,6 +206,11 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int KW = Tile::KW;
   constexpr int VW = Tile::VW;
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
+  // Lazy-rescale slack (see kRescaleSlackF16): here p also multiplies the V
+  // scale in fp16, so p * s must stay finite.  An fp16 cache row spans at
+  // most 2 * 65504, so s <= 131008 / 15 (q4) or / 255 (q8), and 2^slack * s
+  // stays below 65504 with slack 2 (q4) or 6 (q8).
+  constexpr float kSlack = BITS == 4 ? 2.f : 6.f;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -359,7 +365,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (__ballot(mx > m_run) != 0) {
+      if (__ballot(mx > m_run + kSlack) != 0) {
         const float m_new = fmaxf(m_run, mx);
         const float fac = fast_exp2(m_run - m_new);
 #pragma unroll
@@ -407,7 +413,8 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   };
 
   // Two register sets in turn: the loads of the next U tiles are in flight
-  // while the current ones are computed.
+  // while the current ones are computed.  (A third set, with two sets'
+  // loads in flight, measured slower for q4.)
   constexpr int kStep = NW * 16 * U;
   Tile ta[U], tb[U];
   int t0 = wave * 16;
