@@ -239,28 +239,6 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const int nrows = max(r_end - r_begin, 0);
 
-  // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
-  // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
-  // column's group.  qsum: sum of q_h over the column's group.
-  half8_t qb[4];
-  float qsum = 0.f;
-  {
-    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (h < nvh ? h : 0)) * D + 32 * blk;
-    const bool mine = col_used && (32 * blk) / GS == grp;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const half8_t raw = __builtin_bit_cast(half8_t, *reinterpret_cast<const uint4*>(qp + 8 * s));
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const _Float16 v = mine ? raw[BITS == 4 ? q4_order(j) : j] : (_Float16)0.f;
-        qb[s][j] = v;
-        qsum += (float)v;
-      }
-    }
-    qsum += __shfl_xor(qsum, 16);
-    qsum += __shfl_xor(qsum, 32);
-  }
-
   const long hrow0 = (long)bk * a.kv_cap + r_begin;  // first cache row of this split
   const auto rk = stream_rsrc(a.kd + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
   const auto rv1 = stream_rsrc(a.v1d + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
@@ -306,6 +284,39 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       for (int t = 0; t < 6; ++t) load_scales<NG, POL>(T[u].s[t], rs[t], vrow, gsel);
     }
   };
+
+  // The first tile set's loads are issued before q is consumed, so their
+  // latency and q's overlap.
+  Tile ta[U], tb[U];
+  int t0 = wave * 16;
+  uint4 qraw[4];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (h < nvh ? h : 0)) * D + 32 * blk;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qraw[s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
+  }
+  load_tiles(ta, t0);
+
+  // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
+  // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
+  // column's group.  qsum: sum of q_h over the column's group.
+  half8_t qb[4];
+  float qsum = 0.f;
+  {
+    const bool mine = col_used && (32 * blk) / GS == grp;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const half8_t raw = __builtin_bit_cast(half8_t, qraw[s]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const _Float16 v = mine ? raw[BITS == 4 ? q4_order(j) : j] : (_Float16)0.f;
+        qb[s][j] = v;
+        qsum += (float)v;
+      }
+    }
+    qsum += __shfl_xor(qsum, 16);
+    qsum += __shfl_xor(qsum, 32);
+  }
 
   floatx4 acc1[8], acc2[8], accl;
 #pragma unroll
@@ -416,9 +427,6 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // while the current ones are computed.  (A third set, with two sets'
   // loads in flight, measured slower for q4.)
   constexpr int kStep = NW * 16 * U;
-  Tile ta[U], tb[U];
-  int t0 = wave * 16;
-  load_tiles(ta, t0);
   while (t0 < nrows) {
     load_tiles(tb, t0 + kStep);
     compute_tiles(ta, t0);
