@@ -122,6 +122,59 @@ def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=H
     return [mk(*s) for s in sets], (q, sets)
 
 
+def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True, gr=4):
+    """One GDA decode-attention step per call over distinct layer caches
+    (k1, k2, v1, v2 of HKV heads): motif_gda_decode (fused) or the
+    reference's three calls (two motif_sdpa_dual_v + motif_gda_post_split)."""
+    from mlx_motif import _native
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(99)
+    q1 = torch.randn((B, HKV * gr, 1, D), generator=g, device=dev).half()
+    q2 = torch.randn((B, HKV, 1, D), generator=g, device=dev).half()
+    w = torch.rand(2 * D, generator=g, device=dev).half()
+    lam = torch.tensor([0.37], dtype=torch.float32, device=dev)
+    sets = [tuple(torch.randn((B, HKV, cap, D), generator=g, device=dev).half()
+                  for _ in range(4)) for _ in range(nsets)]
+    y = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
+    o = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
+    n = torch.empty((B, HKV, 1, 2 * D), dtype=torch.float16, device=dev)
+    nbytes = max(lib.motif_gda_decode_workspace_bytes(B, HKV, gr, kv_len, D),
+                 lib.motif_sdpa_workspace_bytes(B, HKV * gr, HKV, 1, kv_len, D))
+    ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
+    scale = 1.0 / D ** 0.5
+
+    def mk(k1, k2, v1, v2):
+        def call():
+            st = torch.cuda.current_stream().cuda_stream
+            if fused:
+                _native.check(lib.motif_gda_decode(
+                    q1.data_ptr(), q2.data_ptr(), k1.data_ptr(), k2.data_ptr(), v1.data_ptr(),
+                    v2.data_ptr(), w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B,
+                    HKV, gr, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
+                return
+            _native.check(lib.motif_sdpa_dual_v(
+                q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), v2.data_ptr(), o.data_ptr(), 0, B,
+                HKV * gr, HKV, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
+            _native.check(lib.motif_sdpa_dual_v(
+                q2.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr(), n.data_ptr(), 0, B,
+                HKV, HKV, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
+            _native.check(lib.motif_gda_post_split(
+                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), 0, B, HKV * gr, HKV, gr,
+                1, 2 * D, lam.data_ptr(), 0.8, 1e-5, st))
+        return call
+
+    return [mk(*t) for t in sets], (q1, q2, w, lam, sets, y, o, n, ws)
+
+
+def decode_bytes(kv_len: int, fused: bool, gr: int = 4) -> int:
+    """Cache bytes of one decode step: 4 streams fused, 6 for the three calls
+    (v1 and v2 read by both passes), plus q, y and the attention outputs."""
+    streams = 4 if fused else 6
+    heads = HKV * gr + HKV
+    return streams * B * HKV * kv_len * D * 2 + heads * D * 2 + HKV * gr * 2 * D * 2
+
+
 def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
     from mlx_motif import _native
     from mlx_motif.kernels import quantize
@@ -333,6 +386,15 @@ def run_extra(torch, lib, dev, args):
     report("sdpa_dual_v f16 kv3204 x48 layers", time_calls(torch, calls, 48 * 4, warm),
            alg_bytes("f16", 3204))
     del calls, keep
+    # one GDA decode-attention step (origin + noise passes + gda_post_split)
+    # at kv_len 16000: fused entry vs the reference's three calls; GB/s over
+    # the bytes each one must move (4 vs 6 cache streams)
+    for fused in (True, False):
+        calls, keep = make_decode_calls(torch, lib, dev, 6, fused=fused)
+        report(f"gda decode step kv16000 ({'fused' if fused else 'three calls'})",
+               time_calls(torch, calls, steps, warm), decode_bytes(KV_LEN, fused))
+        del calls, keep
+        torch.cuda.empty_cache()
     # verify slab: 5 rows over a q8 cache of 32768 rows
     calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
     report("verify slab q8 5 rows kv32768", time_calls(torch, calls, steps, warm),

@@ -176,6 +176,34 @@ int motif_gda_post(const void* merged, const void* subln_w, void* y, int dtype, 
                    float one_minus_lambda_init, float eps, void* stream);
 
 /* ------------------------------------------------------------------------ *
+ * One GDA decode-attention step of a layer over the fp16/bf16/fp32 4-slot
+ * cache: the origin pass sdpa_dual_v(q1, k1, v1, v2), the noise pass
+ * sdpa_dual_v(q2, k2, v1, v2) and gda_post_split on their outputs.
+ * Replaces the DUAL_V caller sequence of src/mlx_motif/model.py:749-768
+ * (two sdpa_dual_v calls and gda_post_split); the reference has no single
+ * kernel for it.  For the fp16 cache at D = 128 it runs as two launches:
+ * one attention launch reads each KV head's k1, k2, v1 and v2 rows once for
+ * both passes (4 cache streams instead of the calls' 6), and the split merge
+ * applies the epilogue.  Other dtypes and head dims compose the separate
+ * calls on the device.
+ *   q1 (B, Hkv*gr, 1, D), q2 (B, Hkv, 1, D)          dtype
+ *   k1, k2, v1, v2 (B, Hkv, kv_cap, D)               dtype
+ *   subln_w (2D) dtype; lambda_full: device pointer to ONE fp32 value
+ *   y (B, Hkv*gr, 1, 2D)                             dtype
+ * Origin head h pairs with noise head h / gr (gda.py:248).  The attention
+ * outputs are rounded to dtype before the epilogue, as the reference's are.
+ * Workspace: motif_gda_decode_workspace_bytes(B, Hkv, gr, kv_len, D) bytes,
+ * 256-byte aligned, zeroed before its first use.
+ * ------------------------------------------------------------------------ */
+size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int D);
+
+int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void* k2,
+                     const void* v1, const void* v2, const void* subln_w,
+                     const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                     int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                     float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ *
  * Fused PolyNorm (polynorm, src/mlx_motif/kernels/mlp.py:119-157):
  *   y = w0*x^3*rsqrt(mean(x^6)+eps) + w1*x^2*rsqrt(mean(x^4)+eps)
  *     + w2*x*rsqrt(mean(x^2)+eps) + b

@@ -25,6 +25,13 @@ int launch_sdpa_merge_f16(const SdpaArgs& a, int D, hipStream_t s);
 int launch_sdpa_merge_bf16(const SdpaArgs& a, int D, hipStream_t s);
 int launch_sdpa_merge_f32(const SdpaArgs& a, int D, hipStream_t s);
 
+// Fused GDA decode step (attention + merge/epilogue launches); only the
+// f16 instance has kernels (head_dim 128), the others return
+// MOTIF_ERR_UNSUPPORTED.
+int launch_gda_decode_f16(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
+int launch_gda_decode_bf16(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
+int launch_gda_decode_f32(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
+
 // Pointer alignment (bytes) the kernels need for head dim D.
 int sdpa_fp_align(int dtype, int D);
 int sdpa_q_align(int D, int bits);

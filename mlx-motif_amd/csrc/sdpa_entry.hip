@@ -155,11 +155,123 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
 }
 
+// ------------------------------------------------ fused GDA decode step ---
+// Partial rows of the fused path: (b, KV head, column), G + 1 columns.
+struct GdaDecodeLayout {
+  SdpaPlan plan;
+  size_t counter_bytes, o_bytes, ml_bytes, fused_bytes;
+  size_t sdpa_bytes, yo_bytes, yn_bytes, composed_bytes;
+};
+
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int D) {
+  GdaDecodeLayout L{};
+  // One virtual head per KV head in the planner: the fused kernel runs one
+  // workgroup per (b, KV head, split), like the unfused origin pass.
+  L.plan = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, 0, 0);
+  const size_t prow = (size_t)B * Hkv * (gr + 1);
+  L.counter_bytes = round256(prow * sizeof(unsigned));
+  L.o_bytes = round256(prow * L.plan.nsplit * 2 * D * sizeof(float));
+  L.ml_bytes = round256(prow * L.plan.nsplit * 2 * sizeof(float));
+  L.fused_bytes = L.counter_bytes + L.o_bytes + L.ml_bytes;
+  // Composed path: both attention calls' workspace, then o and n (fp32 bound).
+  const size_t w1 = motif_sdpa_workspace_bytes(B, Hkv * gr, Hkv, 1, kv_len, D);
+  const size_t w2 = motif_sdpa_workspace_bytes(B, Hkv, Hkv, 1, kv_len, D);
+  L.sdpa_bytes = round256(w1 > w2 ? w1 : w2);
+  L.yo_bytes = round256((size_t)B * Hkv * gr * 2 * D * sizeof(float));
+  L.yn_bytes = round256((size_t)B * Hkv * 2 * D * sizeof(float));
+  L.composed_bytes = L.sdpa_bytes + L.yo_bytes + L.yn_bytes;
+  return L;
+}
+
 }  // namespace motif
 
 using namespace motif;
 
 extern "C" {
+
+size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int D) {
+  if (B <= 0 || Hkv <= 0 || gr <= 0 || D <= 0 || kv_len < 0) return 0;
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  return L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
+}
+
+int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void* k2,
+                     const void* v1, const void* v2, const void* subln_w,
+                     const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                     int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                     float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* name = "gda_decode";
+  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
+                "%s: unknown dtype code %d", name, dtype);
+  MOTIF_REQUIRE(B >= 1 && Hkv >= 1 && gr >= 1, "%s: B, H_kv, gr must be >= 1", name);
+  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
+  MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
+                "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
+  MOTIF_REQUIRE(q1 && q2 && y && subln_w && lambda_full &&
+                    (kv_cap == 0 || (k1 && k2 && v1 && v2)),
+                "%s: null pointer", name);
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  const size_t need = L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes needed, %zu given", name, need,
+              workspace == nullptr ? (size_t)0 : workspace_bytes);
+    return MOTIF_ERR_WORKSPACE;
+  }
+  MOTIF_REQUIRE(aligned(workspace, 256), "%s: workspace must be 256-byte aligned", name);
+  hipStream_t s = (hipStream_t)stream;
+  const int gc = gr + 1 <= 2 ? 2 : gr + 1 <= 4 ? 4 : gr + 1 <= 8 ? 8 : 16;
+  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+                     aligned(q1, 16) && aligned(q2, 16) && aligned(k1, 16) && aligned(k2, 16) &&
+                     aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8);
+  if (fused) {
+    SdpaArgs a{};
+    a.q = q1;
+    a.q2 = q2;
+    a.k = k1;
+    a.k2 = k2;
+    a.v1 = v1;
+    a.v2 = v2;
+    a.y = y;
+    a.B = B;
+    a.Hkv = Hkv;
+    a.Hq = Hkv * gr;
+    a.S_q = 1;
+    a.G = gr;
+    a.GV = gr + 1;
+    a.nchunk = 1;
+    a.kv_cap = kv_cap;
+    a.kv_len = kv_len;
+    a.causal = 0;
+    a.nsplit = L.plan.nsplit;
+    a.rows_per_split = L.plan.rows_per_split;
+    a.fused_merge = 0;
+    a.qscale = scale * 1.4426950408889634f;
+    char* w = (char*)workspace;
+    a.counters = (unsigned*)w;
+    a.part_o = (float*)(w + L.counter_bytes);
+    a.part_ml = (float*)(w + L.counter_bytes + L.o_bytes);
+    a.gda_w = subln_w;
+    a.gda_lambda = lambda_full;
+    a.gda_scale = one_minus_lambda_init;
+    a.gda_eps = eps;
+    return launch_gda_decode_f16(a, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+  }
+  // Composition of the separate calls, every step on the device.
+  char* w = (char*)workspace;
+  void* yo = w + L.sdpa_bytes;
+  void* yn = w + L.sdpa_bytes + L.yo_bytes;
+  int rc = motif_sdpa_dual_v(q1, k1, v1, v2, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap, kv_len,
+                             scale, workspace, L.sdpa_bytes, stream);
+  if (rc != MOTIF_OK) return rc;
+  rc = motif_sdpa_dual_v(q2, k2, v1, v2, yn, dtype, B, Hkv, Hkv, D, kv_cap, kv_len, scale,
+                         workspace, L.sdpa_bytes, stream);
+  if (rc != MOTIF_OK) return rc;
+  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
+                              lambda_full, one_minus_lambda_init, eps, stream);
+}
 
 int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
                       int dtype, int B, int Hq, int Hkv, int D, int kv_cap, int kv_len,

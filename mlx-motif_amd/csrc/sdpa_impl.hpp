@@ -366,13 +366,14 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
 // write y (single split) or publish this split's partial with 16-byte
 // write-through stores and, in the workgroup that arrives last for its
 // (b, KV head, chunk), merge all splits.  Called by every thread of the
-// workgroup after a barrier.
-template <typename T, int D, int GC, int NW>
+// workgroup after a barrier.  PARTIALS: always publish partials (also for a
+// single split) and leave the merge to a second launch.
+template <typename T, int D, int GC, int NW, bool PARTIALS = false>
 __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * D + kLdsPad],
                             const float (&lds_m)[NW][GC], const float (&lds_l)[NW][GC],
                             long qrow0, int nvh, int split, int unit) {
   constexpr int C4 = 2 * D / 4;
-  const bool single = a.nsplit == 1;
+  const bool single = !PARTIALS && a.nsplit == 1;
   const int ns = a.nsplit;
   // (single split: no workspace, empty resources that are never used)
   const auto ro = part_rsrc(single ? nullptr : a.part_o + qrow0 * ns * 2 * D,
@@ -404,7 +405,7 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
       if (c == 0) store_through2(rml, (unsigned)((g * ns + split) * 8), make_float2(M, L));
     }
   }
-  if (single || !a.fused_merge) return;  // sdpa_merge_kernel combines the splits
+  if (PARTIALS || single || !a.fused_merge) return;  // a merge launch combines the splits
 
   // ---- last workgroup of this (b, KV head, chunk) combines all splits.
   __shared__ int is_last;
@@ -431,27 +432,32 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
 // own splits to form its factors exp2(m_s - M).  Every load of a batch is
 // issued before any is consumed.  The kernel boundary makes the attention
 // launch's partials visible, so plain loads suffice.
-template <typename T, int D>
-__global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
-  constexpr int C4 = 2 * D / 4;          // float4 columns of one output row
-  constexpr int CW = C4 < 16 ? C4 : 16;  // columns per wave
-  constexpr int NSL = C4 / CW;           // waves per row
-  constexpr int NGR = 64 / CW;           // split groups
-  constexpr int UNR = 8;                 // partial loads in flight per lane
-  const int lane = threadIdx.x;
-  const long vrow = blockIdx.x / NSL;
-  const int col = (blockIdx.x % NSL) * CW + lane % CW;
-  const int grp = lane / CW;
+template <int D>
+struct MergeShape {
+  static constexpr int C4 = 2 * D / 4;          // float4 columns of one output row
+  static constexpr int CW = C4 < 16 ? C4 : 16;  // columns per wave
+  static constexpr int NSL = C4 / CW;           // waves per row
+  static constexpr int NGR = 64 / CW;           // split groups
+  static constexpr int UNR = 8;                 // partial loads in flight per lane
+};
+
+// Unnormalised merged accumulator of float4 column col of partial row vrow
+// (every lane of the column gets it) and the row's total L.
+template <int D>
+__device__ inline float4 merge_row_column(const SdpaArgs& a, long vrow, int col, int lane,
+                                          float& L_out) {
+  using S = MergeShape<D>;
+  const int grp = lane / S::CW;
   const int ns = a.nsplit;
   const float* po = a.part_o + vrow * ns * 2 * D + col * 4;
   const float* pml = a.part_ml + vrow * ns * 2;
 
-  float4 v[UNR];
-  float mj[UNR];
+  float4 v[S::UNR];
+  float mj[S::UNR];
   auto load_batch = [&](int s0) {
 #pragma unroll
-    for (int j = 0; j < UNR; ++j) {
-      const int s = s0 + grp + j * NGR;
+    for (int j = 0; j < S::UNR; ++j) {
+      const int s = s0 + grp + j * S::NGR;
       v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
                     : make_float4(0.f, 0.f, 0.f, 0.f);
       mj[j] = s < ns ? pml[2 * s] : kNegSentinel;
@@ -473,13 +479,13 @@ __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   float L = 0.f;
 #pragma unroll
   for (int i = 0; i < kMaxSplits / 64; ++i) L = fmaf(ml[i].y, fast_exp2(ml[i].x - M), L);
-  L = group_sum<64>(L);
+  L_out = group_sum<64>(L);
 
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = 0; s0 < ns; s0 += NGR * UNR) {
+  for (int s0 = 0; s0 < ns; s0 += S::NGR * S::UNR) {
     if (s0 > 0) load_batch(s0);
 #pragma unroll
-    for (int j = 0; j < UNR; ++j) {
+    for (int j = 0; j < S::UNR; ++j) {
       const float f = fast_exp2(mj[j] - M);  // 0 for splits past ns (sentinel m)
       acc.x = fmaf(v[j].x, f, acc.x);
       acc.y = fmaf(v[j].y, f, acc.y);
@@ -489,13 +495,24 @@ __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   }
   // Sum the NGR split groups of each column (lanes col, col + CW, ...).
 #pragma unroll
-  for (int off = CW; off < 64; off *= 2) {
+  for (int off = S::CW; off < 64; off *= 2) {
     acc.x += __shfl_xor(acc.x, off);
     acc.y += __shfl_xor(acc.y, off);
     acc.z += __shfl_xor(acc.z, off);
     acc.w += __shfl_xor(acc.w, off);
   }
-  if (grp == 0) store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
+  return acc;
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
+  using S = MergeShape<D>;
+  const int lane = threadIdx.x;
+  const long vrow = blockIdx.x / S::NSL;
+  const int col = (blockIdx.x % S::NSL) * S::CW + lane % S::CW;
+  float L;
+  const float4 acc = merge_row_column<D>(a, vrow, col, lane, L);
+  if (lane < S::CW) store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
 }
 
 template <typename T, int D>
@@ -505,6 +522,77 @@ int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
   const long rows = (long)a.B * a.Hq * a.S_q;
   hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3((unsigned)(rows * NSL)), dim3(64), 0, s, a);
   return check_launch("sdpa split merge");
+}
+
+// --------------------------------------------- fused GDA decode merge ---
+// Second launch of a fused GDA decode step (origin and noise passes share
+// one attention launch): one workgroup per origin row (b, h) merges the
+// splits of that row and of its noise head h / G, rounds both to T (the
+// reference's attention outputs are T tensors), and applies gda_post_split
+// (src/mlx_motif/kernels/gda.py:131-192):
+//   d = o - lambda * n,  y = T(d * rsqrt(mean(d^2) + eps) * w * (1 - lambda_init)).
+// Wave w of the NSL waves holds float4 columns [w*CW, (w+1)*CW) of the 2D
+// channels; the sum of squares meets in LDS.
+template <typename T, int D>
+__global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kernel(SdpaArgs a) {
+  using S = MergeShape<D>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long orow = blockIdx.x;  // (b, h) over B * Hq
+  const long b = orow / a.Hq;
+  const int h = (int)(orow - b * a.Hq);
+  const int j = h / a.G;
+  const long prow0 = (b * a.Hkv + j) * (a.G + 1);
+  const int col = wave * S::CW + lane % S::CW;
+  const bool head_lane = lane < S::CW;  // one lane per column stores
+
+  float Lo, Ln;
+  const float4 ao = merge_row_column<D>(a, prow0 + (h - j * a.G), col, lane, Lo);
+  const float4 an = merge_row_column<D>(a, prow0 + a.G, col, lane, Ln);
+  const float lam = *a.gda_lambda;
+  auto out_t = [](float v, float L) {  // o / l rounded to T (o when l == 0)
+    const float x = L == 0.f ? v : v / L;
+    if constexpr (Elem<T>::kBytes == 2) return Elem<T>::to_f32(Elem<T>::from_f32(x));
+    return x;
+  };
+  const float o4[4] = {out_t(ao.x, Lo), out_t(ao.y, Lo), out_t(ao.z, Lo), out_t(ao.w, Lo)};
+  const float n4[4] = {out_t(an.x, Ln), out_t(an.y, Ln), out_t(an.z, Ln), out_t(an.w, Ln)};
+  float d[4];
+  float ssq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    d[e] = o4[e] - lam * n4[e];
+    ssq = fmaf(d[e], d[e], ssq);
+  }
+  ssq = group_sum<64>(head_lane ? ssq : 0.f);
+  __shared__ float lds_ss[S::NSL];
+  if (lane == 0) lds_ss[wave] = ssq;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < S::NSL; ++w) tot += lds_ss[w];
+  const float rms_inv = rsqrtf(tot / (float)(2 * D) + a.gda_eps);
+  if (!head_lane) return;
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    y[e] = d[e] * rms_inv * Elem<T>::load(a.gda_w, col * 4 + e) * a.gda_scale;
+  const long off = orow * 2 * D + col * 4;
+  if constexpr (Elem<T>::kBytes == 2) {
+    *reinterpret_cast<uint2*>((uint16_t*)a.y + off) = make_uint2(
+        (uint32_t)Elem<T>::from_f32(y[0]) | ((uint32_t)Elem<T>::from_f32(y[1]) << 16),
+        (uint32_t)Elem<T>::from_f32(y[2]) | ((uint32_t)Elem<T>::from_f32(y[3]) << 16));
+  } else {
+    *reinterpret_cast<float4*>((float*)a.y + off) = make_float4(y[0], y[1], y[2], y[3]);
+  }
+}
+
+template <typename T, int D>
+int launch_gda_decode_merge_d(const SdpaArgs& a, hipStream_t s) {
+  const long rows = (long)a.B * a.Hq;
+  hipLaunchKernelGGL((gda_decode_merge_kernel<T, D>), dim3((unsigned)rows),
+                     dim3(MergeShape<D>::NSL * 64), 0, s, a);
+  return check_launch("gda decode merge");
 }
 
 // ---------------------------------------------------------------- kernel --

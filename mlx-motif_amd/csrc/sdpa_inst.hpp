@@ -83,4 +83,19 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
   return MOTIF_ERR_UNSUPPORTED;
 }
 
+// Fused GDA decode step: one attention launch for the origin and noise
+// passes, then the merge + gda_post_split launch.  Compiled for the fp16
+// cache at head_dim 128 only; the entry point composes the separate calls
+// otherwise.
+int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int nblocks,
+                                               hipStream_t s) {
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
+    const int rc = launch_gda_decode_mfma_f16(a, gc, nblocks, s);
+    if (rc != MOTIF_OK) return rc;
+    return launch_gda_decode_merge_d<half_t, 128>(a, s);
+  }
+  set_error("gda_decode: no fused variant for this element type");
+  return MOTIF_ERR_UNSUPPORTED;
+}
+
 }  // namespace motif

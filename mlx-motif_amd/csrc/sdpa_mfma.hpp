@@ -51,7 +51,10 @@ __device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
   return L < 0 ? 0 : (L > a.kv_len ? a.kv_len : L);
 }
 
-template <int GC, int NW, int U>
+// DUAL: fused GDA decode step.  Columns 0..G-1 are the origin heads of the
+// KV head (scores from k), column G its noise head (scores from k2); both
+// share the V1/V2 rows, and the partials go to the fused merge launch.
+template <int GC, int NW, int U, bool DUAL = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 sdpa_mfma_f16_kernel(SdpaArgs a) {
   using T = half_t;
@@ -71,7 +74,9 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   const int kvh = bk % a.Hkv;
   const int vh0 = chunk * GC;
   const int nvh = min(GC, a.GV - vh0);
-  const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
+  // First output row: y row (non-DUAL) or partial row (DUAL) of column 0.
+  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
+                          : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
   int max_lim = 0;
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
@@ -85,6 +90,11 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   half8_t qb[4];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
+    if constexpr (DUAL) {
+      qp = col < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + col) * D
+                     : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      qp += 8 * blk;
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
@@ -111,11 +121,13 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   const auto rk = stream_rsrc((const uint16_t*)a.k + hrow0 * D, nbytes);
   const auto rv1 = stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, nbytes);
   const auto rv2 = stream_rsrc((const uint16_t*)a.v2 + hrow0 * D, nbytes);
+  const auto rk2 = DUAL ? stream_rsrc((const uint16_t*)a.k2 + hrow0 * D, nbytes) : rk;
 
   // U tiles of 16 rows per wave per iteration: all of their loads are issued
   // before any of them is consumed, so a wave keeps U x 12 KB in flight.
   for (int base = r_begin + wave * 16; base < r_end; base += NW * 16 * U) {
     half8_t ka[U][4];
+    half8_t ka2[DUAL ? U : 1][4];
     uint32_t v1w[U][4][4], v2w[U][4][4];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -124,6 +136,11 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
       const unsigned koff = (unsigned)((t0 + col) * D * 2 + 16 * blk);
 #pragma unroll
       for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, bload4(rk, koff + 64u * s));
+      if constexpr (DUAL) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          ka2[u][s] = __builtin_bit_cast(half8_t, bload4(rk2, koff + 64u * s));
+      }
       // V rows t0 + 4*blk + r: 16 bytes per lane, dwords 4*col .. 4*col+3
       // (dword 4*col + t holds channels 8*col + 2t, +1); one instruction
       // covers four whole rows.
@@ -150,6 +167,13 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
           sacc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u + v][s], qb[s], sacc[v], 0, 0, 0);
+        if constexpr (DUAL) {
+          floatx4 s2 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka2[u + v][s], qb[s], s2, 0, 0, 0);
+          if (col == a.G) sacc[v] = s2;
+        }
       }
 
       // Scores of rows t_v + 4*blk + r for head col, log2 units.
@@ -231,7 +255,7 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
     }
   }
   __syncthreads();
-  wg_epilogue<T, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+  wg_epilogue<T, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
 // fp16 cache, head_dim 128, <= 8 virtual heads per workgroup.
@@ -267,6 +291,21 @@ inline int launch_sdpa_mfma_f16(const SdpaArgs& a, int gc, int waves, int nblock
       return MOTIF_ERR_UNSUPPORTED;
   }
   return check_launch("sdpa_dual_v (mfma)");
+}
+
+// Fused GDA decode step, fp16 cache, head_dim 128: gc = columns (G + 1,
+// rounded up to 2, 4, 8 or 16).
+inline int launch_gda_decode_mfma_f16(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
+  switch (gc) {
+    case 2: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<8, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 16: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<16, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a); break;
+    default:
+      set_error("gda_decode: no fused variant for %d columns", gc);
+      return MOTIF_ERR_UNSUPPORTED;
+  }
+  return check_launch("gda_decode (mfma)");
 }
 
 }  // namespace motif

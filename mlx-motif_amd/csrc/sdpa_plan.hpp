@@ -38,6 +38,17 @@ struct SdpaArgs {
   int group_size;
   int fused_merge;  // 1: last-arriving workgroup merges; 0: sdpa_merge_kernel does
   float qscale;     // softmax scale * log2(e)
+  // Fused GDA decode step (origin and noise passes in one launch, then the
+  // merge applies gda_post_split): q holds the origin queries (B, Hq, 1, D)
+  // with Hq = Hkv * G, q2 the noise queries (B, Hkv, 1, D), k the origin
+  // keys, k2 the noise keys; partial rows are (b, KV head, column) with
+  // columns 0..G-1 the origin heads and G the noise head.
+  const void* q2;
+  const void* k2;
+  const void* gda_w;         // (2D) subln weight
+  const float* gda_lambda;   // device pointer to lambda_full (fp32)
+  float gda_scale;           // 1 - lambda_init
+  float gda_eps;
 };
 
 struct SdpaPlan {

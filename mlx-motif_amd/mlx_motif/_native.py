@@ -69,6 +69,11 @@ _SIGNATURES = {
         _c_int,
         [_vp] * 3 + [_c_int] * 6 + [_vp, _c_f, _c_f, _vp],
     ),
+    "motif_gda_decode_workspace_bytes": (_c_sz, [_c_int] * 5),
+    "motif_gda_decode": (
+        _c_int,
+        [_vp] * 8 + [_c_f, _c_f, _vp] + [_c_int] * 7 + [_c_f, _vp, _c_sz, _vp],
+    ),
     "motif_polynorm": (_c_int, [_vp] * 4 + [_c_int, _c_i64, _c_int, _c_f, _vp]),
     "motif_set_tuning": (_c_int, [ctypes.c_char_p, _c_int]),
 }

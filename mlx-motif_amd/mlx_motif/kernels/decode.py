@@ -1,0 +1,84 @@
+"""One GDA decode-attention step of a layer: the origin and noise dual-V
+passes and the ``gda_post_split`` epilogue in one call.
+
+The reference runs this as three kernel calls (DUAL_V path of
+``src/mlx_motif/model.py:749-768``)::
+
+    attn_origin = sdpa_dual_v(q1, k1, v1, v2, scale, kv_len=kv_seq)
+    attn_noise = sdpa_dual_v(q2, k2, v1, v2, scale, kv_len=kv_seq)
+    out = gda_post_split(attn_origin, attn_noise, subln.weight, lam, lambda_init, gr, eps)
+
+``gda_decode_attention`` returns the same ``out``.  On the fp16 cache at
+head_dim 128, ``motif_gda_decode`` serves both passes from one attention
+launch that reads each KV head's k1, k2, v1 and v2 rows once (the separate
+calls read v1 and v2 twice), and applies the epilogue in the split merge.
+Other shapes compose the separate native calls inside the library.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _native
+from . import _common
+from .attention import sdpa_dual_v_reference
+from .gda import gda_post_split_reference
+
+
+def gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale: float, subln_weight,
+                                   lambda_full, lambda_init: float, gr: int, eps: float = 1e-5,
+                                   kv_len: int | None = None):
+    """Torch-op composition of the reference's three calls; the attention
+    outputs are rounded to ``q1.dtype`` as the reference's kernels return
+    them, and the epilogue's fp32 result is rounded to ``q1.dtype``."""
+    if kv_len is None:
+        kv_len = k1.shape[2]
+    sl = (Ellipsis, slice(0, kv_len), slice(None))
+    o = sdpa_dual_v_reference(q1, k1[sl], v1[sl], v2[sl], scale).to(q1.dtype)
+    n = sdpa_dual_v_reference(q2, k2[sl], v1[sl], v2[sl], scale).to(q1.dtype)
+    y = gda_post_split_reference(o, n, subln_weight.to(q1.dtype), lambda_full, lambda_init, gr,
+                                 eps)
+    return y.to(q1.dtype)
+
+
+def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lambda_full,
+                         lambda_init: float, gr: int, eps: float = 1e-5,
+                         kv_len: int | None = None):
+    """``q1`` (B, H_kv*gr, 1, D) origin queries, ``q2`` (B, H_kv, 1, D) noise
+    queries; ``k1, k2, v1, v2`` (B, H_kv, KV_cap, D) full-capacity 4-slot
+    cache buffers with ``kv_len`` live rows (default ``KV_cap``).  Returns
+    (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
+    if kv_len is None:
+        kv_len = k1.shape[2]
+    if _common._DISABLE:
+        return gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale, subln_weight,
+                                              lambda_full, lambda_init, gr, eps, kv_len)
+    B, H_o, S_q, D = q1.shape
+    _, H_kv, KV_cap, _ = k1.shape
+    assert S_q == 1 and q2.shape[2] == 1, "gda_decode_attention is decode-only"
+    assert D % 32 == 0, f"D={D} must be a multiple of 32"
+    assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
+    assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
+    for t in (k2, v1, v2):
+        assert t.shape == (B, H_kv, KV_cap, D), "k2,v1,v2 must match (B, H_kv, KV_cap, D)"
+    assert 0 <= kv_len <= KV_cap, f"kv_len={kv_len} must be in [0, {KV_cap}]"
+    dev = _native.require_device(q1, q2, k1, k2, v1, v2)
+    for t in (q2, k1, k2, v1, v2):
+        if t.dtype != q1.dtype:
+            raise TypeError(f"dtype {t.dtype} must match q1 dtype {q1.dtype}")
+    q1, q2, k1, k2, v1, v2 = (_common.contiguous(t) for t in (q1, q2, k1, k2, v1, v2))
+    w = subln_weight.to(device=dev, dtype=q1.dtype).contiguous()
+    lam = _common.f32_scalar_tensor(lambda_full, dev)
+    y = torch.empty((B, H_o, 1, 2 * D), dtype=q1.dtype, device=dev)
+    lib = _native.lib()
+    n = lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D)
+    ws = _native.workspace(dev, n)
+    _native.check(
+        lib.motif_gda_decode(
+            q1.data_ptr(), q2.data_ptr(), k1.data_ptr(), k2.data_ptr(), v1.data_ptr(),
+            v2.data_ptr(), w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps),
+            y.data_ptr(), _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len,
+            float(scale), ws.data_ptr(), ws.numel(), _native.stream_of(dev),
+        )
+    )
+    return y

@@ -39,6 +39,11 @@ How each function is pinned (tests/test_oracle.py):
   gda_post_split     closed form: rows of the output have RMS equal to
                      |w*(1-lambda_init)| when w is constant; lambda=0 reduces
                      to RMSNorm; gr broadcasting == explicit repeat.
+  gda_decode_attention
+                     a composition of the two functions above (pinned as
+                     stated), in the order and with the rounding points of
+                     model.py:749-768; checked against an explicit per-head
+                     loop over the reference's three calls on a tiny shape.
   polynorm           the reference's only numeric golden vector
                      (tests/fixtures/motif_parity_cases.json,
                      component_checks[0]).
@@ -247,6 +252,19 @@ def gda_post(merged, subln_w, lambda_full: float, lambda_init: float, q_groups: 
     q_origin = q_groups * gr
     return gda_post_split(m[:, :q_origin], m[:, q_origin:], subln_w, lambda_full, lambda_init,
                           gr, eps)
+
+
+def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_w, lambda_full: float,
+                         lambda_init: float, gr: int, eps: float, kv_len=None,
+                         dtype: str = "f16") -> np.ndarray:
+    """One GDA decode-attention step, the DUAL_V path of model.py:749-768:
+    attn_origin = sdpa_dual_v(q1, k1, v1, v2), attn_noise = sdpa_dual_v(q2,
+    k2, v1, v2), both returned in the activation dtype by the reference's
+    kernels (so rounded to ``dtype`` here), then gda_post_split with gr
+    origin heads per noise head.  Returns float64 (round once to compare)."""
+    o = round_to(sdpa_dual_v(q1, k1, v1, v2, scale, kv_len), dtype)
+    n = round_to(sdpa_dual_v(q2, k2, v1, v2, scale, kv_len), dtype)
+    return gda_post_split(o, n, subln_w, lambda_full, lambda_init, gr, eps)
 
 
 def polynorm(x, weight, bias, eps: float) -> np.ndarray:

@@ -113,3 +113,22 @@ def test_workspace_sizing_and_tuning():
     # too-small workspace for a multi-split plan is refused before any launch
     st = lib.motif_sdpa_dual_v(1, 1, 1, 1, 1, 0, 1, 32, 8, 128, 16128, 16000, 0.1, None, 0, None)
     assert st == _native.MOTIF_ERR_WORKSPACE and "workspace" in _err()
+
+
+def test_gda_decode_rejections_and_workspace():
+    lib = _native.lib()
+    args = lambda dtype, D, kv_cap, kv_len, ws, n: (  # noqa: E731
+        1, 1, 1, 1, 1, 1, 1, 1, 0.8, 1e-5, 1, dtype, 1, 8, 4, D, kv_cap, kv_len, 0.1, ws, n, None)
+    assert lib.motif_gda_decode(*args(7, 128, 256, 10, None, 0)) == -1 and "dtype" in _err()
+    assert lib.motif_gda_decode(*args(0, 100, 256, 10, None, 0)) == -1
+    assert "multiple of 32" in _err()
+    assert lib.motif_gda_decode(*args(0, 128, 256, 300, None, 0)) == -1 and "kv_len" in _err()
+    st = lib.motif_gda_decode(*args(0, 128, 16128, 16000, None, 0))
+    assert st == _native.MOTIF_ERR_WORKSPACE and "workspace" in _err()
+    # the fused path's partials (B*Hkv*(gr+1) rows) and the composed path's
+    # attention outputs both fit the reported size, which grows with kv_len
+    small = lib.motif_gda_decode_workspace_bytes(1, 8, 4, 16, 128)
+    big = lib.motif_gda_decode_workspace_bytes(1, 8, 4, 16000, 128)
+    assert 0 < small <= big
+    assert big >= 8 * 5 * 32 * (2 * 128 + 2) * 4
+    assert lib.motif_gda_decode_workspace_bytes(0, 8, 4, 16, 128) == 0

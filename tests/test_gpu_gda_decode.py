@@ -1,0 +1,182 @@
+"""Parity of the fused GDA decode step (``motif_gda_decode``) against the
+oracle composition of the reference's three calls (model.py:749-768:
+sdpa_dual_v for the origin heads, sdpa_dual_v for the noise heads, both
+returned in the activation dtype, then gda_post_split), and against the
+separately validated native calls.
+
+The fused path runs for fp16 at head_dim 128 (columns G + 1 = 2 .. 16 per KV
+head, both the 8-wave and the 4-wave variants); bf16, fp32, other head dims
+and mfma=0 take the composed path inside the library.
+
+Bar: the attention outputs carry the dual-V kernels' own bar (max |o -
+o_exact| <= 2e-3 for fp16, 1e-2 bf16, 1e-5 fp32; tests/test_gpu_sdpa.py),
+and the epilogue normalises d = o - lambda*n to unit RMS, so an error e in o
+moves y by about rsqrt(mean d^2) * |w| * (1 - lambda_init) * e.  Per
+element, |gpu - ref| <= rms_inv |w| s (E + lambda E) + 2 ulp(y) + 1e-5 with
+E that attention bar; on top, the mean error must stay below a tenth of the
+mean bar (no systematic offset).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import np_to_torch, randn, torch_dtype, torch_to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ULP = {"f16": 2.0 ** -10, "bf16": 2.0 ** -7, "f32": 2.0 ** -23}
+ATT = {"f16": 2e-3, "bf16": 1e-2, "f32": 1e-5}  # dual-V attention bars
+
+
+def _ulp(x, tag):
+    mag = np.maximum(np.abs(x), 2.0 ** -14)
+    return ULP[tag] * 2.0 ** np.floor(np.log2(mag))
+
+
+def _case(rng, B, Hkv, gr, cap, D, tag, poison_from=None):
+    q1 = randn(rng, (B, Hkv * gr, 1, D), tag)
+    q2 = randn(rng, (B, Hkv, 1, D), tag)
+    ks = [randn(rng, (B, Hkv, cap, D), tag) for _ in range(4)]
+    if poison_from is not None:
+        for t in ks:
+            t[:, :, poison_from:] = 1e4
+    w = randn(rng, (2 * D,), tag)
+    return q1, q2, ks, w
+
+
+def _bar(q1, q2, k1, k2, v1, v2, w, scale, lam, lam_init, gr, eps, kv_len, tag):
+    """Oracle y and the per-element bar of the module docstring."""
+    o = O.sdpa_dual_v(q1, k1, v1, v2, scale, kv_len)
+    n = O.sdpa_dual_v(q2, k2, v1, v2, scale, kv_len)
+    orr, nr = O.round_to(o, tag), O.round_to(n, tag)
+    y = O.gda_post_split(orr, nr, w, lam, lam_init, gr, eps)
+    d = np.asarray(orr, np.float64) - float(np.float32(lam)) * np.repeat(
+        np.asarray(nr, np.float64), gr, axis=1)
+    rms_inv = 1.0 / np.sqrt((d * d).mean(axis=-1, keepdims=True) + eps)
+    tol = (rms_inv * np.abs(np.asarray(w, np.float64)) * (1 - lam_init) * (1 + lam) * ATT[tag]
+           + 2 * _ulp(y, tag) + 1e-5)
+    return y, tol
+
+
+def _run(gpu, rng, B, Hkv, gr, cap, kv_len, D, tag, poison=False):
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention
+
+    q1, q2, (k1, k2, v1, v2), w = _case(rng, B, Hkv, gr, cap, D, tag,
+                                        kv_len if poison else None)
+    dt = torch_dtype(tag)
+    T = [np_to_torch(a, dt, gpu) for a in (q1, q2, k1, k2, v1, v2, w)]
+    scale, lam, lam_init, eps = 1.0 / np.sqrt(D), 0.4321, 0.2, 1e-5
+    lam_t = torch.tensor([lam], dtype=torch.float32, device=gpu)
+    print(f"gda_decode B={B} Hkv={Hkv} gr={gr} cap={cap} kv_len={kv_len} D={D} {tag}", flush=True)
+    y = gda_decode_attention(*T[:6], scale, T[6], lam_t, lam_init, gr, eps, kv_len=kv_len)
+    torch.cuda.synchronize()
+    assert y.shape == (B, Hkv * gr, 1, 2 * D) and y.dtype == dt
+    ref, tol = _bar(q1, q2, k1, k2, v1, v2, w, scale, lam, lam_init, gr, eps, kv_len, tag)
+    got = torch_to_np(y)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert float(err.mean()) <= 0.1 * float(tol.mean()) + 1e-6, (err.mean(), tol.mean())
+    excess = float(np.max(err - tol))
+    return excess, y, T, (scale, lam_t, lam_init, eps)
+
+
+@pytest.mark.parametrize("kv_len", [1, 17, 300, 1024, 3204])
+def test_fused_decode_12p7b_heads(gpu, rng, kv_len):
+    """32 origin heads over 8 KV heads (gr 4) + 8 noise heads, head_dim 128."""
+    cap = (kv_len + 255) // 256 * 256
+    excess, *_ = _run(gpu, rng, 1, 8, 4, cap, kv_len, 128, "f16")
+    assert excess <= 0, f"kv_len={kv_len}: exceeds the bar by {excess:.3e}"
+
+
+@pytest.mark.parametrize("B,Hkv,gr", [(1, 4, 1), (2, 2, 2), (1, 2, 3), (1, 3, 7), (1, 2, 15)])
+def test_fused_decode_column_counts(gpu, rng, B, Hkv, gr):
+    """G + 1 columns of 2, 3 (-> 4), 4, 8 and 16 (the 4-wave variant)."""
+    excess, *_ = _run(gpu, rng, B, Hkv, gr, 256, 200, 128, "f16")
+    assert excess <= 0, f"B={B} Hkv={Hkv} gr={gr}: exceeds the bar by {excess:.3e}"
+
+
+def test_fused_decode_ignores_poisoned_padding(gpu, rng):
+    excess, *_ = _run(gpu, rng, 1, 8, 4, 512, 385, 128, "f16", poison=True)
+    assert excess <= 0
+
+
+def test_fused_decode_kv_len_zero(gpu, rng):
+    """No live rows: both attention outputs are zero, so d = 0 and y = 0."""
+    _, y, _, _ = _run(gpu, rng, 1, 8, 4, 256, 0, 128, "f16")
+    assert not torch_to_np(y).any()
+
+
+@pytest.mark.parametrize("D,tag", [(64, "f16"), (128, "bf16"), (128, "f32"), (256, "f16")])
+def test_composed_path_other_shapes(gpu, rng, D, tag):
+    excess, *_ = _run(gpu, rng, 1, 4, 4, 256, 150, D, tag)
+    assert excess <= 0, f"D={D} {tag}: exceeds the bar by {excess:.3e}"
+
+
+@pytest.mark.parametrize("kv_len", [3204, 16000])
+def test_fused_equals_separate_native_calls(gpu, rng, kv_len):
+    """Full-size property: the fused step and the reference's three calls run
+    through the separately validated native kernels agree to the bar's
+    scale (one rounding of the attention outputs)."""
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention, gda_post_split, sdpa_dual_v
+
+    cap = (kv_len + 127) // 128 * 128
+    B, Hkv, gr, D = 1, 8, 4, 128
+    dt = torch.float16
+    g = torch.Generator(device=gpu)
+    g.manual_seed(7)
+    mk = lambda *s: torch.randn(*s, generator=g, device=gpu).to(dt)  # noqa: E731
+    q1, q2 = mk(B, Hkv * gr, 1, D), mk(B, Hkv, 1, D)
+    k1, k2, v1, v2 = (mk(B, Hkv, cap, D) for _ in range(4))
+    w = mk(2 * D)
+    lam_t = torch.tensor([0.4321], dtype=torch.float32, device=gpu)
+    scale, lam_init, eps = 1.0 / np.sqrt(D), 0.2, 1e-5
+    print(f"gda_decode fused vs separate kv_len={kv_len}", flush=True)
+    y = gda_decode_attention(q1, q2, k1, k2, v1, v2, scale, w, lam_t, lam_init, gr, eps,
+                             kv_len=kv_len)
+    o = sdpa_dual_v(q1, k1, v1, v2, scale, kv_len=kv_len)
+    n = sdpa_dual_v(q2, k2, v1, v2, scale, kv_len=kv_len)
+    y2 = gda_post_split(o, n, w, lam_t, lam_init, gr, eps)
+    torch.cuda.synchronize()
+    a, b = torch_to_np(y), torch_to_np(y2)
+    on, nn = torch_to_np(o), torch_to_np(n)
+    d = on - 0.4321 * np.repeat(nn, gr, axis=1)
+    rms_inv = 1.0 / np.sqrt((d * d).mean(axis=-1, keepdims=True) + eps)
+    tol = (rms_inv * np.abs(torch_to_np(w)) * (1 - lam_init) * 1.4321 * ATT["f16"]
+           + 2 * _ulp(b, "f16") + 1e-5)
+    assert float(np.max(np.abs(a - b) - tol)) <= 0
+    # Most elements are bit-identical: the two paths differ only where a
+    # rescale decision moved an fp16 rounding of p.
+    assert np.mean(a == b) > 0.5
+
+
+def test_mfma_off_takes_composed_path(gpu, rng):
+    from mlx_motif import _native
+
+    _native.set_tuning("mfma", 0)
+    try:
+        excess, *_ = _run(gpu, rng, 1, 8, 4, 256, 200, 128, "f16")
+    finally:
+        _native.set_tuning("mfma", 1)
+    assert excess <= 0
+
+
+def test_disable_toggle_reference_matches_oracle(gpu, rng):
+    """The *_reference twin (what MLX_MOTIF_DISABLE_KERNELS routes to)."""
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention_reference
+
+    q1, q2, (k1, k2, v1, v2), w = _case(rng, 1, 2, 4, 64, 64, "f32")
+    T = [torch.from_numpy(np.asarray(a, np.float32)).to(gpu) for a in (q1, q2, k1, k2, v1, v2, w)]
+    lam_t = torch.tensor([0.4321], dtype=torch.float32, device=gpu)
+    y = gda_decode_attention_reference(*T[:6], 0.125, T[6], lam_t, 0.2, 4, 1e-5, kv_len=50)
+    ref = O.gda_decode_attention(q1, q2, k1, k2, v1, v2, 0.125, w, 0.4321, 0.2, 4, 1e-5, 50,
+                                 dtype="f32")
+    np.testing.assert_allclose(torch_to_np(y), ref, rtol=1e-4, atol=1e-4)

@@ -257,6 +257,43 @@ def test_gda_closed_forms(rng):
     np.testing.assert_array_equal(O.gda_post(m, w, 0.3, 0.6, 2, 4, 0.0), y)
 
 
+def test_gda_decode_attention_per_head_loop(rng):
+    """The decode-step composition against an explicit per-head loop over
+    the reference's three calls (model.py:749-768): torch's float64 SDPA for
+    each origin head h (k1 of KV head h // gr) and noise head (k2), outputs
+    rounded to fp16, then a scalar RMS-norm epilogue."""
+    import torch
+
+    B, Hkv, gr, D, kv, cap = 2, 2, 3, 32, 9, 12
+    q1 = _f16(rng, (B, Hkv * gr, 1, D))
+    q2 = _f16(rng, (B, Hkv, 1, D))
+    k1, k2, v1, v2 = (_f16(rng, (B, Hkv, cap, D)) for _ in range(4))
+    w = _f16(rng, (2 * D,))
+    lam, lam_init, eps, scale = 0.37, 0.55, 1e-5, 0.2
+    y = O.gda_decode_attention(q1, q2, k1, k2, v1, v2, scale, w, lam, lam_init, gr, eps,
+                               kv_len=kv)
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    t = lambda a: torch.from_numpy(a.astype(np.float64))  # noqa: E731
+
+    def att(q, k, j, b):
+        qs = t(q)[None, None]
+        ks = t(k[b, j, :kv])[None, None]
+        a1 = sdpa(qs, ks, t(v1[b, j, :kv])[None, None], scale=scale)
+        a2 = sdpa(qs, ks, t(v2[b, j, :kv])[None, None], scale=scale)
+        o = torch.cat([a1, a2], -1).numpy().reshape(-1)
+        return o.astype(np.float32).astype(np.float16).astype(np.float64)
+
+    lam32 = float(np.float32(lam))
+    for b in range(B):
+        for h in range(Hkv * gr):
+            j = h // gr
+            o = att(q1[b, h, 0], k1, j, b)
+            n = att(q2[b, j, 0], k2, j, b)
+            d = o - lam32 * n
+            ref = d / math.sqrt(float(np.mean(d * d)) + eps) * w.astype(np.float64) * (1 - lam_init)
+            np.testing.assert_allclose(y[b, h, 0], ref, rtol=1e-10, atol=1e-12)
+
+
 def test_lambda_formulas():
     assert abs(O.lambda_init(1) - 0.2) < 1e-15
     assert abs(O.lambda_init(1000) - 0.8) < 1e-12
