@@ -122,11 +122,14 @@ def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=H
     return [mk(*s) for s in sets], (q, sets)
 
 
-def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True, gr=4):
+def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True, gr=4,
+                      bits=None):
     """One GDA decode-attention step per call over distinct layer caches
-    (k1, k2, v1, v2 of HKV heads): motif_gda_decode (fused) or the
-    reference's three calls (two motif_sdpa_dual_v + motif_gda_post_split)."""
+    (k1, k2, v1, v2 of HKV heads): motif_gda_decode / motif_gda_decode_q
+    (fused) or the reference's three calls (two motif_sdpa_dual_v(_q) +
+    motif_gda_post_split).  ``bits`` 4/8: packed cache, group size 64."""
     from mlx_motif import _native
+    from mlx_motif.kernels import quantize
 
     g = torch.Generator(device=dev)
     g.manual_seed(99)
@@ -136,6 +139,9 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     lam = torch.tensor([0.37], dtype=torch.float32, device=dev)
     sets = [tuple(torch.randn((B, HKV, cap, D), generator=g, device=dev).half()
                   for _ in range(4)) for _ in range(nsets)]
+    if bits:
+        sets = [tuple(quantize(t, GS, bits) for t in st) for st in sets]
+        torch.cuda.synchronize()
     y = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
     o = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
     n = torch.empty((B, HKV, 1, 2 * D), dtype=torch.float16, device=dev)
@@ -143,6 +149,28 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
                  lib.motif_sdpa_workspace_bytes(B, HKV * gr, HKV, 1, kv_len, D))
     ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
     scale = 1.0 / D ** 0.5
+
+    def mk_q(k1, k2, v1, v2):
+        p = lambda t: [x.data_ptr() for x in t]  # noqa: E731
+
+        def call():
+            st = torch.cuda.current_stream().cuda_stream
+            if fused:
+                _native.check(lib.motif_gda_decode_q(
+                    q1.data_ptr(), q2.data_ptr(), *p(k1), *p(k2), *p(v1), *p(v2), w.data_ptr(),
+                    lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B, HKV, gr, D, cap, kv_len, bits,
+                    GS, scale, ws.data_ptr(), ws.numel(), st))
+                return
+            _native.check(lib.motif_sdpa_dual_v_q(
+                q1.data_ptr(), *p(k1), *p(v1), *p(v2), o.data_ptr(), 0, B, HKV * gr, HKV, D, cap,
+                kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
+            _native.check(lib.motif_sdpa_dual_v_q(
+                q2.data_ptr(), *p(k2), *p(v1), *p(v2), n.data_ptr(), 0, B, HKV, HKV, D, cap,
+                kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
+            _native.check(lib.motif_gda_post_split(
+                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), 0, B, HKV * gr, HKV, gr,
+                1, 2 * D, lam.data_ptr(), 0.8, 1e-5, st))
+        return call
 
     def mk(k1, k2, v1, v2):
         def call():
@@ -164,15 +192,17 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
                 1, 2 * D, lam.data_ptr(), 0.8, 1e-5, st))
         return call
 
-    return [mk(*t) for t in sets], (q1, q2, w, lam, sets, y, o, n, ws)
+    return [(mk_q if bits else mk)(*t) for t in sets], (q1, q2, w, lam, sets, y, o, n, ws)
 
 
-def decode_bytes(kv_len: int, fused: bool, gr: int = 4) -> int:
+def decode_bytes(kv_len: int, fused: bool, gr: int = 4, bits=None) -> int:
     """Cache bytes of one decode step: 4 streams fused, 6 for the three calls
-    (v1 and v2 read by both passes), plus q, y and the attention outputs."""
+    (v1 and v2 read by both passes), plus q and y.  A packed row holds
+    D*bits/8 code bytes and 2*D/64 fp16 scales and biases."""
     streams = 4 if fused else 6
     heads = HKV * gr + HKV
-    return streams * B * HKV * kv_len * D * 2 + heads * D * 2 + HKV * gr * 2 * D * 2
+    row = D * 2 if not bits else D * bits // 8 + 2 * (D // GS) * 2
+    return streams * B * HKV * kv_len * row + heads * D * 2 + HKV * gr * 2 * D * 2
 
 
 def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
@@ -389,12 +419,14 @@ def run_extra(torch, lib, dev, args):
     # one GDA decode-attention step (origin + noise passes + gda_post_split)
     # at kv_len 16000: fused entry vs the reference's three calls; GB/s over
     # the bytes each one must move (4 vs 6 cache streams)
-    for fused in (True, False):
-        calls, keep = make_decode_calls(torch, lib, dev, 6, fused=fused)
-        report(f"gda decode step kv16000 ({'fused' if fused else 'three calls'})",
-               time_calls(torch, calls, steps, warm), decode_bytes(KV_LEN, fused))
-        del calls, keep
-        torch.cuda.empty_cache()
+    for bits, nsets in ((None, 6), (4, 18), (8, 12)):
+        for fused in (True, False):
+            calls, keep = make_decode_calls(torch, lib, dev, nsets, fused=fused, bits=bits)
+            cache = "f16" if not bits else f"q{bits}"
+            report(f"gda decode step {cache} kv16000 ({'fused' if fused else 'three calls'})",
+                   time_calls(torch, calls, steps, warm), decode_bytes(KV_LEN, fused, bits=bits))
+            del calls, keep
+            torch.cuda.empty_cache()
     # verify slab: 5 rows over a q8 cache of 32768 rows
     calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
     report("verify slab q8 5 rows kv32768", time_calls(torch, calls, steps, warm),

@@ -192,8 +192,9 @@ int motif_gda_post(const void* merged, const void* subln_w, void* y, int dtype, 
  *   y (B, Hkv*gr, 1, 2D)                             dtype
  * Origin head h pairs with noise head h / gr (gda.py:248).  The attention
  * outputs are rounded to dtype before the epilogue, as the reference's are.
- * Workspace: motif_gda_decode_workspace_bytes(B, Hkv, gr, kv_len, D) bytes,
- * 256-byte aligned, zeroed before its first use.
+ * Workspace (this entry point and motif_gda_decode_q):
+ * motif_gda_decode_workspace_bytes(B, Hkv, gr, kv_len, D) bytes, 256-byte
+ * aligned, zeroed before its first use.
  * ------------------------------------------------------------------------ */
 size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int D);
 
@@ -202,6 +203,22 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
                      const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
                      int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
                      float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Same step over the packed MLX-affine q4/q8 cache (QUANT_SDPA path of
+ * model.py:717-748: two sdpa_dual_v_q4 calls + gda_post_split).  Each slot is
+ * a (data, scales, biases) triple laid out as for motif_sdpa_dual_v_q.  The
+ * fused launch covers fp16 scales at D = 128 when (gr + 1) rounded up to a
+ * power of two, times D / group_size, is at most 16; other shapes compose
+ * the separate calls on the device.  Contract as motif_sdpa_dual_v_q. */
+int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
+                       const void* k1_scales, const void* k1_biases, const uint32_t* k2_data,
+                       const void* k2_scales, const void* k2_biases, const uint32_t* v1_data,
+                       const void* v1_scales, const void* v1_biases, const uint32_t* v2_data,
+                       const void* v2_scales, const void* v2_biases, const void* subln_w,
+                       const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                       int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                       int bits, int group_size, float scale, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ *
  * Fused PolyNorm (polynorm, src/mlx_motif/kernels/mlp.py:119-157):

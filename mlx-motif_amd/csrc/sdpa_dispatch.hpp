@@ -31,6 +31,9 @@ int launch_sdpa_merge_f32(const SdpaArgs& a, int D, hipStream_t s);
 int launch_gda_decode_f16(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
 int launch_gda_decode_bf16(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
 int launch_gda_decode_f32(const SdpaArgs& a, int gc, int nblocks, hipStream_t s);
+int launch_gda_decode_q_f16(const SdpaArgs& a, int bits, int gc, int nblocks, hipStream_t s);
+int launch_gda_decode_q_bf16(const SdpaArgs& a, int bits, int gc, int nblocks, hipStream_t s);
+int launch_gda_decode_q_f32(const SdpaArgs& a, int bits, int gc, int nblocks, hipStream_t s);
 
 // Pointer alignment (bytes) the kernels need for head dim D.
 int sdpa_fp_align(int dtype, int D);

@@ -158,7 +158,8 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
 // ------------------------------------------------ fused GDA decode step ---
 // Partial rows of the fused path: (b, KV head, column), G + 1 columns.
 struct GdaDecodeLayout {
-  SdpaPlan plan;
+  SdpaPlan plan;    // fp16-cache kernel (8-wave workgroups)
+  SdpaPlan plan_q;  // packed-cache kernel (4-wave workgroups, one per CU)
   size_t counter_bytes, o_bytes, ml_bytes, fused_bytes;
   size_t sdpa_bytes, yo_bytes, yn_bytes, composed_bytes;
 };
@@ -170,12 +171,15 @@ static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int
   // One virtual head per KV head in the planner: the fused kernel runs one
   // workgroup per (b, KV head, split), like the unfused origin pass.
   L.plan = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, 0, 0);
+  L.plan_q = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu);
+  const int ns = L.plan.nsplit > L.plan_q.nsplit ? L.plan.nsplit : L.plan_q.nsplit;
   const size_t prow = (size_t)B * Hkv * (gr + 1);
   L.counter_bytes = round256(prow * sizeof(unsigned));
-  L.o_bytes = round256(prow * L.plan.nsplit * 2 * D * sizeof(float));
-  L.ml_bytes = round256(prow * L.plan.nsplit * 2 * sizeof(float));
+  L.o_bytes = round256(prow * ns * 2 * D * sizeof(float));
+  L.ml_bytes = round256(prow * ns * 2 * sizeof(float));
   L.fused_bytes = L.counter_bytes + L.o_bytes + L.ml_bytes;
-  // Composed path: both attention calls' workspace, then o and n (fp32 bound).
+  // Composed path: both attention calls' workspace (any cache format), then
+  // o and n (fp32 bound).
   const size_t w1 = motif_sdpa_workspace_bytes(B, Hkv * gr, Hkv, 1, kv_len, D);
   const size_t w2 = motif_sdpa_workspace_bytes(B, Hkv, Hkv, 1, kv_len, D);
   L.sdpa_bytes = round256(w1 > w2 ? w1 : w2);
@@ -184,6 +188,65 @@ static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int
   L.composed_bytes = L.sdpa_bytes + L.yo_bytes + L.yn_bytes;
   return L;
 }
+
+// Checks shared by both fused-decode entry points; the workspace check
+// covers the larger of the fused and composed layouts.
+static int gda_decode_common(const char* name, const GdaDecodeLayout& L, int dtype, int B,
+                             int Hkv, int gr, int D, int kv_cap, int kv_len, void* ws,
+                             size_t ws_bytes) {
+  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
+                "%s: unknown dtype code %d", name, dtype);
+  MOTIF_REQUIRE(B >= 1 && Hkv >= 1 && gr >= 1, "%s: B, H_kv, gr must be >= 1", name);
+  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
+  MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
+                "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
+  const size_t need = L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
+  if (ws == nullptr || ws_bytes < need) {
+    set_error("%s: workspace of %zu bytes needed, %zu given", name, need,
+              ws == nullptr ? (size_t)0 : ws_bytes);
+    return MOTIF_ERR_WORKSPACE;
+  }
+  MOTIF_REQUIRE(aligned(ws, 256), "%s: workspace must be 256-byte aligned", name);
+  return MOTIF_OK;
+}
+
+// Arguments of a fused launch: partial rows (b, KV head, column) after the
+// (unused) counter block.
+static SdpaArgs gda_decode_args(const GdaDecodeLayout& L, const SdpaPlan& p, const void* q1,
+                                const void* q2, void* y, int B, int Hkv, int gr, int kv_cap,
+                                int kv_len, float scale, const void* subln_w,
+                                const float* lambda_full, float one_minus_lambda_init,
+                                float eps, void* ws) {
+  SdpaArgs a{};
+  a.q = q1;
+  a.q2 = q2;
+  a.y = y;
+  a.B = B;
+  a.Hkv = Hkv;
+  a.Hq = Hkv * gr;
+  a.S_q = 1;
+  a.G = gr;
+  a.GV = gr + 1;
+  a.nchunk = 1;
+  a.kv_cap = kv_cap;
+  a.kv_len = kv_len;
+  a.causal = 0;
+  a.nsplit = p.nsplit;
+  a.rows_per_split = p.rows_per_split;
+  a.fused_merge = 0;
+  a.qscale = scale * 1.4426950408889634f;
+  char* w = (char*)ws;
+  a.counters = (unsigned*)w;
+  a.part_o = (float*)(w + L.counter_bytes);
+  a.part_ml = (float*)(w + L.counter_bytes + L.o_bytes);
+  a.gda_w = subln_w;
+  a.gda_lambda = lambda_full;
+  a.gda_scale = one_minus_lambda_init;
+  a.gda_eps = eps;
+  return a;
+}
+
+static int gda_columns(int gr) { return gr + 1 <= 2 ? 2 : gr + 1 <= 4 ? 4 : gr + 1 <= 8 ? 8 : 16; }
 
 }  // namespace motif
 
@@ -204,67 +267,32 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
                      float scale, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   const char* name = "gda_decode";
-  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
-                "%s: unknown dtype code %d", name, dtype);
-  MOTIF_REQUIRE(B >= 1 && Hkv >= 1 && gr >= 1, "%s: B, H_kv, gr must be >= 1", name);
-  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
-  MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
-                "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+                             workspace_bytes);
+  if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q1 && q2 && y && subln_w && lambda_full &&
                     (kv_cap == 0 || (k1 && k2 && v1 && v2)),
                 "%s: null pointer", name);
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
-  const size_t need = L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
-  if (workspace == nullptr || workspace_bytes < need) {
-    set_error("%s: workspace of %zu bytes needed, %zu given", name, need,
-              workspace == nullptr ? (size_t)0 : workspace_bytes);
-    return MOTIF_ERR_WORKSPACE;
-  }
-  MOTIF_REQUIRE(aligned(workspace, 256), "%s: workspace must be 256-byte aligned", name);
   hipStream_t s = (hipStream_t)stream;
-  const int gc = gr + 1 <= 2 ? 2 : gr + 1 <= 4 ? 4 : gr + 1 <= 8 ? 8 : 16;
   const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
                      aligned(q1, 16) && aligned(q2, 16) && aligned(k1, 16) && aligned(k2, 16) &&
                      aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8);
   if (fused) {
-    SdpaArgs a{};
-    a.q = q1;
-    a.q2 = q2;
+    SdpaArgs a = gda_decode_args(L, L.plan, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
+                                 subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
     a.k = k1;
     a.k2 = k2;
     a.v1 = v1;
     a.v2 = v2;
-    a.y = y;
-    a.B = B;
-    a.Hkv = Hkv;
-    a.Hq = Hkv * gr;
-    a.S_q = 1;
-    a.G = gr;
-    a.GV = gr + 1;
-    a.nchunk = 1;
-    a.kv_cap = kv_cap;
-    a.kv_len = kv_len;
-    a.causal = 0;
-    a.nsplit = L.plan.nsplit;
-    a.rows_per_split = L.plan.rows_per_split;
-    a.fused_merge = 0;
-    a.qscale = scale * 1.4426950408889634f;
-    char* w = (char*)workspace;
-    a.counters = (unsigned*)w;
-    a.part_o = (float*)(w + L.counter_bytes);
-    a.part_ml = (float*)(w + L.counter_bytes + L.o_bytes);
-    a.gda_w = subln_w;
-    a.gda_lambda = lambda_full;
-    a.gda_scale = one_minus_lambda_init;
-    a.gda_eps = eps;
-    return launch_gda_decode_f16(a, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+    return launch_gda_decode_f16(a, gda_columns(gr), sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
   }
   // Composition of the separate calls, every step on the device.
   char* w = (char*)workspace;
   void* yo = w + L.sdpa_bytes;
   void* yn = w + L.sdpa_bytes + L.yo_bytes;
-  int rc = motif_sdpa_dual_v(q1, k1, v1, v2, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap, kv_len,
-                             scale, workspace, L.sdpa_bytes, stream);
+  rc = motif_sdpa_dual_v(q1, k1, v1, v2, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap, kv_len, scale,
+                         workspace, L.sdpa_bytes, stream);
   if (rc != MOTIF_OK) return rc;
   rc = motif_sdpa_dual_v(q2, k2, v1, v2, yn, dtype, B, Hkv, Hkv, D, kv_cap, kv_len, scale,
                          workspace, L.sdpa_bytes, stream);
@@ -311,6 +339,70 @@ int motif_sdpa_dual_v_q_rows(const void* q, const uint32_t* k_data, const void* 
                     v1_biases, v2_data, v2_scales, v2_biases, y, dtype, B, Hq, Hkv, S_q, D,
                     kv_cap, kv_len, causal, bits, group_size, scale, workspace, workspace_bytes,
                     stream);
+}
+
+int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
+                       const void* k1_scales, const void* k1_biases, const uint32_t* k2_data,
+                       const void* k2_scales, const void* k2_biases, const uint32_t* v1_data,
+                       const void* v1_scales, const void* v1_biases, const uint32_t* v2_data,
+                       const void* v2_scales, const void* v2_biases, const void* subln_w,
+                       const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                       int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                       int bits, int group_size, float scale, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* name = "gda_decode_q";
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+                             workspace_bytes);
+  if (rc != MOTIF_OK) return rc;
+  MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
+  MOTIF_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+                "%s: group_size=%d must be 32, 64 or 128", name, group_size);
+  MOTIF_REQUIRE(D % group_size == 0, "%s: D=%d must be a multiple of group_size=%d", name, D,
+                group_size);
+  MOTIF_REQUIRE(q1 && q2 && y && subln_w && lambda_full &&
+                    (kv_cap == 0 || (k1_data && k1_scales && k1_biases && k2_data &&
+                                     k2_scales && k2_biases && v1_data && v1_scales &&
+                                     v1_biases && v2_data && v2_scales && v2_biases)),
+                "%s: null pointer", name);
+  hipStream_t s = (hipStream_t)stream;
+  const int gc = gda_columns(gr);
+  const int ng = D / group_size;
+  const uintptr_t data_bits = (uintptr_t)k1_data | (uintptr_t)k2_data | (uintptr_t)v1_data |
+                              (uintptr_t)v2_data;
+  const uintptr_t scale_bits = (uintptr_t)k1_scales | (uintptr_t)k1_biases |
+                               (uintptr_t)k2_scales | (uintptr_t)k2_biases |
+                               (uintptr_t)v1_scales | (uintptr_t)v1_biases |
+                               (uintptr_t)v2_scales | (uintptr_t)v2_biases;
+  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+                     gc * ng <= 16 && (data_bits & 15u) == 0 &&
+                     (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
+                     L.plan_q.rows_per_split % 16 == 0 && aligned(q1, 16) && aligned(q2, 16) &&
+                     aligned(y, 8);
+  if (fused) {
+    SdpaArgs a = gda_decode_args(L, L.plan_q, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
+                                 subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
+    a.kd = k1_data; a.ks = k1_scales; a.kb = k1_biases;
+    a.k2d = k2_data; a.k2s = k2_scales; a.k2b = k2_biases;
+    a.v1d = v1_data; a.v1s = v1_scales; a.v1b = v1_biases;
+    a.v2d = v2_data; a.v2s = v2_scales; a.v2b = v2_biases;
+    a.group_size = group_size;
+    return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+  }
+  char* w = (char*)workspace;
+  void* yo = w + L.sdpa_bytes;
+  void* yn = w + L.sdpa_bytes + L.yo_bytes;
+  rc = motif_sdpa_dual_v_q(q1, k1_data, k1_scales, k1_biases, v1_data, v1_scales, v1_biases,
+                           v2_data, v2_scales, v2_biases, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap,
+                           kv_len, bits, group_size, scale, workspace, L.sdpa_bytes, stream);
+  if (rc != MOTIF_OK) return rc;
+  rc = motif_sdpa_dual_v_q(q2, k2_data, k2_scales, k2_biases, v1_data, v1_scales, v1_biases,
+                           v2_data, v2_scales, v2_biases, yn, dtype, B, Hkv, Hkv, D, kv_cap,
+                           kv_len, bits, group_size, scale, workspace, L.sdpa_bytes, stream);
+  if (rc != MOTIF_OK) return rc;
+  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
+                              lambda_full, one_minus_lambda_init, eps, stream);
 }
 
 }  // extern "C"

@@ -130,16 +130,20 @@ __device__ inline float sum_group_columns(float x) {
 //              t0 + 4*blk .. +3 that hold the lane's scale group
 // Nothing is consumed at load time, so all loads of a tile are in flight
 // together; scale_words() extracts the lane's halves when it is computed.
-template <int BITS, int NG>
+//   k2[KW], s[6..7]  (fused GDA decode step) the noise keys' codes and
+//              their scale / bias words
+template <int BITS, int NG, bool DUAL = false>
 struct QTile {
   static constexpr int WPR = 128 * BITS / 32;
   static constexpr int KW = WPR / 4;
   static constexpr int VW = WPR / 16;
   static constexpr int SW = NG == 1 ? 2 : 4;
+  static constexpr int NS = DUAL ? 8 : 6;
   uint32_t k[KW];
+  uint32_t k2[DUAL ? KW : 1];
   uint32_t v1[4][VW];
   uint32_t v2[4][VW];
-  uint32_t s[6][SW];
+  uint32_t s[NS][SW];
 };
 
 // Raw scale / bias words of one tensor for rows row0 .. row0+3 (NG groups of
@@ -196,12 +200,16 @@ __device__ inline void drop_rows_past(uint32_t (&out)[2], unsigned row0, unsigne
 // chunks (a.nchunk > 1: more virtual heads than one pass holds, e.g. a
 // verify slab) read each row in several workgroups and use cached loads, so
 // all but the first find the rows in L2 or the Infinity Cache.
-template <int BITS, int GS, int GC, int NW, int U, int POL = kCachePolicyStream>
+// DUAL: fused GDA decode step, as in sdpa_mfma_f16_kernel: head h < G of a
+// column scores against k, head G (the noise head) against k2.
+template <int BITS, int GS, int GC, int NW, int U, int POL = kCachePolicyStream,
+          bool DUAL = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int D = 128;
   constexpr int NG = D / GS;  // scale groups per row
-  using Tile = QTile<BITS, NG>;
+  using Tile = QTile<BITS, NG, DUAL>;
+  constexpr int NS = Tile::NS;
   constexpr int WPR = Tile::WPR;
   constexpr int KW = Tile::KW;
   constexpr int VW = Tile::VW;
@@ -224,7 +232,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int kvh = bk % a.Hkv;
   const int vh0 = chunk * GC;
   const int nvh = min(GC, a.GV - vh0);
-  const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
+  // First output row: y row (non-DUAL) or partial row (DUAL) of head 0.
+  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
+                          : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
   const int h = col % GC;    // head of this column
   const int grp = col / GC;  // scale group of this column
@@ -246,13 +256,17 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // Scale resources cover whole 4-row groups (kv_cap % 4 == 0 and the split
   // starts at a multiple of 16 rows, so this stays inside the cache).
   const unsigned sbytes = (unsigned)(((nrows + 3) & ~3) * NG * 2);
-  const __amdgpu_buffer_rsrc_t rs[6] = {
+  const __amdgpu_buffer_rsrc_t rs[8] = {
       stream_rsrc((const uint16_t*)a.ks + hrow0 * NG, sbytes),
       stream_rsrc((const uint16_t*)a.kb + hrow0 * NG, sbytes),
       stream_rsrc((const uint16_t*)a.v1s + hrow0 * NG, sbytes),
       stream_rsrc((const uint16_t*)a.v1b + hrow0 * NG, sbytes),
       stream_rsrc((const uint16_t*)a.v2s + hrow0 * NG, sbytes),
-      stream_rsrc((const uint16_t*)a.v2b + hrow0 * NG, sbytes)};
+      stream_rsrc((const uint16_t*)a.v2b + hrow0 * NG, sbytes),
+      stream_rsrc(DUAL ? (const uint16_t*)a.k2s + hrow0 * NG : nullptr, DUAL ? sbytes : 0u),
+      stream_rsrc(DUAL ? (const uint16_t*)a.k2b + hrow0 * NG : nullptr, DUAL ? sbytes : 0u)};
+  const auto rk2 = stream_rsrc(DUAL ? a.k2d + hrow0 * WPR : nullptr,
+                               DUAL ? (unsigned)(nrows * WPR * 4) : 0u);
 
   // All loads of U tiles starting at split-relative row t0 (rows past the
   // split read 0).
@@ -265,6 +279,13 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       for (int i = 0; i < KW; i += 4) {
         const uint4 x = bload4<POL>(rk, koff + 4u * i);
         T[u].k[i] = x.x; T[u].k[i + 1] = x.y; T[u].k[i + 2] = x.z; T[u].k[i + 3] = x.w;
+      }
+      if constexpr (DUAL) {
+#pragma unroll
+        for (int i = 0; i < KW; i += 4) {
+          const uint4 x = bload4<POL>(rk2, koff + 4u * i);
+          T[u].k2[i] = x.x; T[u].k2[i + 1] = x.y; T[u].k2[i + 2] = x.z; T[u].k2[i + 3] = x.w;
+        }
       }
       const unsigned vrow = r0 + 4u * blk;
 #pragma unroll
@@ -281,7 +302,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         }
       }
 #pragma unroll
-      for (int t = 0; t < 6; ++t) load_scales<NG, POL>(T[u].s[t], rs[t], vrow, gsel);
+      for (int t = 0; t < NS; ++t) load_scales<NG, POL>(T[u].s[t], rs[t], vrow, gsel);
     }
   };
 
@@ -292,6 +313,11 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   uint4 qraw[4];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (h < nvh ? h : 0)) * D + 32 * blk;
+    if constexpr (DUAL) {
+      qp = h < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + h) * D
+                   : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      qp += 32 * blk;
+    }
 #pragma unroll
     for (int s = 0; s < 4; ++s) qraw[s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
@@ -337,14 +363,14 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     for (int u = 0; u < U; ++u) {
       const int row0 = r_begin + t0 + u * NW * 16 + 4 * blk;  // absolute row of r = 0
       const unsigned rrow0 = (unsigned)(t0 + u * NW * 16 + 4 * blk);  // split-relative
-      uint32_t sw[6][2];
+      uint32_t sw[NS][2];
 #pragma unroll
-      for (int t = 0; t < 6; ++t) scale_words<NG>(sw[t], T[u].s[t], sel);
+      for (int t = 0; t < NS; ++t) scale_words<NG>(sw[t], T[u].s[t], sel);
       // Only the split's last tile can hold rows past its end; the test is
       // uniform over the wave, so the others branch around the masking.
       if (t0 + u * NW * 16 + 16 > nrows) {
 #pragma unroll
-        for (int t = 0; t < 6; ++t) drop_rows_past(sw[t], rrow0, (unsigned)nrows);
+        for (int t = 0; t < NS; ++t) drop_rows_past(sw[t], rrow0, (unsigned)nrows);
       }
       floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -357,8 +383,30 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         }
         sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sacc, 0, 0, 0);
       }
-      const half2_t sk01 = as_h2(sw[0][0]), sk23 = as_h2(sw[0][1]);
-      const half2_t bk01 = as_h2(sw[1][0]), bk23 = as_h2(sw[1][1]);
+      uint32_t skw[2] = {sw[0][0], sw[0][1]}, bkw[2] = {sw[1][0], sw[1][1]};
+      if constexpr (DUAL) {  // the noise head's column: k2 codes and scales
+        floatx4 s2 = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          half8_t ka;
+          if constexpr (BITS == 4) {
+            ka = q4_word_codes(T[u].k2[s], magic);
+          } else {
+            ka = q8_words_codes(T[u].k2[2 * s], T[u].k2[2 * s + 1]);
+          }
+          s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], s2, 0, 0, 0);
+        }
+        const bool noise = h == a.G;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sacc[r] = noise ? s2[r] : sacc[r];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          skw[p] = noise ? sw[6][p] : skw[p];
+          bkw[p] = noise ? sw[7][p] : bkw[p];
+        }
+      }
+      const half2_t sk01 = as_h2(skw[0]), sk23 = as_h2(skw[1]);
+      const half2_t bk01 = as_h2(bkw[0]), bk23 = as_h2(bkw[1]);
       const float skr[4] = {(float)sk01.x, (float)sk01.y, (float)sk23.x, (float)sk23.y};
       const float bkr[4] = {(float)bk01.x, (float)bk01.y, (float)bk23.x, (float)bk23.y};
       float sc[4];
@@ -472,7 +520,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     lds_l[wave][h] = accl[0];
   }
   __syncthreads();
-  wg_epilogue<half_t, D, GC, NW>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+  wg_epilogue<half_t, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
 // Packed cache, head_dim 128, fp16 scales: heads x groups <= 16 columns.
@@ -512,6 +560,43 @@ int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hip
       return MOTIF_ERR_UNSUPPORTED;
   }
   return check_launch("sdpa_dual_v_q (mfma)");
+}
+
+// Fused GDA decode step over the packed cache: gc columns per scale group
+// (G + 1 rounded up to a power of two, gc * 128 / gs <= 16), 4 waves.
+template <int BITS, int GS>
+int launch_gda_decode_mfma_q_gs(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
+  constexpr int NG = 128 / GS;
+  constexpr int P = kCachePolicyStream;
+  if (gc * NG > 16 || (gc != 2 && gc != 4 && gc != 8 && gc != 16)) {
+    set_error("gda_decode_q: no fused variant for %d columns at group size %d", gc, GS);
+    return MOTIF_ERR_UNSUPPORTED;
+  }
+  if (gc == 2) {
+    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+  } else if (gc == 4) {
+    if constexpr (4 * NG <= 16)
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+  } else if (gc == 8) {
+    if constexpr (8 * NG <= 16)
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 8, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+  } else {
+    if constexpr (16 * NG <= 16)
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 16, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+  }
+  return check_launch("gda_decode_q (mfma)");
+}
+
+inline int launch_gda_decode_mfma_q(const SdpaArgs& a, int bits, int gs, int gc, int nblocks,
+                                    hipStream_t st) {
+  if (bits == 4) {
+    if (gs == 32) return launch_gda_decode_mfma_q_gs<4, 32>(a, gc, nblocks, st);
+    if (gs == 64) return launch_gda_decode_mfma_q_gs<4, 64>(a, gc, nblocks, st);
+    return launch_gda_decode_mfma_q_gs<4, 128>(a, gc, nblocks, st);
+  }
+  if (gs == 32) return launch_gda_decode_mfma_q_gs<8, 32>(a, gc, nblocks, st);
+  if (gs == 64) return launch_gda_decode_mfma_q_gs<8, 64>(a, gc, nblocks, st);
+  return launch_gda_decode_mfma_q_gs<8, 128>(a, gc, nblocks, st);
 }
 
 inline int launch_sdpa_mfma_q(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,

@@ -45,6 +45,9 @@ struct SdpaArgs {
   // columns 0..G-1 the origin heads and G the noise head.
   const void* q2;
   const void* k2;
+  const uint32_t* k2d;  // packed noise keys (data, scales, biases)
+  const void* k2s;
+  const void* k2b;
   const void* gda_w;         // (2D) subln weight
   const float* gda_lambda;   // device pointer to lambda_full (fp32)
   float gda_scale;           // 1 - lambda_init

@@ -7,8 +7,8 @@ import) routes every wrapper to its reference.
 
     attention.py — sdpa_dual_v, sdpa_dual_v_q4 (+ multi-row *_rows variants)
     gda.py       — gda_post, gda_post_split
-    decode.py    — gda_decode_attention (both dual-V passes + gda_post_split
-                   in one call; the reference composes three)
+    decode.py    — gda_decode_attention(_q4) (both dual-V passes +
+                   gda_post_split in one call; the reference composes three)
     mlp.py       — polynorm, _dequant_probe (test helper)
     quant.py     — quantize / dequantize (MLX affine format of the KV cache)
 """
@@ -21,7 +21,12 @@ from .attention import (
     sdpa_dual_v_reference,
     sdpa_dual_v_rows,
 )
-from .decode import gda_decode_attention, gda_decode_attention_reference
+from .decode import (
+    gda_decode_attention,
+    gda_decode_attention_q4,
+    gda_decode_attention_q4_reference,
+    gda_decode_attention_reference,
+)
 from .gda import (
     gda_post,
     gda_post_reference,
@@ -44,6 +49,8 @@ __all__ = [
     "gda_post_split_reference",
     "gda_decode_attention",
     "gda_decode_attention_reference",
+    "gda_decode_attention_q4",
+    "gda_decode_attention_q4_reference",
     "sdpa_dual_v",
     "sdpa_dual_v_reference",
     "sdpa_dual_v_q4",

@@ -13,6 +13,8 @@ head_dim 128, ``motif_gda_decode`` serves both passes from one attention
 launch that reads each KV head's k1, k2, v1 and v2 rows once (the separate
 calls read v1 and v2 twice), and applies the epilogue in the split merge.
 Other shapes compose the separate native calls inside the library.
+``gda_decode_attention_q4`` is the same step over the packed q4/q8 cache
+(QUANT_SDPA path, ``model.py:717-748``: two ``sdpa_dual_v_q4`` calls).
 """
 
 from __future__ import annotations
@@ -21,7 +23,7 @@ import torch
 
 from .. import _native
 from . import _common
-from .attention import sdpa_dual_v_reference
+from .attention import _q_contract, sdpa_dual_v_q4_reference, sdpa_dual_v_reference
 from .gda import gda_post_split_reference
 
 
@@ -79,6 +81,71 @@ def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lam
             v2.data_ptr(), w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps),
             y.data_ptr(), _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len,
             float(scale), ws.data_ptr(), ws.numel(), _native.stream_of(dev),
+        )
+    )
+    return y
+
+
+def gda_decode_attention_q4_reference(q1, q2, k1_q, k2_q, v1_q, v2_q, scale: float,
+                                      subln_weight, lambda_full, lambda_init: float, gr: int,
+                                      group_size: int = 64, bits: int = 4, eps: float = 1e-5,
+                                      kv_len: int | None = None):
+    """Torch-op composition of the packed-cache step (model.py:717-748)."""
+    o = sdpa_dual_v_q4_reference(q1, k1_q, v1_q, v2_q, scale, group_size, bits,
+                                 kv_len).to(q1.dtype)
+    n = sdpa_dual_v_q4_reference(q2, k2_q, v1_q, v2_q, scale, group_size, bits,
+                                 kv_len).to(q1.dtype)
+    y = gda_post_split_reference(o, n, subln_weight.to(q1.dtype), lambda_full, lambda_init, gr,
+                                 eps)
+    return y.to(q1.dtype)
+
+
+def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q: tuple,
+                            scale: float, subln_weight, lambda_full, lambda_init: float, gr: int,
+                            group_size: int = 64, bits: int = 4, eps: float = 1e-5,
+                            kv_len: int | None = None):
+    """The decode step over the packed cache: each ``*_q`` is a ``(data
+    uint32, scales, biases)`` triple of (B, H_kv, KV_cap, ...) tensors as
+    ``sdpa_dual_v_q4`` takes them.  Returns (B, H_kv*gr, 1, 2D) in
+    ``q1.dtype``."""
+    if _common._DISABLE:
+        return gda_decode_attention_q4_reference(q1, q2, k1_q, k2_q, v1_q, v2_q, scale,
+                                                 subln_weight, lambda_full, lambda_init, gr,
+                                                 group_size, bits, eps, kv_len)
+    B, H_o, S_q, D = q1.shape
+    _, H_kv, KV_cap, n_uint = k1_q[0].shape
+    if kv_len is None:
+        kv_len = KV_cap
+    assert n_uint * (32 // bits) == D, (
+        f"k_data last axis = {n_uint} ⇒ packed D = {n_uint * (32 // bits)}, expected {D}"
+    )
+    assert S_q == 1 and q2.shape[2] == 1, "gda_decode_attention_q4 is decode-only"
+    assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
+    assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
+    _q_contract(D, H_o, H_kv, group_size, bits, kv_len, KV_cap)
+    slots = (k1_q, k2_q, v1_q, v2_q)
+    dev = _native.require_device(q1, q2, *(x for t in slots for x in t))
+    for t in slots:
+        assert tuple(t[0].shape) == (B, H_kv, KV_cap, n_uint), "packed slots must match k1"
+        for x in t[1:]:
+            if x.dtype != q1.dtype:
+                raise TypeError(f"scales/biases dtype {x.dtype} must match q1 dtype {q1.dtype}")
+    if q2.dtype != q1.dtype:
+        raise TypeError(f"q2 dtype {q2.dtype} must match q1 dtype {q1.dtype}")
+    q1, q2 = _common.contiguous(q1), _common.contiguous(q2)
+    slots = tuple(tuple(_common.contiguous(x) for x in t) for t in slots)
+    w = subln_weight.to(device=dev, dtype=q1.dtype).contiguous()
+    lam = _common.f32_scalar_tensor(lambda_full, dev)
+    y = torch.empty((B, H_o, 1, 2 * D), dtype=q1.dtype, device=dev)
+    lib = _native.lib()
+    ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
+    ptrs = [x.data_ptr() for t in slots for x in t]
+    _native.check(
+        lib.motif_gda_decode_q(
+            q1.data_ptr(), q2.data_ptr(), *ptrs, w.data_ptr(), lam.data_ptr(),
+            float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q1.dtype), B,
+            H_kv, gr, D, KV_cap, kv_len, bits, group_size, float(scale), ws.data_ptr(),
+            ws.numel(), _native.stream_of(dev),
         )
     )
     return y

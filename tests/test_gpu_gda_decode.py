@@ -180,3 +180,56 @@ def test_disable_toggle_reference_matches_oracle(gpu, rng):
     ref = O.gda_decode_attention(q1, q2, k1, k2, v1, v2, 0.125, w, 0.4321, 0.2, 4, 1e-5, 50,
                                  dtype="f32")
     np.testing.assert_allclose(torch_to_np(y), ref, rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------ packed cache ---
+def _run_q(gpu, rng, B, Hkv, gr, cap, kv_len, D, bits, gs, tag, poison=False):
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention_q4
+
+    q1, q2, ks, w = _case(rng, B, Hkv, gr, cap, D, tag)
+    if poison:
+        for t in ks:
+            t[:, :, kv_len:] = 1e3
+    trips = [O.quantize(t, gs, bits, out_dtype=tag) for t in ks]
+    dt = torch_dtype(tag)
+    gt = [(np_to_torch(d, None, gpu), np_to_torch(s, dt, gpu), np_to_torch(b, dt, gpu))
+          for d, s, b in trips]
+    scale, lam, lam_init, eps = 1.0 / np.sqrt(D), 0.4321, 0.2, 1e-5
+    lam_t = torch.tensor([lam], dtype=torch.float32, device=gpu)
+    print(f"gda_decode_q B={B} Hkv={Hkv} gr={gr} cap={cap} kv_len={kv_len} bits={bits} gs={gs} "
+          f"{tag}", flush=True)
+    y = gda_decode_attention_q4(np_to_torch(q1, dt, gpu), np_to_torch(q2, dt, gpu), *gt, scale,
+                                np_to_torch(w, dt, gpu), lam_t, lam_init, gr, gs, bits, eps,
+                                kv_len=kv_len)
+    torch.cuda.synchronize()
+    assert y.shape == (B, Hkv * gr, 1, 2 * D) and y.dtype == dt
+    deq = [O.dequantize(*t, group_size=gs, bits=bits) for t in trips]
+    ref, tol = _bar(q1, q2, *deq, w, scale, lam, lam_init, gr, eps, kv_len, tag)
+    got = torch_to_np(y)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert float(err.mean()) <= 0.1 * float(tol.mean()) + 1e-6, (err.mean(), tol.mean())
+    return float(np.max(err - tol))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("kv_len", [1, 64, 300, 3204])
+def test_fused_decode_q_12p7b_heads(gpu, rng, bits, kv_len):
+    cap = (kv_len + 255) // 256 * 256
+    excess = _run_q(gpu, rng, 1, 8, 4, cap, kv_len, 128, bits, 64, "f16")
+    assert excess <= 0, f"bits={bits} kv_len={kv_len}: exceeds the bar by {excess:.3e}"
+
+
+@pytest.mark.parametrize("gr,gs", [(1, 32), (3, 32), (4, 128), (7, 64), (15, 128), (4, 32)])
+def test_fused_decode_q_groups_and_columns(gpu, rng, gr, gs):
+    """Fused for (gr+1 -> 2/4/8/16 columns) x (128/gs groups) <= 16; gr 4 at
+    gs 32 needs 32 columns and takes the composed path."""
+    excess = _run_q(gpu, rng, 1, 2, gr, 256, 200, 128, 4, gs, "f16")
+    assert excess <= 0, f"gr={gr} gs={gs}: exceeds the bar by {excess:.3e}"
+
+
+def test_fused_decode_q_poisoned_padding_and_bf16(gpu, rng):
+    assert _run_q(gpu, rng, 1, 8, 4, 512, 385, 128, 4, 64, "f16", poison=True) <= 0
+    assert _run_q(gpu, rng, 1, 4, 4, 256, 150, 128, 8, 64, "bf16") <= 0
