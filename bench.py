@@ -360,7 +360,7 @@ def main() -> int:
         },
         "gbps": f16["gbps"],
         "pct_peak": f16["pct_peak"],
-        "q4": res["q4"],
+        "q4": dict(res["q4"], traffic=load_traffic("sdpa_dual_v_q4_kv16000")),
         "q8": res["q8"],
         "roofline": {
             "bound": "hbm",
