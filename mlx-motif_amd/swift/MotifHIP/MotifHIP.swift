@@ -126,6 +126,60 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// Workspace bytes of one fused decode step (either cache format).
+    public static func gdaDecodeWorkspaceBytes(batch: Int, kvHeads: Int, gr: Int, kvLen: Int,
+                                              headDim: Int) -> Int {
+        Int(motif_gda_decode_workspace_bytes(Int32(batch), Int32(kvHeads), Int32(gr),
+                                             Int32(kvLen), Int32(headDim)))
+    }
+
+    /// One GDA decode-attention step of a layer: origin pass (q1: kvHeads*gr
+    /// heads over k1), noise pass (q2: kvHeads heads over k2), both over v1/v2,
+    /// then gda_post_split; output (B, kvHeads*gr, 1, 2D).  Replaces the three
+    /// calls of the reference's decode step (MotifMLXModel.swift:433-505).
+    public static func gdaDecode(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        keys1: UnsafeRawPointer, keys2: UnsafeRawPointer, value1: UnsafeRawPointer,
+        value2: UnsafeRawPointer, sublnWeight: UnsafeRawPointer,
+        lambdaFull: UnsafePointer<Float>, oneMinusLambdaInit: Float, eps: Float,
+        output: UnsafeMutableRawPointer, dtype: MotifHIPDType, batch: Int, kvHeads: Int,
+        gr: Int, headDim: Int, kvCapacity: Int, kvLen: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode(originQueries, noiseQueries, keys1, keys2, value1, value2,
+                                  sublnWeight, lambdaFull, oneMinusLambdaInit, eps, output,
+                                  dtype.rawValue, Int32(batch), Int32(kvHeads), Int32(gr),
+                                  Int32(headDim), Int32(kvCapacity), Int32(kvLen), scale,
+                                  workspace, workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// Same step over the packed q4/q8 cache.
+    public static func gdaDecodeQuantized(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        keys1: MotifHIPQuantizedTriple, keys2: MotifHIPQuantizedTriple,
+        value1: MotifHIPQuantizedTriple, value2: MotifHIPQuantizedTriple,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int, kvCapacity: Int,
+        kvLen: Int, bits: Int, groupSize: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_q(originQueries, noiseQueries,
+                                    keys1.data, keys1.scales, keys1.biases,
+                                    keys2.data, keys2.scales, keys2.biases,
+                                    value1.data, value1.scales, value1.biases,
+                                    value2.data, value2.scales, value2.biases,
+                                    sublnWeight, lambdaFull, oneMinusLambdaInit, eps, output,
+                                    dtype.rawValue, Int32(batch), Int32(kvHeads), Int32(gr),
+                                    Int32(headDim), Int32(kvCapacity), Int32(kvLen),
+                                    Int32(bits), Int32(groupSize), scale, workspace,
+                                    workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// PolyNorm over the last axis of x (rows, D).
     public static func polynorm(
         x: UnsafeRawPointer, weight: UnsafeRawPointer, bias: UnsafeRawPointer,
