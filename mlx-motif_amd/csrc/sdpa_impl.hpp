@@ -400,9 +400,15 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
     }
     if (single) {
       store_y4<T, D>(a, (qrow0 + g) * 2 * D + c, O, L);
-    } else {
+    } else if (!PARTIALS && a.fused_merge) {
       store_through4(ro, (unsigned)(((g * ns + split) * 2 * D + c) * 4), O);
       if (c == 0) store_through2(rml, (unsigned)((g * ns + split) * 8), make_float2(M, L));
+    } else {  // read by the merge launch: the kernel boundary publishes them
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, O), ro,
+                                             (unsigned)(((g * ns + split) * 2 * D + c) * 4), 0, 0);
+      if (c == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, make_float2(M, L)), rml,
+                                              (unsigned)((g * ns + split) * 8), 0, 0);
     }
   }
   if (PARTIALS || single || !a.fused_merge) return;  // a merge launch combines the splits
@@ -504,12 +510,42 @@ __device__ inline float4 merge_row_column(const SdpaArgs& a, long vrow, int col,
   return acc;
 }
 
+// Merge block -> (virtual row, slice of NSL).  With one head chunk per KV
+// head (decode), the attention workgroups of unit u = (b, KV head) were
+// dispatched to XCD u % 8 (round-robin over the 8 XCDs), where their
+// partials were written; the merge blocks of u's rows take the same residue,
+// block = 8 k + u % 8.  Placement affects speed only.
+__device__ inline bool merge_block_coords(const SdpaArgs& a, int bid, int nsl, int rows_per_unit,
+                                          long& vrow, int& slice) {
+  if (a.nchunk != 1) {
+    vrow = bid / nsl;
+    slice = bid % nsl;
+    return true;
+  }
+  const int per_unit = rows_per_unit * nsl;
+  const int k = bid >> 3;
+  const int u = (k / per_unit) * 8 + (bid & 7);
+  if (u >= a.B * a.Hkv) return false;  // padding of the last group of 8
+  const int rem = k % per_unit;
+  vrow = (long)u * rows_per_unit + rem / nsl;
+  slice = rem % nsl;
+  return true;
+}
+
+inline unsigned merge_grid_blocks(const SdpaArgs& a, int nsl, long rows, int rows_per_unit) {
+  if (a.nchunk != 1) return (unsigned)(rows * nsl);
+  const int bh = a.B * a.Hkv;
+  return (unsigned)((bh + 7) / 8 * 8 * rows_per_unit * nsl);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   using S = MergeShape<D>;
   const int lane = threadIdx.x;
-  const long vrow = blockIdx.x / S::NSL;
-  const int col = (blockIdx.x % S::NSL) * S::CW + lane % S::CW;
+  long vrow;
+  int slice;
+  if (!merge_block_coords(a, blockIdx.x, S::NSL, a.G * a.S_q, vrow, slice)) return;
+  const int col = slice * S::CW + lane % S::CW;
   float L;
   const float4 acc = merge_row_column<D>(a, vrow, col, lane, L);
   if (lane < S::CW) store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
@@ -520,7 +556,8 @@ int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
   constexpr int C4 = 2 * D / 4;
   constexpr int NSL = C4 / (C4 < 16 ? C4 : 16);
   const long rows = (long)a.B * a.Hq * a.S_q;
-  hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3((unsigned)(rows * NSL)), dim3(64), 0, s, a);
+  hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3(merge_grid_blocks(a, NSL, rows, a.G * a.S_q)),
+                     dim3(64), 0, s, a);
   return check_launch("sdpa split merge");
 }
 
@@ -538,7 +575,9 @@ __global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kern
   using S = MergeShape<D>;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const long orow = blockIdx.x;  // (b, h) over B * Hq
+  long orow;  // (b, h) over B * Hq
+  int unused_slice;
+  if (!merge_block_coords(a, blockIdx.x, 1, a.G, orow, unused_slice)) return;
   const long b = orow / a.Hq;
   const int h = (int)(orow - b * a.Hq);
   const int j = h / a.G;
@@ -590,7 +629,7 @@ __global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kern
 template <typename T, int D>
 int launch_gda_decode_merge_d(const SdpaArgs& a, hipStream_t s) {
   const long rows = (long)a.B * a.Hq;
-  hipLaunchKernelGGL((gda_decode_merge_kernel<T, D>), dim3((unsigned)rows),
+  hipLaunchKernelGGL((gda_decode_merge_kernel<T, D>), dim3(merge_grid_blocks(a, 1, rows, a.G)),
                      dim3(MergeShape<D>::NSL * 64), 0, s, a);
   return check_launch("gda decode merge");
 }
