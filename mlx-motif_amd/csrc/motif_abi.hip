@@ -55,12 +55,13 @@ Tuning& tuning() {
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max,
-                   int waves_pref, int wgs_per_cu) {
+                   int waves_pref, int wgs_per_cu, int gc_fixed) {
   SdpaPlan p{};
   const int G = Hkv > 0 ? Hq / Hkv : 1;
   const int GV = G * S_q;
   int gc = 1;
   while (gc < GV && gc < gc_max) gc *= 2;
+  if (gc_fixed > 0) gc = gc_fixed;
   p.gc = gc;
   p.nchunk = (GV + gc - 1) / gc;
   // 8-wave workgroups when their cross-wave LDS merge fits (D * gc <= 512
@@ -79,7 +80,8 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   // of it for kernels that run one wave per SIMD: wgs_per_cu = 1).
   // With several head chunks per KV head (a verify slab), each chunk's
   // workgroups should still cover the CUs: up to 3x more workgroups.
-  const int per_cu = wgs_per_cu > 0 ? wgs_per_cu * (p.nchunk < 3 ? p.nchunk : 3) : 8 / p.waves;
+  int per_cu = wgs_per_cu > 0 ? wgs_per_cu * (p.nchunk < 3 ? p.nchunk : 3) : 8 / p.waves;
+  if (gc_fixed > 0) per_cu = 1;  // multi-block kernels run one wave per SIMD
   int min_wgs = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count() * per_cu;
   int rows = kv_len > 0 ? kv_len : 1;
   int rps;
@@ -133,8 +135,10 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
   size_t ws = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0).workspace_bytes;
   if (D == kSdpaMfmaQD) {
     for (int gs = 32; gs <= 128; gs *= 2) {
+      const int nb = sdpa_q_blocks((Hkv > 0 ? Hq / Hkv : 1) * S_q, D, gs);
       const SdpaPlan p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),
-                                   kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu);
+                                   kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu,
+                                   nb > 1 ? nb * sdpa_gc_max_q(D, gs) : 0);
       if (p.workspace_bytes > ws) ws = p.workspace_bytes;
     }
   }

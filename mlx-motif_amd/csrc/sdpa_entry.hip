@@ -23,7 +23,8 @@ static bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a)
 // and plan/workspace set-up.
 static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, int B, int Hq,
                        int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal, float scale,
-                       void* ws, size_t ws_bytes, int gc_max, int waves_pref, int wgs_per_cu) {
+                       void* ws, size_t ws_bytes, int gc_max, int waves_pref, int wgs_per_cu,
+                       int gc_fixed = 0) {
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "%s: unknown dtype code %d", name, dtype);
   MOTIF_REQUIRE(B >= 1 && Hq >= 1 && Hkv >= 1 && S_q >= 1, "%s: B, H_q, H_kv, S_q must be >= 1",
@@ -33,7 +34,7 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
   MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
                 "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
   MOTIF_REQUIRE((long)B * Hkv * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
-  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, gc_max, waves_pref, wgs_per_cu);
+  p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, gc_max, waves_pref, wgs_per_cu, gc_fixed);
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hkv;
@@ -128,12 +129,28 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   SdpaArgs a{};
   SdpaPlan p{};
   // The matrix-core kernel puts (head, scale group) pairs on 16 columns and
-  // runs 4-wave workgroups, one per CU.
+  // runs 4-wave workgroups, one per CU.  When the virtual heads of a KV head
+  // fill 2-3 blocks of columns (a verify slab), one workgroup carries all of
+  // them (NB column blocks), provided the pointers suit that kernel; its plan
+  // has one head chunk of NB blocks.
   const bool mfma_q = D == kSdpaMfmaQD && dtype == MOTIF_F16 && tuning().mfma;
+  int nb = 1;
+  if (mfma_q && Hkv >= 1 && Hq % Hkv == 0) {
+    const int ng = D / gs;
+    const uintptr_t scale_bits = (uintptr_t)ks | (uintptr_t)kb | (uintptr_t)v1s |
+                                 (uintptr_t)v1b | (uintptr_t)v2s | (uintptr_t)v2b;
+    const uintptr_t data_bits = (uintptr_t)kd | (uintptr_t)v1d | (uintptr_t)v2d;
+    const bool wide_ok = ((data_bits | (uintptr_t)q) & 15u) == 0 &&
+                         (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
+                         tuning().rows_per_split % 16 == 0;
+    if (wide_ok) nb = sdpa_q_blocks(Hq / Hkv * S_q, D, gs);
+  }
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
                        ws_bytes, mfma_q ? sdpa_gc_max_q(D, gs) : sdpa_gc_max(D),
-                       mfma_q ? kSdpaMfmaQWaves : 0, mfma_q ? kSdpaMfmaQWgsPerCu : 0);
+                       mfma_q ? kSdpaMfmaQWaves : 0, mfma_q ? kSdpaMfmaQWgsPerCu : 0,
+                       nb > 1 ? nb * sdpa_gc_max_q(D, gs) : 0);
   if (rc != MOTIF_OK) return rc;
+  if (nb > 1) a.fused_merge = 0;  // multi-block launches always merge in a second launch
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (kd && ks && kb && v1d && v1s && v1b && v2d && v2s &&
                                            v2b)),
                 "%s: null tensor pointer", name);

@@ -368,7 +368,7 @@ __device__ void merge_splits(const SdpaArgs& a, long qrow0, int nvh) {
 // (b, KV head, chunk), merge all splits.  Called by every thread of the
 // workgroup after a barrier.  PARTIALS: always publish partials (also for a
 // single split) and leave the merge to a second launch.
-template <typename T, int D, int GC, int NW, bool PARTIALS = false>
+template <typename T, int D, int GC, int NW, bool PARTIALS = false, bool FUSED_MERGE = true>
 __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * D + kLdsPad],
                             const float (&lds_m)[NW][GC], const float (&lds_l)[NW][GC],
                             long qrow0, int nvh, int split, int unit) {
@@ -411,22 +411,26 @@ __device__ void wg_epilogue(const SdpaArgs& a, const float (&lds_o)[NW][GC][2 * 
                                               (unsigned)((g * ns + split) * 8), 0, 0);
     }
   }
-  if (PARTIALS || single || !a.fused_merge) return;  // a merge launch combines the splits
+  if constexpr (PARTIALS || !FUSED_MERGE) {
+    return;  // a merge launch combines the splits
+  } else {
+    if (single || !a.fused_merge) return;
 
-  // ---- last workgroup of this (b, KV head, chunk) combines all splits.
-  __shared__ int is_last;
-  wait_stores_done();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    unsigned t = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_SYSTEM);
-    is_last = (t == (unsigned)(a.nsplit - 1));
-    if (is_last)  // re-arm for the next call
-      __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    // ---- last workgroup of this (b, KV head, chunk) combines all splits.
+    __shared__ int is_last;
+    wait_stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned t = __hip_atomic_fetch_add(&a.counters[unit], 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_SYSTEM);
+      is_last = (t == (unsigned)(a.nsplit - 1));
+      if (is_last)  // re-arm for the next call
+        __hip_atomic_store(&a.counters[unit], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    merge_splits<T, D, GC, NW>(a, qrow0, nvh);
   }
-  __syncthreads();
-  if (!is_last) return;
-  merge_splits<T, D, GC, NW>(a, qrow0, nvh);
 }
 
 // ------------------------------------------------------- merge kernel ---

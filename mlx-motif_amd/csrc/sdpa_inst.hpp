@@ -55,6 +55,10 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
   const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
     const int ng = D / a.group_size;
+    // Multi-block plan (sdpa_q_run checked the pointers and shapes for it).
+    if (D == 128 && p.gc > sdpa_gc_max_q(D, a.group_size))
+      return launch_sdpa_mfma_q_wide(a, bits, a.group_size, p.gc / sdpa_gc_max_q(D, a.group_size),
+                                     nblocks, s);
     const uintptr_t scale_bits = (uintptr_t)a.ks | (uintptr_t)a.kb | (uintptr_t)a.v1s |
                                  (uintptr_t)a.v1b | (uintptr_t)a.v2s | (uintptr_t)a.v2b;
     const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;

@@ -202,18 +202,25 @@ __device__ inline void drop_rows_past(uint32_t (&out)[2], unsigned row0, unsigne
 // all but the first find the rows in L2 or the Infinity Cache.
 // DUAL: fused GDA decode step, as in sdpa_mfma_f16_kernel: head h < G of a
 // column scores against k, head G (the noise head) against k2.
+// NB: column blocks per wave.  Block bb holds heads bb*GC .. bb*GC+GC-1 of
+// the workgroup's NB*GC; the K and V codes of a tile are unpacked once and
+// feed every block's MFMAs, so a verify slab (e.g. 5 rows x GQA 4 = 20
+// virtual heads) runs as one pass instead of one workgroup per 8 heads.
+// The accumulators of NB > 1 blocks live in AGPRs at one wave per SIMD.
 template <int BITS, int GS, int GC, int NW, int U, int POL = kCachePolicyStream,
-          bool DUAL = false>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+          bool DUAL = false, int NB = 1>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NB > 1 ? 1 : 2)))
 sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int D = 128;
   constexpr int NG = D / GS;  // scale groups per row
+  constexpr int GCW = NB * GC;  // heads per workgroup
   using Tile = QTile<BITS, NG, DUAL>;
   constexpr int NS = Tile::NS;
   constexpr int WPR = Tile::WPR;
   constexpr int KW = Tile::KW;
   constexpr int VW = Tile::VW;
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
+  static_assert(!DUAL || NB == 1, "the fused decode step uses one column block");
   // Lazy-rescale slack (see kRescaleSlackF16): here p also multiplies the V
   // scale in fp16, so p * s must stay finite.  An fp16 cache row spans at
   // most 2 * 65504, so s <= 131008 / 15 (q4) or / 255 (q8), and 2^slack * s
@@ -230,21 +237,28 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int bk = unit / a.nchunk;
   const int b = bk / a.Hkv;
   const int kvh = bk % a.Hkv;
-  const int vh0 = chunk * GC;
-  const int nvh = min(GC, a.GV - vh0);
+  const int vh0 = chunk * GCW;
+  const int nvh = min(GCW, a.GV - vh0);
   // First output row: y row (non-DUAL) or partial row (DUAL) of head 0.
   const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
                           : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
-  const int h = col % GC;    // head of this column
   const int grp = col / GC;  // scale group of this column
-  const bool col_used = grp < NG && h < nvh;
+  int hb[NB];                // head (within the workgroup) of this column, per block
+  bool used[NB];
+  int lim[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    hb[bb] = bb * GC + col % GC;
+    used[bb] = grp < NG && hb[bb] < nvh;
+    lim[bb] = hb[bb] < nvh ? vhead_limit(a, vh0 + hb[bb]) : 0;
+  }
+  const int h = hb[0];
   const int gsel = grp < NG ? grp : 0;  // group whose scales this lane reads
   // v_perm selector keeping half (gsel & 1) of two words: low word = row r.
   const uint32_t sel = (gsel & 1) ? 0x07060302u : 0x05040100u;
   int max_lim = 0;
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
-  const int lim = h < nvh ? vhead_limit(a, vh0 + h) : 0;
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const int nrows = max(r_end - r_begin, 0);
@@ -310,49 +324,58 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // latency and q's overlap.
   Tile ta[U], tb[U];
   int t0 = wave * 16;
-  uint4 qraw[4];
-  {
-    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (h < nvh ? h : 0)) * D + 32 * blk;
+  uint4 qraw[NB][4];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    const uint16_t* qp =
+        (const uint16_t*)a.q + (qrow0 + (hb[bb] < nvh ? hb[bb] : 0)) * D + 32 * blk;
     if constexpr (DUAL) {
       qp = h < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + h) * D
                    : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
       qp += 32 * blk;
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qraw[s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
+    for (int s = 0; s < 4; ++s) qraw[bb][s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
   load_tiles(ta, t0);
 
   // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
   // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
   // column's group.  qsum: sum of q_h over the column's group.
-  half8_t qb[4];
-  float qsum = 0.f;
-  {
-    const bool mine = col_used && (32 * blk) / GS == grp;
+  half8_t qb[NB][4];
+  float qsum[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    const bool mine = used[bb] && (32 * blk) / GS == grp;
+    qsum[bb] = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const half8_t raw = __builtin_bit_cast(half8_t, qraw[s]);
+      const half8_t raw = __builtin_bit_cast(half8_t, qraw[bb][s]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const _Float16 v = mine ? raw[BITS == 4 ? q4_order(j) : j] : (_Float16)0.f;
-        qb[s][j] = v;
-        qsum += (float)v;
+        qb[bb][s][j] = v;
+        qsum[bb] += (float)v;
       }
     }
-    qsum += __shfl_xor(qsum, 16);
-    qsum += __shfl_xor(qsum, 32);
+    qsum[bb] += __shfl_xor(qsum[bb], 16);
+    qsum[bb] += __shfl_xor(qsum[bb], 32);
   }
 
-  floatx4 acc1[8], acc2[8], accl;
+  floatx4 acc1[NB][8], acc2[NB][8], accl[NB];
+  float beta1[NB], beta2[NB];  // sum_r p * b_V over this lane's rows
+  float m_run[NB];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    acc1[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int bb = 0; bb < NB; ++bb) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc1[bb][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      acc2[bb][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    accl[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    beta1[bb] = beta2[bb] = 0.f;
+    m_run[bb] = kNegSentinel;
   }
-  accl = floatx4{0.f, 0.f, 0.f, 0.f};
-  float beta1 = 0.f, beta2 = 0.f;  // sum_r p * b_V over this lane's rows
-  float m_run = kNegSentinel;
   const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
   const uint32_t magic = magic_vgpr();
 
@@ -372,7 +395,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
         for (int t = 0; t < NS; ++t) drop_rows_past(sw[t], rrow0, (unsigned)nrows);
       }
-      floatx4 sacc = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 sacc[NB];
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) sacc[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         half8_t ka;
@@ -381,7 +406,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         } else {
           ka = q8_words_codes(T[u].k[2 * s], T[u].k[2 * s + 1]);
         }
-        sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sacc, 0, 0, 0);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+          sacc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[bb][s], sacc[bb], 0, 0, 0);
       }
       uint32_t skw[2] = {sw[0][0], sw[0][1]}, bkw[2] = {sw[1][0], sw[1][1]};
       if constexpr (DUAL) {  // the noise head's column: k2 codes and scales
@@ -394,11 +421,11 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           } else {
             ka = q8_words_codes(T[u].k2[2 * s], T[u].k2[2 * s + 1]);
           }
-          s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], s2, 0, 0, 0);
+          s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[0][s], s2, 0, 0, 0);
         }
         const bool noise = h == a.G;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sacc[r] = noise ? s2[r] : sacc[r];
+        for (int r = 0; r < 4; ++r) sacc[0][r] = noise ? s2[r] : sacc[0][r];
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
           skw[p] = noise ? sw[6][p] : skw[p];
@@ -409,51 +436,55 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       const half2_t bk01 = as_h2(bkw[0]), bk23 = as_h2(bkw[1]);
       const float skr[4] = {(float)sk01.x, (float)sk01.y, (float)sk23.x, (float)sk23.y};
       const float bkr[4] = {(float)bk01.x, (float)bk01.y, (float)bk23.x, (float)bk23.y};
-      float sc[4];
-      float mx = kNegSentinel;
+      half4_t w1[NB], w2[NB], pbb[NB];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // Unused columns have Q^T = 0 and qsum = 0, so t = 0 there without
-        // a select (their scale words are finite cache values or 0).
-        float t = fmaf(skr[r], sacc[r], bkr[r] * qsum);
-        t = sum_group_columns<GC>(t);
-        const int row = row0 + r;
-        const bool ok = row < r_end && row < lim;
-        sc[r] = ok ? t * a.qscale : kNegSentinel;
-        mx = fmaxf(mx, sc[r]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (__ballot(mx > m_run + kSlack) != 0) {
-        const float m_new = fmaxf(m_run, mx);
-        const float fac = fast_exp2(m_run - m_new);
+      for (int bb = 0; bb < NB; ++bb) {
+        float sc[4];
+        float mx = kNegSentinel;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          acc1[j] *= fac;
-          acc2[j] *= fac;
+        for (int r = 0; r < 4; ++r) {
+          // Unused columns have Q^T = 0 and qsum = 0, so t = 0 there without
+          // a select (their scale words are finite cache values or 0).
+          float t = fmaf(skr[r], sacc[bb][r], bkr[r] * qsum[bb]);
+          t = sum_group_columns<GC>(t);
+          const int row = row0 + r;
+          const bool ok = row < r_end && row < lim[bb];
+          sc[r] = ok ? t * a.qscale : kNegSentinel;
+          mx = fmaxf(mx, sc[r]);
         }
-        accl *= fac;
-        beta1 *= fac;
-        beta2 *= fac;
-        m_run = m_new;
-      }
-      float p[4];
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (__ballot(mx > m_run[bb] + kSlack) != 0) {
+          const float m_new = fmaxf(m_run[bb], mx);
+          const float fac = fast_exp2(m_run[bb] - m_new);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        p[r] = sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run) : 0.f;
-      // p rounded to fp16 once; the V weights, the bias terms and l all use
-      // these same values.
-      const half2_t p01 = half2_t{(_Float16)p[0], (_Float16)p[1]};
-      const half2_t p23 = half2_t{(_Float16)p[2], (_Float16)p[3]};
-      const half4_t pb = {p01.x, p01.y, p23.x, p23.y};
-      const half2_t w1a = p01 * as_h2(sw[2][0]), w1b = p23 * as_h2(sw[2][1]);
-      const half2_t w2a = p01 * as_h2(sw[4][0]), w2b = p23 * as_h2(sw[4][1]);
-      const half4_t w1 = {w1a.x, w1a.y, w1b.x, w1b.y};
-      const half4_t w2 = {w2a.x, w2a.y, w2b.x, w2b.y};
-      beta1 = __builtin_amdgcn_fdot2(p01, as_h2(sw[3][0]), beta1, false);
-      beta1 = __builtin_amdgcn_fdot2(p23, as_h2(sw[3][1]), beta1, false);
-      beta2 = __builtin_amdgcn_fdot2(p01, as_h2(sw[5][0]), beta2, false);
-      beta2 = __builtin_amdgcn_fdot2(p23, as_h2(sw[5][1]), beta2, false);
+          for (int j = 0; j < 8; ++j) {
+            acc1[bb][j] *= fac;
+            acc2[bb][j] *= fac;
+          }
+          accl[bb] *= fac;
+          beta1[bb] *= fac;
+          beta2[bb] *= fac;
+          m_run[bb] = m_new;
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          p[r] = sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run[bb]) : 0.f;
+        // p rounded to fp16 once; the V weights, the bias terms and l all
+        // use these same values.
+        const half2_t p01 = half2_t{(_Float16)p[0], (_Float16)p[1]};
+        const half2_t p23 = half2_t{(_Float16)p[2], (_Float16)p[3]};
+        pbb[bb] = half4_t{p01.x, p01.y, p23.x, p23.y};
+        const half2_t w1a = p01 * as_h2(sw[2][0]), w1b = p23 * as_h2(sw[2][1]);
+        const half2_t w2a = p01 * as_h2(sw[4][0]), w2b = p23 * as_h2(sw[4][1]);
+        w1[bb] = half4_t{w1a.x, w1a.y, w1b.x, w1b.y};
+        w2[bb] = half4_t{w2a.x, w2a.y, w2b.x, w2b.y};
+        beta1[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[3][0]), beta1[bb], false);
+        beta1[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[3][1]), beta1[bb], false);
+        beta2[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[5][0]), beta2[bb], false);
+        beta2[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[5][1]), beta2[bb], false);
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         uint32_t x1[4], x2[4];
@@ -464,10 +495,15 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         }
         const half4_t a1 = v_codes<BITS>(x1, BITS == 4 ? i : (i & 3), magic);
         const half4_t a2 = v_codes<BITS>(x2, BITS == 4 ? i : (i & 3), magic);
-        acc1[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, w1, acc1[i], 0, 0, 0);
-        acc2[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2, w2, acc2[i], 0, 0, 0);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          acc1[bb][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, w1[bb], acc1[bb][i], 0, 0, 0);
+          acc2[bb][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a2, w2[bb], acc2[bb][i], 0, 0, 0);
+        }
       }
-      accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pb, accl, 0, 0, 0);
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb)
+        accl[bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pbb[bb], accl[bb], 0, 0, 0);
     }
   };
 
@@ -485,42 +521,49 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     t0 += kStep;
   }
 
-  // Bias terms: sum the four row blocks of each column.
-  beta1 += __shfl_xor(beta1, 16);
-  beta1 += __shfl_xor(beta1, 32);
-  beta2 += __shfl_xor(beta2, 16);
-  beta2 += __shfl_xor(beta2, 32);
-
   // acc[i][r] of lane (col, blk) is channel 8*(4*blk + r) + i for head h; it
   // is valid where that channel's group is the column's group, i.e. where
   // the row block's 32 channels belong to group grp.
-  __shared__ __attribute__((aligned(16))) float lds_o[NW][GC][2 * D + kLdsPad];
-  __shared__ float lds_m[NW][GC];
-  __shared__ float lds_l[NW][GC];
-  if (col_used && (32 * blk) / GS == grp) {
+  __shared__ __attribute__((aligned(16))) float lds_o[NW][GCW][2 * D + kLdsPad];
+  __shared__ float lds_m[NW][GCW];
+  __shared__ float lds_l[NW][GCW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ch = 8 * (4 * blk + r);
-      *reinterpret_cast<float4*>(&lds_o[wave][h][ch]) =
-          make_float4(acc1[0][r] + beta1, acc1[1][r] + beta1, acc1[2][r] + beta1,
-                      acc1[3][r] + beta1);
-      *reinterpret_cast<float4*>(&lds_o[wave][h][ch + 4]) =
-          make_float4(acc1[4][r] + beta1, acc1[5][r] + beta1, acc1[6][r] + beta1,
-                      acc1[7][r] + beta1);
-      *reinterpret_cast<float4*>(&lds_o[wave][h][D + ch]) =
-          make_float4(acc2[0][r] + beta2, acc2[1][r] + beta2, acc2[2][r] + beta2,
-                      acc2[3][r] + beta2);
-      *reinterpret_cast<float4*>(&lds_o[wave][h][D + ch + 4]) =
-          make_float4(acc2[4][r] + beta2, acc2[5][r] + beta2, acc2[6][r] + beta2,
-                      acc2[7][r] + beta2);
+  for (int bb = 0; bb < NB; ++bb) {
+    // Bias terms: sum the four row blocks of each column.
+    float be1 = beta1[bb], be2 = beta2[bb];
+    be1 += __shfl_xor(be1, 16);
+    be1 += __shfl_xor(be1, 32);
+    be2 += __shfl_xor(be2, 16);
+    be2 += __shfl_xor(be2, 32);
+    const int hh = hb[bb];
+    if (used[bb] && (32 * blk) / GS == grp) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ch = 8 * (4 * blk + r);
+        *reinterpret_cast<float4*>(&lds_o[wave][hh][ch]) =
+            make_float4(acc1[bb][0][r] + be1, acc1[bb][1][r] + be1, acc1[bb][2][r] + be1,
+                        acc1[bb][3][r] + be1);
+        *reinterpret_cast<float4*>(&lds_o[wave][hh][ch + 4]) =
+            make_float4(acc1[bb][4][r] + be1, acc1[bb][5][r] + be1, acc1[bb][6][r] + be1,
+                        acc1[bb][7][r] + be1);
+        *reinterpret_cast<float4*>(&lds_o[wave][hh][D + ch]) =
+            make_float4(acc2[bb][0][r] + be2, acc2[bb][1][r] + be2, acc2[bb][2][r] + be2,
+                        acc2[bb][3][r] + be2);
+        *reinterpret_cast<float4*>(&lds_o[wave][hh][D + ch + 4]) =
+            make_float4(acc2[bb][4][r] + be2, acc2[bb][5][r] + be2, acc2[bb][6][r] + be2,
+                        acc2[bb][7][r] + be2);
+      }
+    }
+    if (col < GC && hh < nvh && blk == 0) {
+      lds_m[wave][hh] = m_run[bb];
+      lds_l[wave][hh] = accl[bb][0];
     }
   }
-  if (col < GC && h < nvh && blk == 0) {
-    lds_m[wave][h] = m_run;
-    lds_l[wave][h] = accl[0];
-  }
   __syncthreads();
-  wg_epilogue<half_t, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+  // The in-kernel merge's LDS does not fit beside NB > 1 blocks' staging:
+  // those launches always use the merge launch.
+  wg_epilogue<half_t, D, GCW, NW, DUAL, NB == 1>(a, lds_o, lds_m, lds_l, qrow0, nvh, split,
+                                                 unit);
 }
 
 // Packed cache, head_dim 128, fp16 scales: heads x groups <= 16 columns.
@@ -597,6 +640,34 @@ inline int launch_gda_decode_mfma_q(const SdpaArgs& a, int bits, int gs, int gc,
   if (gs == 32) return launch_gda_decode_mfma_q_gs<8, 32>(a, gc, nblocks, st);
   if (gs == 64) return launch_gda_decode_mfma_q_gs<8, 64>(a, gc, nblocks, st);
   return launch_gda_decode_mfma_q_gs<8, 128>(a, gc, nblocks, st);
+}
+
+// Two column blocks of GC = 16 / groups (at most 8) heads per wave, one
+// head chunk (all virtual heads of the KV head in one workgroup).
+template <int BITS, int GS>
+int launch_sdpa_mfma_q_wide_gs(const SdpaArgs& a, int nb, int nblocks, hipStream_t st) {
+  constexpr int NG = 128 / GS;
+  constexpr int GC = 16 / NG < 8 ? 16 / NG : 8;
+  if (nb != 2 || a.nchunk != 1) {
+    set_error("sdpa_dual_v_q: no variant with %d column blocks and %d head chunks", nb,
+              a.nchunk);
+    return MOTIF_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, GC, 4, 1, kCachePolicyStream, false, 2>),
+                     dim3(nblocks), dim3(256), 0, st, a);
+  return check_launch("sdpa_dual_v_q (mfma, column blocks)");
+}
+
+inline int launch_sdpa_mfma_q_wide(const SdpaArgs& a, int bits, int gs, int nb, int nblocks,
+                                   hipStream_t st) {
+  if (bits == 4) {
+    if (gs == 32) return launch_sdpa_mfma_q_wide_gs<4, 32>(a, nb, nblocks, st);
+    if (gs == 64) return launch_sdpa_mfma_q_wide_gs<4, 64>(a, nb, nblocks, st);
+    return launch_sdpa_mfma_q_wide_gs<4, 128>(a, nb, nblocks, st);
+  }
+  if (gs == 32) return launch_sdpa_mfma_q_wide_gs<8, 32>(a, nb, nblocks, st);
+  if (gs == 64) return launch_sdpa_mfma_q_wide_gs<8, 64>(a, nb, nblocks, st);
+  return launch_sdpa_mfma_q_wide_gs<8, 128>(a, nb, nblocks, st);
 }
 
 inline int launch_sdpa_mfma_q(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,

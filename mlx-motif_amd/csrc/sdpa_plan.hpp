@@ -79,8 +79,11 @@ constexpr int kMaxSplits = 256;
 // gc_max: the largest per-workgroup head count compiled for this head dim.
 // waves_pref: waves per workgroup (0: 8 where the LDS merge fits, else 4);
 // wgs_per_cu: workgroups one CU holds at once (0: 8 / waves).
+// gc_fixed > 0: exactly that many heads per workgroup (the packed-cache
+// kernel's multi-block launches, which also hold one workgroup per CU), in
+// place of a power of two <= gc_max.
 SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max,
-                   int waves_pref, int wgs_per_cu);
+                   int waves_pref, int wgs_per_cu, int gc_fixed = 0);
 
 // Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
 // workgroups at one wave per SIMD, one per CU.
@@ -98,6 +101,18 @@ inline int sdpa_gc_max_q(int D, int group_size) {
   const int lim = 16 / (ng > 0 ? ng : 1);
   const int base = sdpa_gc_max(D);
   return lim < base ? lim : base;
+}
+
+// Column blocks per wave of the packed-cache kernel for GV virtual heads per
+// KV head: 2 when they need more than one block of sdpa_gc_max_q(D, gs)
+// heads but fit two (one pass over the cache instead of two head chunks),
+// else 1.  Measured on a q8 slab at 32768 rows: 16 heads 41.9 -> 37.6 us; for
+// 20 heads two chunks of two blocks were slower than three chunks of one
+// (55.8 vs 52.9 us), and a third block's accumulators spill.
+constexpr int kSdpaMfmaQMaxBlocks = 2;
+inline int sdpa_q_blocks(int GV, int D, int group_size) {
+  const int gcq = sdpa_gc_max_q(D, group_size);
+  return GV > gcq && GV <= kSdpaMfmaQMaxBlocks * gcq ? kSdpaMfmaQMaxBlocks : 1;
 }
 
 }  // namespace motif

@@ -53,8 +53,10 @@ def test_rows_single_row_equals_decode(gpu, rng):
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("S,cap,kv_len", [(5, 512, 400), (3, 256, 3)])
+@pytest.mark.parametrize("S,cap,kv_len", [(5, 512, 400), (3, 256, 3), (4, 512, 300)])
 def test_rows_packed(gpu, rng, bits, S, cap, kv_len):
+    """S x GQA 4 virtual heads: 12 and 16 take the two-column-block kernel
+    (one workgroup per KV head and split), 20 three head chunks."""
     from mlx_motif.kernels import sdpa_dual_v_q4_rows
 
     q = randn(rng, (1, 32, S, 128), "f16")
@@ -79,4 +81,20 @@ def test_verify_slab_q8_32k(gpu, rng):
     y = sdpa_dual_v_q4_rows(np_to_torch(q, torch_dtype("f16"), gpu), *(G(t) for t in trips),
                             1 / np.sqrt(128), group_size=64, bits=8, kv_len=cap)
     ref = O.sdpa_dual_v_q(q, *trips, 1 / np.sqrt(128), 64, 8, cap, causal=True)
+    assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_two_column_blocks_decode_group_size_32(gpu, rng, bits):
+    """GQA 6 at group size 32: 6 heads x 4 scale groups need two column
+    blocks of 4 heads in one workgroup."""
+    from mlx_motif.kernels import sdpa_dual_v_q4
+
+    q = randn(rng, (1, 48, 1, 128), "f16")
+    trips = [O.quantize(randn(rng, (1, 8, 512, 128), "f16"), 32, bits) for _ in range(3)]
+    G = lambda t: (np_to_torch(t[0], None, gpu), np_to_torch(t[1], torch_dtype("f16"), gpu),  # noqa: E731
+                   np_to_torch(t[2], torch_dtype("f16"), gpu))
+    y = sdpa_dual_v_q4(np_to_torch(q, torch_dtype("f16"), gpu), *(G(t) for t in trips),
+                       1 / np.sqrt(128), group_size=32, bits=bits, kv_len=437)
+    ref = O.sdpa_dual_v_q(q, *trips, 1 / np.sqrt(128), 32, bits, 437)
     assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
