@@ -112,6 +112,37 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   return p;
 }
 
+PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
+  PrefillPlan p{};
+  const int G = Hkv > 0 ? Hq / Hkv : 1;
+  const int GV = G * S_q;
+  const int cus = device_cu_count();
+  const int bh = B * Hkv;
+  // 8 waves (128 virtual heads per block) when that still gives a block per
+  // CU, else 4.
+  p.waves = (long)bh * ((GV + 127) / 128) >= cus ? 8 : 4;
+  p.nqb = (GV + p.waves * 16 - 1) / (p.waves * 16);
+  const long units = (long)bh * p.nqb;
+  const int rows = kv_len > 0 ? kv_len : 1;
+  int nsplit = units >= cus ? 1 : (int)((cus + units - 1) / units);
+  const int max_split = (rows + 127) / 128;  // at least 128 rows per split
+  if (nsplit > max_split) nsplit = max_split;
+  if (nsplit > kMaxSplits) nsplit = kMaxSplits;
+  if (nsplit < 1) nsplit = 1;
+  int rps = (rows + nsplit - 1) / nsplit;
+  rps = (rps + kPrefillTileRowsHost - 1) / kPrefillTileRowsHost * kPrefillTileRowsHost;
+  p.rows_per_split = rps;
+  p.nsplit = (rows + rps - 1) / rps;
+  if (p.nsplit < 1) p.nsplit = 1;
+  if (p.nsplit > 1) {
+    const size_t vrows = (size_t)B * Hq * S_q;
+    p.workspace_bytes = round_up(vrows * sizeof(unsigned), 256) +
+                        round_up(vrows * p.nsplit * 2 * D * sizeof(float), 256) +
+                        round_up(vrows * p.nsplit * 2 * sizeof(float), 256);
+  }
+  return p;
+}
+
 }  // namespace motif
 
 using namespace motif;
@@ -140,6 +171,10 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
                                    kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu,
                                    nb > 1 ? nb * sdpa_gc_max_q(D, gs) : 0);
       if (p.workspace_bytes > ws) ws = p.workspace_bytes;
+    }
+    if ((Hq / Hkv) * S_q >= kPrefillMinHeads) {
+      const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
+      if (pp.workspace_bytes > ws) ws = pp.workspace_bytes;
     }
   }
   return ws;

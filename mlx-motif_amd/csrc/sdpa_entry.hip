@@ -99,6 +99,34 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   a.v2 = v2;
   a.y = y;
   hipStream_t s = (hipStream_t)stream;
+  // Many virtual heads per KV head (a prefill chunk or a long verify slab):
+  // the kernel with LDS-shared K/V tiles reads the cache once per block of
+  // up to 128 heads instead of once per 8.
+  if (dtype == MOTIF_F16 && D == 128 && tuning().mfma && a.GV >= kPrefillMinHeads &&
+      aligned(q, 16) && aligned(y, 16) && aligned(k, 16) && aligned(v1, 16) &&
+      aligned(v2, 16)) {
+    const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
+    if (pp.nsplit > 1 && (ws == nullptr || ws_bytes < pp.workspace_bytes)) {
+      set_error("%s: workspace of %zu bytes needed, %zu given", name, pp.workspace_bytes,
+                ws == nullptr ? (size_t)0 : ws_bytes);
+      return MOTIF_ERR_WORKSPACE;
+    }
+    a.nchunk = pp.nqb;
+    a.nsplit = pp.nsplit;
+    a.rows_per_split = pp.rows_per_split;
+    a.fused_merge = 0;
+    if (pp.nsplit > 1) {
+      char* w = (char*)ws;
+      const size_t vrows = (size_t)B * Hq * S_q;
+      const size_t cbytes = (vrows * sizeof(unsigned) + 255) / 256 * 256;
+      const size_t obytes = (vrows * pp.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
+      a.counters = (unsigned*)w;
+      a.part_o = (float*)(w + cbytes);
+      a.part_ml = (float*)(w + cbytes + obytes);
+    }
+    rc = launch_sdpa_prefill_f16(a, pp.waves, B * Hkv * pp.nqb * pp.nsplit, s);
+    return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
+  }
   switch (dtype) {
     case MOTIF_F16: rc = dispatch_sdpa_fp_f16(a, p, D, s); break;
     case MOTIF_BF16: rc = dispatch_sdpa_fp_bf16(a, p, D, s); break;

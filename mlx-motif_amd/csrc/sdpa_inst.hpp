@@ -6,6 +6,7 @@
 #include "sdpa_impl.hpp"
 #include "sdpa_mfma.hpp"
 #include "sdpa_mfma_q.hpp"
+#include "sdpa_prefill.hpp"
 
 namespace motif {
 
@@ -99,6 +100,16 @@ int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int n
     return launch_gda_decode_merge_d<half_t, 128>(a, s);
   }
   set_error("gda_decode: no fused variant for this element type");
+  return MOTIF_ERR_UNSUPPORTED;
+}
+
+// Multi-row attention with LDS-shared K/V tiles (fp16 cache, head_dim 128).
+int MOTIF_CAT(launch_sdpa_prefill_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, int nblocks,
+                                                 hipStream_t s) {
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
+    return launch_prefill_kernel_f16(a, waves, nblocks, s);
+  }
+  set_error("sdpa_dual_v_rows: no shared-tile variant for this element type");
   return MOTIF_ERR_UNSUPPORTED;
 }
 

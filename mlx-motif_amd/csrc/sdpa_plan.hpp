@@ -85,6 +85,20 @@ constexpr int kMaxSplits = 256;
 SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_max,
                    int waves_pref, int wgs_per_cu, int gc_fixed = 0);
 
+// Plan of the multi-row kernel with LDS-shared K/V tiles (fp16 cache, head
+// dim 128): query blocks of waves x 16 virtual heads, rows split over
+// workgroups only when the query blocks do not fill the GPU.  Used when a KV
+// head has at least kPrefillMinHeads virtual heads.
+constexpr int kPrefillMinHeads = 64;
+constexpr int kPrefillTileRowsHost = 32;  // KV rows per tile (kPrefillTileRows)
+struct PrefillPlan {
+  int waves;  // 4 or 8
+  int nqb;    // query blocks per (b, KV head)
+  int nsplit, rows_per_split;
+  size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1
+};
+PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
+
 // Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
 // workgroups at one wave per SIMD, one per CU.
 constexpr int kSdpaMfmaQD = 128;

@@ -1,0 +1,90 @@
+"""Parity of the multi-row kernel with LDS-shared K/V tiles (fp16 cache,
+head_dim 128), which ``motif_sdpa_dual_v_rows`` uses once a KV head has at
+least 64 virtual heads (query heads x query rows): chunked prefill and long
+verify slabs.  Against the oracle with the bottom-right causal mask of the
+multi-row fallback (model.py:769-807) or no mask; max |gpu - oracle| <= 2e-3
+(fp32 accumulation, fp16 output).
+
+Cases: query blocks of 4 and 8 waves, row splits with the merge launch (few
+query blocks) and without (many), causal rows that see no key (kv_len < S),
+poisoned padding past kv_len, and agreement with the chunked decode kernels
+(mfma switched off routes the same call through the VALU kernels).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import np_to_torch, randn, torch_to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal, poison=False, scale_qk=1.0):
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    D = 128
+    q = randn(rng, (B, Hq, S, D), "f16", scale_qk)
+    k, v1, v2 = (randn(rng, (B, Hkv, cap, D), "f16") for _ in range(3))
+    if poison and kv_len < cap:
+        for t in (k, v1, v2):
+            t[:, :, kv_len:] = 1e4
+    T = lambda a: np_to_torch(a, torch.float16, gpu)  # noqa: E731
+    print(f"prefill B={B} Hq={Hq} Hkv={Hkv} S={S} cap={cap} kv_len={kv_len} causal={causal}",
+          flush=True)
+    y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(D), kv_len=kv_len, causal=causal)
+    torch.cuda.synchronize()
+    assert y.shape == (B, Hq, S, 2 * D)
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(D), kv_len, causal)
+    got = torch_to_np(y)
+    assert np.isfinite(got).all()
+    return float(np.max(np.abs(got - ref))), y, (q, k, v1, v2)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,cap,kv_len", [
+    (1, 32, 8, 16, 3328, 3204),    # 64 heads per KV head: one 4-wave block, row splits
+    (1, 32, 8, 64, 1280, 1100),    # 256 heads: 8-wave blocks? (few units -> splits)
+    (1, 32, 8, 200, 1024, 1000),   # ragged last block
+    (2, 8, 2, 96, 512, 400),       # batch 2
+    (1, 40, 8, 33, 768, 700),      # GQA 5, ragged
+])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_matches_oracle(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal):
+    err, *_ = _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal)
+    assert err <= 2e-3, f"S={S} kv_len={kv_len} causal={causal}: {err:.3e}"
+
+
+def test_prefill_long_chunk(gpu, rng):
+    """A 512-row prefill chunk over a 3716-row cache (many query blocks, no
+    row split)."""
+    err, *_ = _run(gpu, rng, 1, 32, 8, 512, 3840, 3716, True)
+    assert err <= 2e-3, f"{err:.3e}"
+
+
+def test_prefill_rows_without_keys_and_poison(gpu, rng):
+    """kv_len < S: with the bottom-right mask the first S - kv_len rows see
+    no key and come out zero; rows past kv_len are poisoned."""
+    err, y, _ = _run(gpu, rng, 1, 16, 4, 80, 256, 50, True, poison=True)
+    assert err <= 2e-3
+    assert not torch_to_np(y)[:, :, :30].any()
+
+
+def test_prefill_agrees_with_valu_kernels(gpu, rng):
+    import torch
+
+    from mlx_motif import _native
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    err, y, (q, k, v1, v2) = _run(gpu, rng, 1, 32, 8, 24, 640, 600, True)
+    T = lambda a: np_to_torch(a, torch.float16, gpu)  # noqa: E731
+    _native.set_tuning("mfma", 0)
+    try:
+        y2 = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=600, causal=True)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning("mfma", 1)
+    assert float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2)))) <= 2e-3
