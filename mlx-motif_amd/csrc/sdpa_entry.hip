@@ -170,7 +170,7 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
     const uintptr_t data_bits = (uintptr_t)kd | (uintptr_t)v1d | (uintptr_t)v2d;
     const bool wide_ok = ((data_bits | (uintptr_t)q) & 15u) == 0 &&
                          (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
-                         tuning().rows_per_split % 16 == 0;
+                         kv_len <= kMfmaMaxRows;
     if (wide_ok) nb = sdpa_q_blocks(Hq / Hkv * S_q, D, gs);
   }
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
@@ -321,7 +321,8 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
                 "%s: null pointer", name);
   hipStream_t s = (hipStream_t)stream;
   const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
-                     aligned(q1, 16) && aligned(q2, 16) && aligned(k1, 16) && aligned(k2, 16) &&
+                     kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
+                     aligned(k1, 16) && aligned(k2, 16) &&
                      aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8);
   if (fused) {
     SdpaArgs a = gda_decode_args(L, L.plan, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
@@ -423,7 +424,7 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
   const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
                      gc * ng <= 16 && (data_bits & 15u) == 0 &&
                      (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
-                     L.plan_q.rows_per_split % 16 == 0 && aligned(q1, 16) && aligned(q2, 16) &&
+                     kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
                      aligned(y, 8);
   if (fused) {
     SdpaArgs a = gda_decode_args(L, L.plan_q, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,

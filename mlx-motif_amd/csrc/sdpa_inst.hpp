@@ -17,7 +17,8 @@ int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan
                                               hipStream_t s) {
   const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
-    if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0)
+    if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0 &&
+        a.kv_len <= kMfmaMaxRows)
       return launch_sdpa_mfma_f16(a, p.gc, p.waves, nblocks, s);
   }
   switch (D) {
@@ -64,7 +65,7 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
                                  (uintptr_t)a.v1b | (uintptr_t)a.v2s | (uintptr_t)a.v2b;
     const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;
     const bool aligned = (data_bits & 15u) == 0 && (scale_bits & (ng == 1 ? 7u : 15u)) == 0 &&
-                         a.kv_cap % 4 == 0 && a.rows_per_split % 16 == 0;
+                         a.kv_cap % 4 == 0 && a.kv_len <= kMfmaMaxRows;
     if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16)
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
   }

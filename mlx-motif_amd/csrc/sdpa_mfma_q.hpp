@@ -227,7 +227,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // stays below 65504 with slack 2 (q4) or 6 (q8).
   constexpr float kSlack = BITS == 4 ? 2.f : 6.f;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave index as a wave-uniform (scalar) value: tile rows and the tests on
+  // them are then scalar, and so are the branches that depend on them.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int blk = lane >> 4;
 
@@ -259,17 +261,19 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const uint32_t sel = (gsel & 1) ? 0x07060302u : 0x05040100u;
   int max_lim = 0;
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
-  const int r_begin = split * a.rows_per_split;
-  const int r_end = min(r_begin + a.rows_per_split, max_lim);
-  const int nrows = max(r_end - r_begin, 0);
-
-  const long hrow0 = (long)bk * a.kv_cap + r_begin;  // first cache row of this split
-  const auto rk = stream_rsrc(a.kd + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
-  const auto rv1 = stream_rsrc(a.v1d + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
-  const auto rv2 = stream_rsrc(a.v2d + hrow0 * WPR, (unsigned)(nrows * WPR * 4));
-  // Scale resources cover whole 4-row groups (kv_cap % 4 == 0 and the split
-  // starts at a multiple of 16 rows, so this stays inside the cache).
-  const unsigned sbytes = (unsigned)(((nrows + 3) & ~3) * NG * 2);
+  // Rows are dealt to the splits in blocks of NW 16-row tiles, round robin,
+  // as in sdpa_mfma_f16_kernel: tile k of wave w in split s is tile
+  // (k * nsplit + s) * NW + w of the KV head.  The resources cover rows
+  // [0, max_lim) of the KV head (scales: whole 4-row groups, inside the
+  // cache since kv_cap % 4 == 0); rows past them read 0.
+  const int ns = a.nsplit;
+  auto tile_row = [&](int k) { return 16 * ((k * ns + split) * NW + wave); };
+  const long hrow0 = (long)bk * a.kv_cap;  // first cache row of this KV head
+  const unsigned dbytes = (unsigned)(max_lim * WPR * 4);
+  const auto rk = stream_rsrc(a.kd + hrow0 * WPR, dbytes);
+  const auto rv1 = stream_rsrc(a.v1d + hrow0 * WPR, dbytes);
+  const auto rv2 = stream_rsrc(a.v2d + hrow0 * WPR, dbytes);
+  const unsigned sbytes = (unsigned)(((max_lim + 3) & ~3) * NG * 2);
   const __amdgpu_buffer_rsrc_t rs[8] = {
       stream_rsrc((const uint16_t*)a.ks + hrow0 * NG, sbytes),
       stream_rsrc((const uint16_t*)a.kb + hrow0 * NG, sbytes),
@@ -279,15 +283,13 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       stream_rsrc((const uint16_t*)a.v2b + hrow0 * NG, sbytes),
       stream_rsrc(DUAL ? (const uint16_t*)a.k2s + hrow0 * NG : nullptr, DUAL ? sbytes : 0u),
       stream_rsrc(DUAL ? (const uint16_t*)a.k2b + hrow0 * NG : nullptr, DUAL ? sbytes : 0u)};
-  const auto rk2 = stream_rsrc(DUAL ? a.k2d + hrow0 * WPR : nullptr,
-                               DUAL ? (unsigned)(nrows * WPR * 4) : 0u);
+  const auto rk2 = stream_rsrc(DUAL ? a.k2d + hrow0 * WPR : nullptr, DUAL ? dbytes : 0u);
 
-  // All loads of U tiles starting at split-relative row t0 (rows past the
-  // split read 0).
-  auto load_tiles = [&](Tile (&T)[U], int t0) {
+  // All loads of this wave's tiles k0 .. k0 + U - 1 (rows past max_lim read 0).
+  auto load_tiles = [&](Tile (&T)[U], int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const unsigned r0 = (unsigned)(t0 + u * NW * 16);
+      const unsigned r0 = (unsigned)tile_row(k0 + u);
       const unsigned koff = ((r0 + col) * WPR + KW * blk) * 4u;
 #pragma unroll
       for (int i = 0; i < KW; i += 4) {
@@ -323,7 +325,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // The first tile set's loads are issued before q is consumed, so their
   // latency and q's overlap.
   Tile ta[U], tb[U];
-  int t0 = wave * 16;
+  int k0 = 0;
   uint4 qraw[NB][4];
 #pragma unroll
   for (int bb = 0; bb < NB; ++bb) {
@@ -337,7 +339,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qraw[bb][s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
-  load_tiles(ta, t0);
+  load_tiles(ta, k0);
 
   // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
   // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
@@ -379,21 +381,22 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
   const uint32_t magic = magic_vgpr();
 
-  // Scores, online softmax and both V products of U loaded tiles at
-  // split-relative row t0.
-  auto compute_tiles = [&](const Tile (&T)[U], int t0) {
+  // Scores, online softmax and both V products of this wave's loaded tiles
+  // k0 .. k0 + U - 1.
+  auto compute_tiles = [&](const Tile (&T)[U], int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int row0 = r_begin + t0 + u * NW * 16 + 4 * blk;  // absolute row of r = 0
-      const unsigned rrow0 = (unsigned)(t0 + u * NW * 16 + 4 * blk);  // split-relative
+      const int tr = tile_row(k0 + u);
+      const int row0 = tr + 4 * blk;  // row of r = 0
       uint32_t sw[NS][2];
 #pragma unroll
       for (int t = 0; t < NS; ++t) scale_words<NG>(sw[t], T[u].s[t], sel);
-      // Only the split's last tile can hold rows past its end; the test is
-      // uniform over the wave, so the others branch around the masking.
-      if (t0 + u * NW * 16 + 16 > nrows) {
+      // Only a tile reaching past max_lim holds rows whose scale words may be
+      // stale cache contents; the test is uniform over the wave, so the
+      // others branch around the masking.
+      if (tr + 16 > max_lim) {
 #pragma unroll
-        for (int t = 0; t < NS; ++t) drop_rows_past(sw[t], rrow0, (unsigned)nrows);
+        for (int t = 0; t < NS; ++t) drop_rows_past(sw[t], (unsigned)row0, (unsigned)max_lim);
       }
       floatx4 sacc[NB];
 #pragma unroll
@@ -448,7 +451,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           float t = fmaf(skr[r], sacc[bb][r], bkr[r] * qsum[bb]);
           t = sum_group_columns<GC>(t);
           const int row = row0 + r;
-          const bool ok = row < r_end && row < lim[bb];
+          const bool ok = row < lim[bb];  // lim <= max_lim
           sc[r] = ok ? t * a.qscale : kNegSentinel;
           mx = fmaxf(mx, sc[r]);
         }
@@ -510,15 +513,14 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   // Two register sets in turn: the loads of the next U tiles are in flight
   // while the current ones are computed.  (A third set, with two sets'
   // loads in flight, measured slower for q4.)
-  constexpr int kStep = NW * 16 * U;
-  while (t0 < nrows) {
-    load_tiles(tb, t0 + kStep);
-    compute_tiles(ta, t0);
-    t0 += kStep;
-    if (t0 >= nrows) break;
-    load_tiles(ta, t0 + kStep);
-    compute_tiles(tb, t0);
-    t0 += kStep;
+  while (tile_row(k0) < max_lim) {
+    load_tiles(tb, k0 + U);
+    compute_tiles(ta, k0);
+    k0 += U;
+    if (tile_row(k0) >= max_lim) break;
+    load_tiles(ta, k0 + U);
+    compute_tiles(tb, k0);
+    k0 += U;
   }
 
   // acc[i][r] of lane (col, blk) is channel 8*(4*blk + r) + i for head h; it

@@ -34,6 +34,10 @@ struct SdpaArgs {
   int GV;      // virtual heads per KV head = G * S_q (one per (head, query row))
   int nchunk;  // ceil(GV / GC): workgroups per KV head and split
   int kv_cap, kv_len, causal;
+  // Splits per (b, KV head, chunk).  The VALU and shared-tile kernels give
+  // split s the contiguous rows [s * rows_per_split, (s + 1) * rows_per_split);
+  // the matrix-core decode kernels deal blocks of (waves x 16) rows to the
+  // splits round robin and ignore rows_per_split.
   int nsplit, rows_per_split;
   int group_size;
   int fused_merge;  // 1: last-arriving workgroup merges; 0: sdpa_merge_kernel does
@@ -98,6 +102,12 @@ struct PrefillPlan {
   size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1
 };
 PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
+
+// The matrix-core decode kernels deal 16-row tiles of a whole KV head to
+// their splits and address them with 32-bit byte offsets from the head's
+// first row: they take kv_len <= kMfmaMaxRows (the VALU kernels take the
+// rest).
+constexpr int kMfmaMaxRows = 1 << 22;
 
 // Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
 // workgroups at one wave per SIMD, one per CU.
