@@ -124,7 +124,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
       a.part_o = (float*)(w + cbytes);
       a.part_ml = (float*)(w + cbytes + obytes);
     }
-    rc = launch_sdpa_prefill_f16(a, pp.waves, B * Hkv * pp.nqb * pp.nsplit, s);
+    rc = launch_sdpa_prefill_f16(a, pp.waves, sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit), s);
     return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
   }
   switch (dtype) {

@@ -26,14 +26,21 @@ namespace motif {
 constexpr int kPrefillTileRows = 32;
 constexpr int kPrefillRowHalves = 128 + 8;  // LDS row stride (halves): 16-byte pad
 
-// Workgroup -> (query block, (b, KV head) unit, split).
-__device__ inline void prefill_block_coords(const SdpaArgs& a, int bid, int& qblk, int& unit,
+// Workgroup -> (query block, (b, KV head) unit, split), as sdpa_block_coords
+// places head chunks: workgroups are dealt to the 8 XCDs round robin, and
+// the query blocks of one (b, KV head, split) share an XCD, so its K/V
+// tiles are fetched into that XCD's L2 once and read there by every query
+// block.  Groups of 8 (unit, split) pairs are padded; padding blocks exit.
+__device__ inline bool prefill_block_coords(const SdpaArgs& a, int bid, int& qblk, int& unit,
                                             int& split) {
   const int bh = a.B * a.Hkv;
-  qblk = bid % a.nchunk;
-  const int rest = bid / a.nchunk;
-  unit = rest % bh;
-  split = rest / bh;
+  const int slot = bid >> 3;
+  qblk = slot % a.nchunk;
+  const int g = (slot / a.nchunk) * 8 + (bid & 7);  // g = split * bh + unit
+  if (g >= bh * a.nsplit) return false;
+  split = g / bh;
+  unit = g % bh;
+  return true;
 }
 
 template <int NW>
@@ -52,7 +59,7 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
   const int blk = lane >> 4;
 
   int qblk, unit, split;
-  prefill_block_coords(a, blockIdx.x, qblk, unit, split);
+  if (!prefill_block_coords(a, blockIdx.x, qblk, unit, split)) return;  // grid padding
   const int b = unit / a.Hkv;
   const int kvh = unit % a.Hkv;
   const int wg_vh0 = qblk * NW * 16;
