@@ -226,3 +226,62 @@ def test_to_quantized(disabled, rng):
     assert qc.offset == 6 and qc.k1[0].shape == (1, 4, 6, 16)
     rd, _, _ = O.quantize(new[0].numpy(), 64, 8)
     np.testing.assert_array_equal(qc.k1[0].view(torch.int32).numpy().view(np.uint32), rd)
+
+
+def test_fp_cache_state_roundtrip_and_growth(rng):
+    """``state`` is the live [:offset] region and restores into a fresh
+    cache, which keeps growing past the restored offset (reference
+    tests/test_grouped_cache.py:269-299)."""
+    B, H, D = 1, 4, 128
+    cache = C.MotifGroupedKVCache()
+    for _ in range(3):
+        t = _t(rng, (B, H, 1, D))
+        cache.update_and_fetch_4(t, t, t, t)
+    saved = cache.state
+    assert all(a.shape[2] == 3 for a in saved)
+    restored = C.MotifGroupedKVCache()
+    restored.meta_state = cache.meta_state
+    restored.state = saved
+    assert restored.offset == 3
+    for a, b in zip(saved, restored.state):
+        np.testing.assert_array_equal(a.numpy(), b.numpy())
+    tb = _t(rng, (B, H, 1, D))
+    out = restored.update_and_fetch_4(tb, tb, tb, tb)
+    assert restored.offset == 4 and all(x.shape[2] >= 4 for x in out)
+    assert all(s.shape == (B, H, 4, D) for s in restored.state)
+    np.testing.assert_array_equal(restored.state[0][:, :, :3].numpy(), saved[0].numpy())
+    np.testing.assert_array_equal(restored.state[0][:, :, 3:].numpy(), tb.numpy())
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_cache_state_roundtrip_and_growth(disabled, rng, bits):
+    """Quantised ``state``: every (data, scales, biases) part trimmed to the
+    offset, exact round trip through ``meta_state``/``state``, growth after a
+    restore that is not step-aligned (reference
+    tests/test_grouped_cache.py:302-336)."""
+    B, H, D = 1, 4, 128
+    cache = C.MotifGroupedQuantizedKVCache(group_size=64, bits=bits)
+    for _ in range(3):
+        t = _t(rng, (B, H, 1, D))
+        cache.update_and_fetch_4(t, t, t, t)
+    saved = cache.state
+    assert all(part.shape[2] == 3 for slot in saved for part in slot)
+    restored = C.MotifGroupedQuantizedKVCache()
+    restored.meta_state = cache.meta_state
+    restored.state = saved
+    assert restored.offset == 3 and (restored.group_size, restored.bits) == (64, bits)
+    for a, b in zip(saved, restored.state):
+        for x, y in zip(a, b):
+            assert x.shape == y.shape
+            np.testing.assert_array_equal(x.numpy(), y.numpy())
+    tb = _t(rng, (B, H, 1, D))
+    out = restored.update_and_fetch_4(tb, tb, tb, tb)
+    assert all(x.shape == (B, H, 4, D) for x in out) and restored.offset == 4
+    # The restored rows are unchanged by the growth and the new row is the
+    # quantisation of the new token.
+    grown = restored.state
+    for a, b in zip(saved, grown):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x.numpy(), y[:, :, :3].numpy())
+    rd, _, _ = O.quantize(tb.numpy(), 64, bits)
+    np.testing.assert_array_equal(grown[0][0][:, :, 3:].view(torch.int32).numpy().view(np.uint32), rd)
