@@ -42,6 +42,7 @@ for _p in (ROOT, ROOT / "mlx-motif_amd"):
         sys.path.insert(0, str(_p))
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 matrix-core peak
 METRIC = "decode-attn µs/call + achieved HBM GB/s (% peak) at KV=16k, fp16 & q4 cache"
 
 B, HQ, HKV, D = 1, 32, 8, 128
@@ -431,6 +432,18 @@ def run_extra(torch, lib, dev, args):
     calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
     report("verify slab q8 5 rows kv32768", time_calls(torch, calls, steps, warm),
            alg_bytes("q8", 32768, s_q=5))
+    del calls, keep
+    torch.cuda.empty_cache()
+    # prefill chunk: 512 query rows of 32 heads over a 3716-row fp16 cache
+    # (bottom-right causal), the multi-row kernel with LDS-shared K/V tiles;
+    # matrix-core bound, so reported as TFLOP/s of QK^T and both PV products
+    calls, keep = make_fp16_calls(torch, lib, dev, 4, kv_len=3716, cap=3840, s_q=512)
+    us = time_calls(torch, calls, steps, warm)
+    flops = 2 * HQ * 512 * 3716 * D * 3
+    log("EXTRA " + json.dumps({"workload": "prefill chunk f16 512 rows kv3716 (causal)",
+                               "us_per_call": round(us, 3),
+                               "tflops": round(flops / us / 1e6, 1),
+                               "pct_peak_f16_mfma": round(100 * flops / us / 1e6 / PEAK_F16_TFLOPS, 1)}))
     del calls, keep
     torch.cuda.empty_cache()
     # gda_post_split prefill [1,16,3204,128]

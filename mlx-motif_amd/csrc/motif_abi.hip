@@ -118,9 +118,13 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   const int GV = G * S_q;
   const int cus = device_cu_count();
   const int bh = B * Hkv;
-  // 8 waves (128 virtual heads per block) when that still gives a block per
-  // CU, else 4.
-  p.waves = (long)bh * ((GV + 127) / 128) >= cus ? 8 : 4;
+  // 8 waves (128 virtual heads per block, two waves per SIMD) from 512
+  // virtual heads per KV head on, even if the row splits that fill the GPU
+  // then need the merge launch; 4 below (measured, 32 q-heads over 8 KV
+  // heads: 512 rows over 3716 157 -> 127 us, 256 rows 93 -> 76 us; at 64
+  // rows 4 waves are faster, 41 vs 47 us).
+  p.waves = GV >= 512 ? 8 : 4;
+  if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
   p.nqb = (GV + p.waves * 16 - 1) / (p.waves * 16);
   const long units = (long)bh * p.nqb;
   const int rows = kv_len > 0 ? kv_len : 1;

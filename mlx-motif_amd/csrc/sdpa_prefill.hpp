@@ -7,9 +7,13 @@
 // workgroup holds NW waves x 16 virtual heads (consecutive query rows of one
 // head), and every 32-row K/V tile is loaded from HBM once per workgroup into
 // LDS and read by all of its waves:
-//   - staging: each thread loads its 16-byte pieces of the next tile into
-//     registers while the current tile is computed, then writes them to the
-//     other LDS buffer (double buffering, one barrier per tile);
+//   - staging: tiles are copied from HBM straight into a ring of NS LDS
+//     stages (buffer loads with the LDS-direct bit, no registers), NS - 1
+//     tiles ahead of the one being computed; the waves share each tile's 24
+//     1-KB copies, wait for their own copies, then meet at one barrier per
+//     tile.  Within a 256-byte row, 16-byte chunk c sits at position
+//     c ^ (row % 16), so the K reads (16 rows, one chunk) and the V reads
+//     (one row, 16 chunks) are free of bank conflicts;
 //   - per wave: S^T = K Q^T (16x16x32 MFMA, two 16-row halves), online
 //     softmax in log2 units with lazy rescaling, O^T = V^T P^T over the 32
 //     rows as 16x16x32 MFMAs, exactly as the decode kernel does in registers;
@@ -24,7 +28,40 @@
 namespace motif {
 
 constexpr int kPrefillTileRows = 32;
-constexpr int kPrefillRowHalves = 128 + 8;  // LDS row stride (halves): 16-byte pad
+constexpr int kPrefillStages = 4;  // LDS ring: 4 x 24 KB
+
+// 16 bytes per lane from byte offset voff of the range-checked resource r
+// (past its end: zeros) into LDS at lds_base + 16 * lane.  Issued as asm so
+// that the compiler neither waits on these copies at barriers nor before LDS
+// reads; the kernel waits with wait_vm<>() / wait_vm_groups<>().
+__device__ inline void lds_copy16_rsrc(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(r)
+               : "memory");
+}
+__device__ inline unsigned lds_byte_addr(const void* p) {
+  return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+// Waits on this wave's outstanding vector memory operations (at most N
+// left); also a compiler barrier for memory accesses.
+template <int N>
+__device__ inline void prefill_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// prefill_wait_vm<n * L>() for a wave-uniform n in [0, NMAX].
+template <int L, int NMAX>
+__device__ inline void prefill_wait_vm_groups(int n) {
+  if constexpr (NMAX > 0) {
+    if (n >= NMAX) {
+      prefill_wait_vm<NMAX * L>();
+      return;
+    }
+    prefill_wait_vm_groups<L, NMAX - 1>(n);
+  } else {
+    prefill_wait_vm<0>();
+  }
+}
 
 // Workgroup -> (query block, (b, KV head) unit, split), as sdpa_block_coords
 // places head chunks: workgroups are dealt to the 8 XCDs round robin, and
@@ -43,18 +80,13 @@ __device__ inline bool prefill_block_coords(const SdpaArgs& a, int bid, int& qbl
   return true;
 }
 
-template <int NW>
+template <int NW, int NS = kPrefillStages>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
 sdpa_prefill_f16_kernel(SdpaArgs a) {
   constexpr int D = 128;
   constexpr int TR = kPrefillTileRows;
-  constexpr int RS = kPrefillRowHalves;
-  constexpr int NT = NW * 64;
-  constexpr int CHUNKS = TR * D * 2 / 16;  // 16-byte pieces per tensor tile
-  constexpr int CPT = CHUNKS / NT;           // pieces per thread per tensor
-  static_assert(CHUNKS % NT == 0, "whole pieces per thread");
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;
   const int blk = lane >> 4;
 
@@ -83,6 +115,10 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
       qb[s] = __builtin_bit_cast(half8_t, w);
     }
+    // q is waited for here, before the first tile copies are issued: the
+    // compiler's own wait would otherwise sit inside the tile loop and, as
+    // vmcnt(0), drain the copies in flight on every iteration.
+    asm volatile("" ::"v"(qb[0]), "v"(qb[1]), "v"(qb[2]), "v"(qb[3]));
   }
 
   // Rows [r_begin, r_end) of this KV head through range-checked resources.
@@ -93,27 +129,25 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
       stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, nbytes),
       stream_rsrc((const uint16_t*)a.v2 + hrow0 * D, nbytes)};
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds_kv[2][3][TR * RS];
-  // Staged pieces of the next tile (registers), written to the idle LDS
-  // buffer after the current tile is computed.  A second register set (two
-  // tiles in flight) spills at this register budget.
-  uint4 stage[3][CPT];
-  auto load_stage = [&](int t0) {  // t0: split-relative first row of the tile
+  // Ring stage st, tensor t (K, V1, V2): 32 rows x 256 bytes, chunk c of row
+  // r at byte r * 256 + (c ^ (r % 16)) * 16.
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NS][3][TR * D * 2];
+  constexpr int CPW = 3 * TR * D * 2 / 1024 / NW;  // 1 KB copies per wave per tile
+  static_assert(3 * TR * D * 2 / 1024 % NW == 0, "whole copies per wave");
+  static_assert((NS - 1) * CPW <= 63, "vmcnt counts at most 63");
+  // Copy j = wave + c * NW of a tile: tensor j / 8 (= c * NW / 8 for 4 or 8
+  // waves), rows 4 g .. 4 g + 3 with g = j % 8; lane L fills row 4 g + L / 16
+  // at chunk position L % 16 with chunk (L % 16) ^ row.
+  static_assert(NW == 4 || NW == 8, "copies are dealt over 4 or 8 waves");
+  auto issue = [&](int st, int tile) {
 #pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int piece = threadIdx.x + c * NT;
-      const unsigned off = (unsigned)((t0 + piece / 16) * D * 2 + (piece % 16) * 16);
-#pragma unroll
-      for (int t = 0; t < 3; ++t) stage[t][c] = bload4(rsrc[t], off);
-    }
-  };
-  auto store_stage = [&](int buf) {
-#pragma unroll
-    for (int c = 0; c < CPT; ++c) {
-      const int piece = threadIdx.x + c * NT;
-      const int o = (piece / 16) * RS + (piece % 16) * 8;
-#pragma unroll
-      for (int t = 0; t < 3; ++t) *reinterpret_cast<uint4*>(&lds_kv[buf][t][o]) = stage[t][c];
+    for (int c = 0; c < CPW; ++c) {
+      const int t = c * NW / 8;
+      const int g = (wave + c * NW) % 8;
+      const int r = 4 * g + lane / 16;
+      const int chunk = (lane % 16) ^ (r % 16);
+      const unsigned voff = (unsigned)((tile * TR + r) * D * 2 + chunk * 16);
+      lds_copy16_rsrc(rsrc[t], voff, lds_byte_addr(&ring[st][t][g * 1024]));
     }
   };
 
@@ -128,20 +162,21 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
   const half8_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
                         (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
 
-  // One 32-row tile from LDS buffer buf: rows t0 + 16*h + 4*blk + r hold
+  // One 32-row tile from ring stage st: rows t0 + 16*h + 4*blk + r hold
   // k index 8*blk + 4*h + r of the PV products (as in the decode kernel).
-  auto compute = [&](int buf, int t0) {
-    const uint16_t* Kt = lds_kv[buf][0];
-    const uint16_t* V1t = lds_kv[buf][1];
-    const uint16_t* V2t = lds_kv[buf][2];
+  auto compute = [&](int st, int t0) {
+    const uint8_t* Kt = ring[st][0];
+    const uint8_t* V1t = ring[st][1];
+    const uint8_t* V2t = ring[st][2];
     floatx4 sacc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       sacc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
+        const int kr = 16 * h + col;
         const half8_t ka = __builtin_bit_cast(
-            half8_t, *reinterpret_cast<const uint4*>(&Kt[(16 * h + col) * RS + 32 * s + 8 * blk]));
+            half8_t, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
         sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sacc[h], 0, 0, 0);
       }
     }
@@ -182,7 +217,8 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int o = (16 * h + 4 * blk + r) * RS + 8 * col;
+        const int vr = 16 * h + 4 * blk + r;
+        const int o = vr * 256 + ((col ^ (vr % 16)) * 16);
         const uint4 w1 = *reinterpret_cast<const uint4*>(&V1t[o]);
         const uint4 w2 = *reinterpret_cast<const uint4*>(&V2t[o]);
         v1w[h][r][0] = w1.x; v1w[h][r][1] = w1.y; v1w[h][r][2] = w1.z; v1w[h][r][3] = w1.w;
@@ -212,21 +248,30 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
   };
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
-  // all of its threads.  Tile i sits in LDS buffer i % 2; the store into
-  // buffer (i + 1) % 2 follows the barrier that ended tile i - 1's reads.
+  // all of its threads.  Tile i sits in stage i % NS.  At the barrier of
+  // tile i every wave has computed tile i - 1, so stage (i - 1) % NS is
+  // refilled (with tile i + NS - 1) right after it.
   const int nrows = max(r_end - r_begin, 0);
   const int ntiles = (nrows + TR - 1) / TR;
-  if (ntiles > 0) {
-    load_stage(0);
-    store_stage(0);
+  int inflight = 0;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) {
+    if (t < ntiles) {
+      issue(t, t);
+      ++inflight;
+    }
   }
-  __syncthreads();
+  int st = 0;
   for (int i = 0; i < ntiles; ++i) {
-    const int buf = i & 1;
-    if (i + 1 < ntiles) load_stage((i + 1) * TR);
-    compute(buf, i * TR);
-    if (i + 1 < ntiles) store_stage(buf ^ 1);
-    __syncthreads();
+    prefill_wait_vm_groups<CPW, NS - 2>(inflight - 1);  // this wave's copies of tile i landed
+    asm volatile("s_barrier" ::: "memory");             // every wave's copies landed
+    --inflight;
+    if (i + NS - 1 < ntiles) {
+      issue(st == 0 ? NS - 1 : st - 1, i + NS - 1);
+      ++inflight;
+    }
+    compute(st, i * TR);
+    st = st + 1 == NS ? 0 : st + 1;
   }
 
   // acc[j][r] of lane (col, blk) is channel 8*(4*blk + r) + j of column col.
