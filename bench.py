@@ -370,6 +370,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(f16["gbps"] / PEAK_HBM_GBPS, 4),
             "traffic": load_traffic("sdpa_dual_v_f16_kv16000"),
+            "basis": "algorithmic bytes / us per call; a call is the attention launch "
+                     "plus the split-merge launch (HIP events around graph-replayed calls)",
         },
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
