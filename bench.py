@@ -294,10 +294,10 @@ def main() -> int:
     ap.add_argument("--valu", action="store_true",
                     help="route attention through the VALU kernels (matrix cores off), "
                          "for comparison")
-    ap.add_argument("--traffic", nargs="?", const="f16", choices=("f16", "q4", "q8"),
+    ap.add_argument("--traffic", nargs="?", const="f16", choices=("f16", "q4", "q8", "prefill"),
                     help="counter pass: one 256 MiB copy, then 16 eager decode calls on the "
-                         "given cache (default f16; no timing, no JSON); run under rocprofv3 "
-                         "--pmc")
+                         "given cache (default f16), or 6 prefill-chunk calls (512 rows over "
+                         "3716, fp16); no timing, no JSON; run under rocprofv3 --pmc")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -389,6 +389,14 @@ def traffic_pass(torch, lib, dev, kind: str = "f16") -> int:
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
+    if kind == "prefill":
+        calls, keep = make_fp16_calls(torch, lib, dev, 2, kv_len=3716, cap=3840, s_q=512)
+        for i in range(6):
+            calls[i % len(calls)]()
+        torch.cuda.synchronize()
+        log("traffic pass: copy 268435456 B + 6 prefill calls (512 rows over 3716)")
+        del calls, keep
+        return 0
     if kind == "f16":
         calls, keep = make_fp16_calls(torch, lib, dev, 8)
     else:
