@@ -237,7 +237,8 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
 /* ------------------------------------------------------------------------ *
  * Tuning knobs of the split-KV kernels (process-wide; for benchmarks and
  * sweeps, not needed for correct use).  key: "rows_per_split",
- * "waves_per_wg", "min_wgs" (value 0 restores the default), "mfma" (1, the
+ * "waves_per_wg" (also the block size of the LDS-shared-tile multi-row
+ * kernel), "min_wgs" (value 0 restores the default), "mfma" (1, the
  * default: matrix-core kernels where compiled; 0: VALU kernels only),
  * "fused_merge" (0, the default: a second launch combines the splits; 1: the
  * last workgroup to finish combines them inside the attention launch).
