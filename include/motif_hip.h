@@ -241,7 +241,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * kernel), "min_wgs" (value 0 restores the default), "mfma" (1, the
  * default: matrix-core kernels where compiled; 0: VALU kernels only),
  * "fused_merge" (0, the default: a second launch combines the splits; 1: the
- * last workgroup to finish combines them inside the attention launch).
+ * last workgroup to finish combines them inside the attention launch),
+ * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
+ * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.
  * ------------------------------------------------------------------------ */
 int motif_set_tuning(const char* key, int value);

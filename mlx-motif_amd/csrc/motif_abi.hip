@@ -216,6 +216,8 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     tuning().fused_merge = value;
+  } else if (!strcmp(key, "poly_rows")) {
+    tuning().poly_rows = value;
   } else {
     set_error("motif_set_tuning: unknown key '%s'", key);
     return MOTIF_ERR_CONTRACT;

@@ -37,6 +37,7 @@ struct Tuning {
   int min_wgs = 0;         // 0 = automatic
   int mfma = 1;            // 1 = matrix-core kernels where compiled, 0 = VALU kernels
   int fused_merge = 0;     // 1 = last-arriving workgroup merges splits, 0 = merge kernel
+  int poly_rows = 0;       // persistent PolyNorm workgroups per CU (0 = by register use)
 };
 Tuning& tuning();
 

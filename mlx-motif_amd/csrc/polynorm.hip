@@ -8,11 +8,15 @@
 //   LPR = 16   : rows of <= 128 values, 16 rows per 256-thread workgroup
 //   LPR = 64   : rows of <= 2048 values, one wave per row
 //   LPR = 512  : rows of <= 16384 values, one 512-thread workgroup per row
+//                (fp32); 16-bit rows run persistent workgroups that load
+//                the next row while the current one is reduced and stored
 //   LPR = 1024 : rows of <= 32768 values, one 1024-thread workgroup per row
 // (the wide rows merge their wave sums in LDS; 4 loads in flight per lane
 // measured faster than 7 at 256 lanes for 13824-value rows)
 // Rows whose length is not a multiple of 8, or longer, take a strided
 // scalar path that reads x twice.
+#include <algorithm>
+
 #include "motif_common.hpp"
 
 namespace motif {
@@ -143,6 +147,92 @@ __global__ void __launch_bounds__(TPB) polynorm_vec_kernel(PolyArgs a) {
   }
 }
 
+// Wide 16-bit rows, persistent: workgroup b takes rows b, b + grid, ...
+// and loads row r + grid into a second register set while row r is reduced
+// and stored, so every workgroup keeps a row of loads in flight.  The
+// cross-wave sums alternate between two LDS slots, one barrier per row.
+template <typename T, int NCH, int TPB>
+__global__ void __launch_bounds__(TPB) polynorm_rows_kernel(PolyArgs a) {
+  static_assert(sizeof(T) == 2, "16-bit rows");
+  constexpr int NWV = TPB / 64;
+  const int tid = threadIdx.x;
+  const int nchunks = a.D / 8;
+  __shared__ float red[2][3][NWV];
+  uint4 raw0[NCH], raw1[NCH];
+  auto load_row = [&](uint4 (&dst)[NCH], long row) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + TPB * j;
+      dst[j] = row < a.rows && c < nchunks
+                   ? ld_stream4((const uint16_t*)a.x + row * (long)a.D + (long)c * 8)
+                   : make_uint4(0, 0, 0, 0);
+    }
+  };
+  const float inv_d = 1.0f / (float)a.D;
+  const float w0 = Elem<T>::load(a.w, 0), w1 = Elem<T>::load(a.w, 1), w2 = Elem<T>::load(a.w, 2);
+  const float bb = Elem<T>::load(a.b, 0);
+  // Row `row` from cur (loaded), with row + grid loading into nxt.
+  auto process = [&](const uint4 (&cur)[NCH], uint4 (&nxt)[NCH], long row, int par) {
+    load_row(nxt, row + gridDim.x);  // zeros past the last row
+    float s2 = 0.f, s4 = 0.f, s6 = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const uint32_t w[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = Elem<T>::get(w, e);
+        const float x2 = v * v;
+        const float x4 = x2 * x2;
+        s2 += x2;
+        s4 += x4;
+        s6 += x4 * x2;
+      }
+    }
+    s2 = group_sum<64>(s2);
+    s4 = group_sum<64>(s4);
+    s6 = group_sum<64>(s6);
+    if ((tid & 63) == 0) {
+      red[par][0][tid >> 6] = s2;
+      red[par][1][tid >> 6] = s4;
+      red[par][2][tid >> 6] = s6;
+    }
+    __syncthreads();
+    s2 = s4 = s6 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) {
+      s2 += red[par][0][i];
+      s4 += red[par][1][i];
+      s6 += red[par][2][i];
+    }
+    const float rs2 = rsqrtf(s2 * inv_d + a.eps);
+    const float rs4 = rsqrtf(s4 * inv_d + a.eps);
+    const float rs6 = rsqrtf(s6 * inv_d + a.eps);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + TPB * j;
+      if (c < nchunks) {
+        const uint32_t w[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+        float out[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          out[e] = poly_out(Elem<T>::get(w, e), rs2, rs4, rs6, w0, w1, w2, bb);
+        store8v<T>(a.y, row * (long)a.D + (long)c * 8, out);
+      }
+    }
+  };
+  // The trip count depends only on blockIdx, so every barrier is reached by
+  // the whole workgroup.
+  long row = blockIdx.x;
+  load_row(raw0, row);
+  while (row < a.rows) {
+    process(raw0, raw1, row, 0);
+    row += gridDim.x;
+    if (row >= a.rows) break;
+    process(raw1, raw0, row, 1);
+    row += gridDim.x;
+  }
+}
+
 // Any D: one workgroup per row, two passes over x.
 template <typename T>
 __global__ void __launch_bounds__(256) polynorm_scalar_kernel(PolyArgs a) {
@@ -207,6 +297,24 @@ static int launch_poly(const PolyArgs& a, bool vec_ok, hipStream_t st) {
       return check_launch("polynorm");
     }
     if (nchunks <= 512 * 4) {
+      if constexpr (sizeof(T) == 2) {
+        // Persistent rows: as many workgroups per CU as the register use of
+        // NCH chunks per lane lets reside (measured at [3204, 13824]:
+        // 44.0 us one row per workgroup, 33.9 us persistent at 2 per CU).
+        const int nch = (nchunks + 511) / 512;
+        const int per_cu = tuning().poly_rows > 0 ? tuning().poly_rows
+                                                  : (nch == 1 ? 4 : nch == 2 ? 3 : 2);
+        {
+          const long grid = std::min<long>(a.rows, (long)device_cu_count() * per_cu);
+          switch (nch) {
+            case 1: hipLaunchKernelGGL((polynorm_rows_kernel<T, 1, 512>), (unsigned)grid, 512, 0, st, a); break;
+            case 2: hipLaunchKernelGGL((polynorm_rows_kernel<T, 2, 512>), (unsigned)grid, 512, 0, st, a); break;
+            case 3: hipLaunchKernelGGL((polynorm_rows_kernel<T, 3, 512>), (unsigned)grid, 512, 0, st, a); break;
+            default: hipLaunchKernelGGL((polynorm_rows_kernel<T, 4, 512>), (unsigned)grid, 512, 0, st, a); break;
+          }
+          return check_launch("polynorm");
+        }
+      }
       launch_poly_lpr<T, 512, 512>(a, (nchunks + 511) / 512, st);
       return check_launch("polynorm");
     }

@@ -109,7 +109,8 @@ def test_gda_prefill_workloads(gpu, rng, shape, gr):
 
 
 @pytest.mark.parametrize("shape", [(2, 4, 16), (1, 1, 64), (3, 7, 256), (1, 1, 4096),
-                                   (5, 13824), (2, 3, 20), (4, 100000)])
+                                   (5, 13824), (2, 3, 20), (4, 100000), (700, 4096),
+                                   (300, 8200), (513, 2056)])
 @pytest.mark.parametrize("tag", ["f32", "f16", "bf16"])
 def test_polynorm(gpu, rng, shape, tag):
     from mlx_motif.kernels import polynorm
