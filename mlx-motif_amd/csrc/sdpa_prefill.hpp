@@ -80,8 +80,10 @@ __device__ inline bool prefill_block_coords(const SdpaArgs& a, int bid, int& qbl
   return true;
 }
 
+// The ring's LDS holds one workgroup per CU: two waves per SIMD at 8 waves,
+// one at 4.
 template <int NW, int NS = kPrefillStages>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 sdpa_prefill_f16_kernel(SdpaArgs a) {
   constexpr int D = 128;
   constexpr int TR = kPrefillTileRows;
