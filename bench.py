@@ -29,6 +29,7 @@ other workloads of the path on stderr.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -124,11 +125,15 @@ def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=H
 
 
 def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True, gr=4,
-                      bits=None):
+                      bits=None, append=None):
     """One GDA decode-attention step per call over distinct layer caches
     (k1, k2, v1, v2 of HKV heads): motif_gda_decode / motif_gda_decode_q
     (fused) or the reference's three calls (two motif_sdpa_dual_v(_q) +
-    motif_gda_post_split).  ``bits`` 4/8: packed cache, group size 64."""
+    motif_gda_post_split).  ``bits`` 4/8: packed cache, group size 64.
+    ``append``: also write the token's four rows at row kv_len - 1, inside
+    the step ("fused": motif_gda_decode(_q)_append) or before it ("write":
+    the cache write -- four row copies, or motif_quant_write4 -- then the
+    fused step)."""
     from mlx_motif import _native
     from mlx_motif.kernels import quantize
 
@@ -143,6 +148,8 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     if bits:
         sets = [tuple(quantize(t, GS, bits) for t in st) for st in sets]
         torch.cuda.synchronize()
+    rows = [torch.randn((B, HKV, 1, D), generator=g, device=dev).half() for _ in range(4)]
+    rp = [r.data_ptr() for r in rows]
     y = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
     o = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
     n = torch.empty((B, HKV, 1, 2 * D), dtype=torch.float16, device=dev)
@@ -154,13 +161,25 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     def mk_q(k1, k2, v1, v2):
         p = lambda t: [x.data_ptr() for x in t]  # noqa: E731
 
+        slots = (k1, k2, v1, v2)
+        data = (ctypes.c_void_p * 4)(*(t[0].data_ptr() for t in slots))
+        scl = (ctypes.c_void_p * 4)(*(t[1].data_ptr() for t in slots))
+        bia = (ctypes.c_void_p * 4)(*(t[2].data_ptr() for t in slots))
+
         def call():
             st = torch.cuda.current_stream().cuda_stream
+            tail = (w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B, HKV, gr, D, cap,
+                    kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st)
+            if append == "fused":
+                _native.check(lib.motif_gda_decode_q_append(
+                    q1.data_ptr(), q2.data_ptr(), *rp, *p(k1), *p(k2), *p(v1), *p(v2), *tail))
+                return
+            if append == "write":
+                _native.check(lib.motif_quant_write4(*rp, data, scl, bia, 0, B, HKV, 1, D, cap,
+                                                     kv_len - 1, bits, GS, st))
             if fused:
                 _native.check(lib.motif_gda_decode_q(
-                    q1.data_ptr(), q2.data_ptr(), *p(k1), *p(k2), *p(v1), *p(v2), w.data_ptr(),
-                    lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B, HKV, gr, D, cap, kv_len, bits,
-                    GS, scale, ws.data_ptr(), ws.numel(), st))
+                    q1.data_ptr(), q2.data_ptr(), *p(k1), *p(k2), *p(v1), *p(v2), *tail))
                 return
             _native.check(lib.motif_sdpa_dual_v_q(
                 q1.data_ptr(), *p(k1), *p(v1), *p(v2), o.data_ptr(), 0, B, HKV * gr, HKV, D, cap,
@@ -176,6 +195,16 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     def mk(k1, k2, v1, v2):
         def call():
             st = torch.cuda.current_stream().cuda_stream
+            if append == "fused":
+                _native.check(lib.motif_gda_decode_append(
+                    q1.data_ptr(), q2.data_ptr(), *rp, k1.data_ptr(), k2.data_ptr(),
+                    v1.data_ptr(), v2.data_ptr(), w.data_ptr(), lam.data_ptr(), 0.8, 1e-5,
+                    y.data_ptr(), 0, B, HKV, gr, D, cap, kv_len, scale, ws.data_ptr(),
+                    ws.numel(), st))
+                return
+            if append == "write":  # the fp cache's write: a slice copy per slot
+                for c, r in zip((k1, k2, v1, v2), rows):
+                    c[:, :, kv_len - 1:kv_len].copy_(r)
             if fused:
                 _native.check(lib.motif_gda_decode(
                     q1.data_ptr(), q2.data_ptr(), k1.data_ptr(), k2.data_ptr(), v1.data_ptr(),
@@ -436,6 +465,19 @@ def run_extra(torch, lib, dev, args):
             cache = "f16" if not bits else f"q{bits}"
             report(f"gda decode step {cache} kv16000 ({'fused' if fused else 'three calls'})",
                    time_calls(torch, calls, steps, warm), decode_bytes(KV_LEN, fused, bits=bits))
+            del calls, keep
+            torch.cuda.empty_cache()
+    # the same step with the token's cache write: inside the attention launch
+    # vs the cache write (4 slice copies / motif_quant_write4) before the step
+    for bits, nsets in ((None, 6), (4, 18), (8, 12)):
+        cache = "f16" if not bits else f"q{bits}"
+        row = D * 2 if not bits else D * bits // 8 + 2 * (D // GS) * 2
+        nbytes = decode_bytes(KV_LEN, True, bits=bits) + 4 * B * HKV * (row + D * 2)
+        for mode in ("fused", "write"):
+            calls, keep = make_decode_calls(torch, lib, dev, nsets, bits=bits, append=mode)
+            label = "write in the step" if mode == "fused" else "write, then step"
+            report(f"gda decode step + token write {cache} kv16000 ({label})",
+                   time_calls(torch, calls, steps, warm), nbytes)
             del calls, keep
             torch.cuda.empty_cache()
     # verify slab: 5 rows over a q8 cache of 32768 rows

@@ -224,6 +224,38 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                        int bits, int group_size, float scale, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Decode step with append: one call per layer for a decode token (no single
+ * counterpart in the reference, whose step is the cache write
+ * MotifGroupedKVCache.update_and_fetch_4 / the quantized cache's
+ * update_and_fetch_4_quantized, src/mlx_motif/cache.py:337, 467, followed by
+ * the calls above).  Writes the new token's rows k1_new, k2_new,
+ * v1_new, v2_new (each (B, Hkv, 1, D) dtype) at row kv_len - 1 of the four
+ * slots -- quantised as motif_quant_write4 does for the packed cache -- and
+ * then runs the step over kv_len rows.  kv_len counts the new row (>= 1).
+ * When the step is fused, the write happens inside the attention launch:
+ * the one wave whose tiles include row kv_len - 1 of a KV head stores that
+ * head's rows before it loads them.  Otherwise the row is written first
+ * (a row copy, or motif_quant_write4) and the separate calls follow. */
+int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
+                            const void* k2_new, const void* v1_new, const void* v2_new,
+                            void* k1, void* k2, void* v1, void* v2, const void* subln_w,
+                            const float* lambda_full, float one_minus_lambda_init, float eps,
+                            void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                            int kv_len, float scale, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
+                              const void* k2_new, const void* v1_new, const void* v2_new,
+                              uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                              uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                              uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                              uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                              const void* subln_w, const float* lambda_full,
+                              float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                              int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                              int group_size, float scale, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * Fused PolyNorm (polynorm, src/mlx_motif/kernels/mlp.py:119-157):
  *   y = w0*x^3*rsqrt(mean(x^6)+eps) + w1*x^2*rsqrt(mean(x^4)+eps)

@@ -305,13 +305,18 @@ size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int 
   return L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
 }
 
-int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void* k2,
-                     const void* v1, const void* v2, const void* subln_w,
-                     const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
-                     int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
-                     float scale, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The fused decode step; new_kv (k1, k2, v1, v2 rows of the new token, each
+// (B, Hkv, 1, D)) or null: with it, row kv_len - 1 of the cache is written
+// first (inside the attention launch when fused).
+static int gda_decode_fp(const char* name, const void* q1, const void* q2, const void* k1,
+                         const void* k2, const void* v1, const void* v2, const void* subln_w,
+                         const float* lambda_full, float one_minus_lambda_init, float eps,
+                         void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                         int kv_len, float scale, void* workspace, size_t workspace_bytes,
+                         const void* const* new_kv, void* stream) {
   clear_error();
-  const char* name = "gda_decode";
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
   int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
@@ -319,11 +324,17 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
   MOTIF_REQUIRE(q1 && q2 && y && subln_w && lambda_full &&
                     (kv_cap == 0 || (k1 && k2 && v1 && v2)),
                 "%s: null pointer", name);
+  if (new_kv) {
+    MOTIF_REQUIRE(new_kv[0] && new_kv[1] && new_kv[2] && new_kv[3], "%s: null new row", name);
+    MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the appended row", name, kv_len);
+  }
   hipStream_t s = (hipStream_t)stream;
   const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
                      aligned(k1, 16) && aligned(k2, 16) &&
-                     aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8);
+                     aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8) &&
+                     (!new_kv || ((uintptr_t)new_kv[0] | (uintptr_t)new_kv[1] |
+                                  (uintptr_t)new_kv[2] | (uintptr_t)new_kv[3]) % 16 == 0);
   if (fused) {
     SdpaArgs a = gda_decode_args(L, L.plan, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
                                  subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
@@ -331,7 +342,24 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
     a.k2 = k2;
     a.v1 = v1;
     a.v2 = v2;
+    if (new_kv) {
+      a.new_k1 = new_kv[0]; a.new_k2 = new_kv[1]; a.new_v1 = new_kv[2]; a.new_v2 = new_kv[3];
+      a.append = 1;
+    }
     return launch_gda_decode_f16(a, gda_columns(gr), sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+  }
+  if (new_kv) {  // row kv_len - 1 of each slot: B * Hkv rows of D values
+    const size_t row = (size_t)D * (dtype == MOTIF_F32 ? 4 : 2);
+    const void* dst[4] = {k1, k2, v1, v2};
+    for (int t = 0; t < 4; ++t) {
+      const hipError_t e = hipMemcpy2DAsync(
+          (char*)const_cast<void*>(dst[t]) + (size_t)(kv_len - 1) * row, (size_t)kv_cap * row,
+          new_kv[t], row, row, (size_t)B * Hkv, hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) {
+        set_error("%s: row copy failed: %s", name, hipGetErrorString(e));
+        return MOTIF_ERR_HIP;
+      }
+    }
   }
   // Composition of the separate calls, every step on the device.
   char* w = (char*)workspace;
@@ -345,6 +373,31 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
   if (rc != MOTIF_OK) return rc;
   return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
                               lambda_full, one_minus_lambda_init, eps, stream);
+}
+
+extern "C" {
+
+int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void* k2,
+                     const void* v1, const void* v2, const void* subln_w,
+                     const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                     int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                     float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  return gda_decode_fp("gda_decode", q1, q2, k1, k2, v1, v2, subln_w, lambda_full,
+                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D, kv_cap, kv_len,
+                       scale, workspace, workspace_bytes, nullptr, stream);
+}
+
+int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
+                            const void* k2_new, const void* v1_new, const void* v2_new,
+                            void* k1, void* k2, void* v1, void* v2, const void* subln_w,
+                            const float* lambda_full, float one_minus_lambda_init, float eps,
+                            void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                            int kv_len, float scale, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  const void* const nk[4] = {k1_new, k2_new, v1_new, v2_new};
+  return gda_decode_fp("gda_decode_append", q1, q2, k1, k2, v1, v2, subln_w, lambda_full,
+                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D, kv_cap, kv_len,
+                       scale, workspace, workspace_bytes, nk, stream);
 }
 
 int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
@@ -387,17 +440,21 @@ int motif_sdpa_dual_v_q_rows(const void* q, const uint32_t* k_data, const void* 
                     stream);
 }
 
-int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
-                       const void* k1_scales, const void* k1_biases, const uint32_t* k2_data,
-                       const void* k2_scales, const void* k2_biases, const uint32_t* v1_data,
-                       const void* v1_scales, const void* v1_biases, const uint32_t* v2_data,
-                       const void* v2_scales, const void* v2_biases, const void* subln_w,
-                       const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
-                       int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
-                       int bits, int group_size, float scale, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// Same over the packed cache; new_kv rows are quantised into row kv_len - 1
+// (inside the attention launch when fused, else by motif_quant_write4).
+static int gda_decode_q(const char* name, const void* q1, const void* q2,
+                        const uint32_t* k1_data, const void* k1_scales, const void* k1_biases,
+                        const uint32_t* k2_data, const void* k2_scales, const void* k2_biases,
+                        const uint32_t* v1_data, const void* v1_scales, const void* v1_biases,
+                        const uint32_t* v2_data, const void* v2_scales, const void* v2_biases,
+                        const void* subln_w, const float* lambda_full,
+                        float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                        int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                        int group_size, float scale, void* workspace, size_t workspace_bytes,
+                        const void* const* new_kv, void* stream) {
   clear_error();
-  const char* name = "gda_decode_q";
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
   int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
@@ -412,6 +469,10 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                                      k2_scales && k2_biases && v1_data && v1_scales &&
                                      v1_biases && v2_data && v2_scales && v2_biases)),
                 "%s: null pointer", name);
+  if (new_kv) {
+    MOTIF_REQUIRE(new_kv[0] && new_kv[1] && new_kv[2] && new_kv[3], "%s: null new row", name);
+    MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the appended row", name, kv_len);
+  }
   hipStream_t s = (hipStream_t)stream;
   const int gc = gda_columns(gr);
   const int ng = D / group_size;
@@ -425,7 +486,9 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                      gc * ng <= 16 && (data_bits & 15u) == 0 &&
                      (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
-                     aligned(y, 8);
+                     aligned(y, 8) &&
+                     (!new_kv || ((uintptr_t)new_kv[0] | (uintptr_t)new_kv[1] |
+                                  (uintptr_t)new_kv[2] | (uintptr_t)new_kv[3]) % 16 == 0);
   if (fused) {
     SdpaArgs a = gda_decode_args(L, L.plan_q, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
                                  subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
@@ -434,7 +497,22 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
     a.v1d = v1_data; a.v1s = v1_scales; a.v1b = v1_biases;
     a.v2d = v2_data; a.v2s = v2_scales; a.v2b = v2_biases;
     a.group_size = group_size;
+    if (new_kv) {
+      a.new_k1 = new_kv[0]; a.new_k2 = new_kv[1]; a.new_v1 = new_kv[2]; a.new_v2 = new_kv[3];
+      a.append = 1;
+    }
     return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+  }
+  if (new_kv) {
+    uint32_t* const data[4] = {const_cast<uint32_t*>(k1_data), const_cast<uint32_t*>(k2_data),
+                               const_cast<uint32_t*>(v1_data), const_cast<uint32_t*>(v2_data)};
+    void* const scl[4] = {const_cast<void*>(k1_scales), const_cast<void*>(k2_scales),
+                          const_cast<void*>(v1_scales), const_cast<void*>(v2_scales)};
+    void* const bia[4] = {const_cast<void*>(k1_biases), const_cast<void*>(k2_biases),
+                          const_cast<void*>(v1_biases), const_cast<void*>(v2_biases)};
+    rc = motif_quant_write4(new_kv[0], new_kv[1], new_kv[2], new_kv[3], data, scl, bia, dtype, B,
+                            Hkv, 1, D, kv_cap, kv_len - 1, bits, group_size, stream);
+    if (rc != MOTIF_OK) return rc;
   }
   char* w = (char*)workspace;
   void* yo = w + L.sdpa_bytes;
@@ -449,6 +527,43 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
   if (rc != MOTIF_OK) return rc;
   return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
                               lambda_full, one_minus_lambda_init, eps, stream);
+}
+
+extern "C" {
+
+int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
+                       const void* k1_scales, const void* k1_biases, const uint32_t* k2_data,
+                       const void* k2_scales, const void* k2_biases, const uint32_t* v1_data,
+                       const void* v1_scales, const void* v1_biases, const uint32_t* v2_data,
+                       const void* v2_scales, const void* v2_biases, const void* subln_w,
+                       const float* lambda_full, float one_minus_lambda_init, float eps, void* y,
+                       int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                       int bits, int group_size, float scale, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  return gda_decode_q("gda_decode_q", q1, q2, k1_data, k1_scales, k1_biases, k2_data, k2_scales,
+                      k2_biases, v1_data, v1_scales, v1_biases, v2_data, v2_scales, v2_biases,
+                      subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D,
+                      kv_cap, kv_len, bits, group_size, scale, workspace, workspace_bytes,
+                      nullptr, stream);
+}
+
+int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
+                              const void* k2_new, const void* v1_new, const void* v2_new,
+                              uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                              uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                              uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                              uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                              const void* subln_w, const float* lambda_full,
+                              float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                              int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                              int group_size, float scale, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const void* const nk[4] = {k1_new, k2_new, v1_new, v2_new};
+  return gda_decode_q("gda_decode_q_append", q1, q2, k1_data, k1_scales, k1_biases, k2_data,
+                      k2_scales, k2_biases, v1_data, v1_scales, v1_biases, v2_data, v2_scales,
+                      v2_biases, subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B,
+                      Hkv, gr, D, kv_cap, kv_len, bits, group_size, scale, workspace,
+                      workspace_bytes, nk, stream);
 }
 
 }  // extern "C"

@@ -51,6 +51,28 @@ __device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
   return L < 0 ? 0 : (L > a.kv_len ? a.kv_len : L);
 }
 
+// Append (fused decode step): the wave whose tiles include row kv_len - 1
+// of this KV head stores the new token's four slot rows there.  Tile T of a
+// KV head is tile k of wave T % NW in split (T / NW) % nsplit.
+template <int NW>
+__device__ inline bool append_owner(const SdpaArgs& a, int split, int wave) {
+  if (!a.append || a.kv_len < 1) return false;
+  const int t = (a.kv_len - 1) / 16;
+  return wave == t % NW && split == (t / NW) % a.nsplit;
+}
+
+// fp16 rows: lane L copies 16 bytes (chunk L % 16) of slot L / 16 (k1, k2,
+// v1, v2) into row kv_len - 1 of KV head bk.
+__device__ inline void append_rows_f16(const SdpaArgs& a, long bk, int lane) {
+  const int slot = lane / 16;
+  const int chunk = lane % 16;
+  const void* src = slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
+  const void* dst = slot == 0 ? a.k : slot == 1 ? a.k2 : slot == 2 ? a.v1 : a.v2;
+  const uint4 w = *reinterpret_cast<const uint4*>((const uint8_t*)src + bk * 256 + chunk * 16);
+  *reinterpret_cast<uint4*>((uint8_t*)const_cast<void*>(dst) +
+                            (bk * a.kv_cap + a.kv_len - 1) * 256 + chunk * 16) = w;
+}
+
 // DUAL: fused GDA decode step.  Columns 0..G-1 are the origin heads of the
 // KV head (scores from k), column G its noise head (scores from k2); both
 // share the V1/V2 rows, and the partials go to the fused merge launch.
@@ -84,6 +106,14 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
   const bool col_ok = col < nvh;
   const int lim = col_ok ? vhead_limit(a, vh0 + col) : 0;  // <= max_lim
+
+  // Append: issue the new rows' stores first; the owner waits for them
+  // before the loads of the tile that holds row kv_len - 1.
+  bool owner = false;
+  if constexpr (DUAL) {
+    owner = append_owner<NW>(a, split, wave);
+    if (owner) append_rows_f16(a, bk, lane);
+  }
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds head col,
   // channels 32*s + 8*blk .. +7 for k-step s.
@@ -134,6 +164,14 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   // U tiles per wave per iteration: all of their loads are issued before
   // any of them is consumed, so a wave keeps U x 12 KB in flight.
   for (int k0 = 0; tile_row(k0) < max_lim; k0 += U) {
+    if constexpr (DUAL) {
+      if (owner) {
+        bool has = false;
+#pragma unroll
+        for (int u = 0; u < U; ++u) has |= tile_row(k0 + u) == (a.kv_len - 1) / 16 * 16;
+        if (has) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new rows are stored
+      }
+    }
     half8_t ka[U][4];
     half8_t ka2[DUAL ? U : 1][4];
     uint32_t v1w[U][4][4], v2w[U][4][4];

@@ -26,6 +26,7 @@
 // fp16-cache kernel.
 #pragma once
 
+#include "quant_impl.hpp"
 #include "sdpa_mfma.hpp"
 
 namespace motif {
@@ -196,6 +197,34 @@ __device__ inline void drop_rows_past(uint32_t (&out)[2], unsigned row0, unsigne
   }
 }
 
+// Packed rows: lane L quantises chunk L % 16 (8 values) of slot L / 16 (k1,
+// k2, v1, v2) of the new token exactly as motif_quant_write4 does, and
+// stores the codes, scale and bias at row kv_len - 1 of KV head bk.
+template <int BITS, int GS>
+__device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
+  constexpr int D = 128;
+  constexpr int LPG = GS / 8;
+  constexpr int NG = D / GS;
+  constexpr int WPR = D * BITS / 32;
+  const int slot = lane / 16;
+  const int chunk = lane % 16;
+  const void* src = slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
+  const uint32_t* data = slot == 0 ? a.kd : slot == 1 ? a.k2d : slot == 2 ? a.v1d : a.v2d;
+  const void* sc = slot == 0 ? a.ks : slot == 1 ? a.k2s : slot == 2 ? a.v1s : a.v2s;
+  const void* bi = slot == 0 ? a.kb : slot == 1 ? a.k2b : slot == 2 ? a.v1b : a.v2b;
+  float v[8];
+  load8<half_t>(src, bk * D + (long)chunk * 8, v);
+  uint32_t w[2];
+  float scale, bias;
+  quantize8<BITS, LPG>(v, w, scale, bias);
+  const long crow = bk * a.kv_cap + a.kv_len - 1;
+  store_words<BITS>(const_cast<uint32_t*>(data), crow * WPR + (long)chunk * (8 * BITS / 32), w);
+  if (chunk % LPG == 0) {
+    Elem<half_t>::store(const_cast<void*>(sc), crow * NG + chunk / LPG, scale);
+    Elem<half_t>::store(const_cast<void*>(bi), crow * NG + chunk / LPG, bias);
+  }
+}
+
 // POL: cache policy of the K/V/scale loads.  Launches with several head
 // chunks (a.nchunk > 1: more virtual heads than one pass holds, e.g. a
 // verify slab) read each row in several workgroups and use cached loads, so
@@ -285,10 +314,23 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       stream_rsrc(DUAL ? (const uint16_t*)a.k2b + hrow0 * NG : nullptr, DUAL ? sbytes : 0u)};
   const auto rk2 = stream_rsrc(DUAL ? a.k2d + hrow0 * WPR : nullptr, DUAL ? dbytes : 0u);
 
+  // Append: the owner quantises and stores the new rows first, and waits for
+  // the stores before it loads the tile that holds row kv_len - 1.
+  bool owner = false;
+  if constexpr (DUAL) {
+    owner = append_owner<NW>(a, split, wave);
+    if (owner) append_rows_q<BITS, GS>(a, bk, lane);
+  }
+  const int append_tile = (a.kv_len - 1) / 16 * 16;  // first row of that tile
+
   // All loads of this wave's tiles k0 .. k0 + U - 1 (rows past max_lim read 0).
   auto load_tiles = [&](Tile (&T)[U], int k0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if constexpr (DUAL) {
+        if (owner && tile_row(k0 + u) == append_tile)
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new rows are stored
+      }
       const unsigned r0 = (unsigned)tile_row(k0 + u);
       const unsigned koff = ((r0 + col) * WPR + KW * blk) * 4u;
 #pragma unroll

@@ -56,6 +56,15 @@ struct SdpaArgs {
   const float* gda_lambda;   // device pointer to lambda_full (fp32)
   float gda_scale;           // 1 - lambda_init
   float gda_eps;
+  // Fused decode step with append (append != 0): the new token's rows of
+  // the four slots (B, Hkv, 1, D), written at row kv_len - 1 of the cache
+  // (quantised for the packed cache) by the one wave whose tiles include
+  // that row, before it loads the row.
+  const void* new_k1;
+  const void* new_k2;
+  const void* new_v1;
+  const void* new_v2;
+  int append;
 };
 
 struct SdpaPlan {

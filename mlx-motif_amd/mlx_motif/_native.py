@@ -78,6 +78,14 @@ _SIGNATURES = {
         _c_int,
         [_vp] * 16 + [_c_f, _c_f, _vp] + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],
     ),
+    "motif_gda_decode_append": (
+        _c_int,
+        [_vp] * 12 + [_c_f, _c_f, _vp] + [_c_int] * 7 + [_c_f, _vp, _c_sz, _vp],
+    ),
+    "motif_gda_decode_q_append": (
+        _c_int,
+        [_vp] * 20 + [_c_f, _c_f, _vp] + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],
+    ),
     "motif_polynorm": (_c_int, [_vp] * 4 + [_c_int, _c_i64, _c_int, _c_f, _vp]),
     "motif_set_tuning": (_c_int, [ctypes.c_char_p, _c_int]),
 }

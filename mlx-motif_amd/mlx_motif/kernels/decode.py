@@ -15,6 +15,14 @@ calls read v1 and v2 twice), and applies the epilogue in the split merge.
 Other shapes compose the separate native calls inside the library.
 ``gda_decode_attention_q4`` is the same step over the packed q4/q8 cache
 (QUANT_SDPA path, ``model.py:717-748``: two ``sdpa_dual_v_q4`` calls).
+
+With ``new_kv=(k1_new, k2_new, v1_new, v2_new)`` either function also
+writes the decode token's rows into the cache first -- the reference's
+``update_and_fetch_4`` / ``update_and_fetch_4_quantized``
+(``src/mlx_motif/cache.py:337, 467``) for one token -- at row ``kv_len - 1``
+(``kv_len`` then counts the new row).  The fused fp16 / packed kernels store
+the rows inside the attention launch, before the one wave that reads that
+row block loads it; other shapes write the row first and then run the step.
 """
 
 from __future__ import annotations
@@ -25,6 +33,7 @@ from .. import _native
 from . import _common
 from .attention import _q_contract, sdpa_dual_v_q4_reference, sdpa_dual_v_reference
 from .gda import gda_post_split_reference
+from .quant import quantize_reference
 
 
 def gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale: float, subln_weight,
@@ -43,16 +52,57 @@ def gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale: float, subln_w
     return y.to(q1.dtype)
 
 
+def _new_rows(new_kv, B, H_kv, D, dtype, kv_len):
+    """Checks the decode token's four (B, H_kv, 1, D) rows."""
+    if len(new_kv) != 4:
+        raise ValueError("new_kv must be (k1_new, k2_new, v1_new, v2_new)")
+    if kv_len < 1:
+        raise ValueError(f"kv_len={kv_len} must count the appended row (>= 1)")
+    for t in new_kv:
+        assert tuple(t.shape) == (B, H_kv, 1, D), "new_kv rows must be (B, H_kv, 1, D)"
+        if t.dtype != dtype:
+            raise TypeError(f"new_kv dtype {t.dtype} must match q1 dtype {dtype}")
+    return tuple(_common.contiguous(t) for t in new_kv)
+
+
+def _write_rows_reference(caches, new_kv, kv_len):
+    """Torch-op cache write of one token at row ``kv_len - 1``."""
+    for c, r in zip(caches, new_kv):
+        c[:, :, kv_len - 1:kv_len, :] = r
+
+
+def _write_rows_q_reference(slots, new_kv, kv_len, group_size, bits):
+    """Quantise the token's rows (``quantize_reference``) and store the
+    (data, scales, biases) triples at row ``kv_len - 1``."""
+    for t, r in zip(slots, new_kv):
+        for dst, src in zip(t, quantize_reference(r, group_size, bits)):
+            dst[:, :, kv_len - 1:kv_len, :] = src
+
+
+def _require_in_place(tensors):
+    for t in tensors:
+        if not t.is_contiguous():
+            raise ValueError("new_kv writes the cache in place: cache buffers must be "
+                             "contiguous")
+
+
 def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lambda_full,
                          lambda_init: float, gr: int, eps: float = 1e-5,
-                         kv_len: int | None = None):
+                         kv_len: int | None = None, new_kv=None):
     """``q1`` (B, H_kv*gr, 1, D) origin queries, ``q2`` (B, H_kv, 1, D) noise
     queries; ``k1, k2, v1, v2`` (B, H_kv, KV_cap, D) full-capacity 4-slot
-    cache buffers with ``kv_len`` live rows (default ``KV_cap``).  Returns
-    (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
+    cache buffers with ``kv_len`` live rows (default ``KV_cap``).  With
+    ``new_kv`` the token's rows are first written at row ``kv_len - 1``.
+    Returns (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
     if kv_len is None:
         kv_len = k1.shape[2]
+    if new_kv is not None:
+        new_kv = _new_rows(new_kv, q1.shape[0], k1.shape[1], q1.shape[3], q1.dtype, kv_len)
+        _require_in_place((k1, k2, v1, v2))
     if _common._DISABLE:
+        if new_kv is not None:
+            assert kv_len <= k1.shape[2], f"kv_len={kv_len} exceeds KV_cap={k1.shape[2]}"
+            _write_rows_reference((k1, k2, v1, v2), new_kv, kv_len)
         return gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale, subln_weight,
                                               lambda_full, lambda_init, gr, eps, kv_len)
     B, H_o, S_q, D = q1.shape
@@ -64,7 +114,7 @@ def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lam
     for t in (k2, v1, v2):
         assert t.shape == (B, H_kv, KV_cap, D), "k2,v1,v2 must match (B, H_kv, KV_cap, D)"
     assert 0 <= kv_len <= KV_cap, f"kv_len={kv_len} must be in [0, {KV_cap}]"
-    dev = _native.require_device(q1, q2, k1, k2, v1, v2)
+    dev = _native.require_device(q1, q2, k1, k2, v1, v2, *(new_kv or ()))
     for t in (q2, k1, k2, v1, v2):
         if t.dtype != q1.dtype:
             raise TypeError(f"dtype {t.dtype} must match q1 dtype {q1.dtype}")
@@ -75,14 +125,16 @@ def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lam
     lib = _native.lib()
     n = lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D)
     ws = _native.workspace(dev, n)
-    _native.check(
-        lib.motif_gda_decode(
-            q1.data_ptr(), q2.data_ptr(), k1.data_ptr(), k2.data_ptr(), v1.data_ptr(),
-            v2.data_ptr(), w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps),
-            y.data_ptr(), _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len,
-            float(scale), ws.data_ptr(), ws.numel(), _native.stream_of(dev),
-        )
-    )
+    tail = (w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps), y.data_ptr(),
+            _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len, float(scale),
+            ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    caches = (k1.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr())
+    if new_kv is None:
+        rc = lib.motif_gda_decode(q1.data_ptr(), q2.data_ptr(), *caches, *tail)
+    else:
+        rc = lib.motif_gda_decode_append(q1.data_ptr(), q2.data_ptr(),
+                                         *(t.data_ptr() for t in new_kv), *caches, *tail)
+    _native.check(rc)
     return y
 
 
@@ -103,19 +155,27 @@ def gda_decode_attention_q4_reference(q1, q2, k1_q, k2_q, v1_q, v2_q, scale: flo
 def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q: tuple,
                             scale: float, subln_weight, lambda_full, lambda_init: float, gr: int,
                             group_size: int = 64, bits: int = 4, eps: float = 1e-5,
-                            kv_len: int | None = None):
+                            kv_len: int | None = None, new_kv=None):
     """The decode step over the packed cache: each ``*_q`` is a ``(data
     uint32, scales, biases)`` triple of (B, H_kv, KV_cap, ...) tensors as
-    ``sdpa_dual_v_q4`` takes them.  Returns (B, H_kv*gr, 1, 2D) in
-    ``q1.dtype``."""
-    if _common._DISABLE:
-        return gda_decode_attention_q4_reference(q1, q2, k1_q, k2_q, v1_q, v2_q, scale,
-                                                 subln_weight, lambda_full, lambda_init, gr,
-                                                 group_size, bits, eps, kv_len)
+    ``sdpa_dual_v_q4`` takes them.  With ``new_kv`` the token's rows (in
+    ``q1.dtype``) are first quantised into row ``kv_len - 1``.  Returns
+    (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
     B, H_o, S_q, D = q1.shape
     _, H_kv, KV_cap, n_uint = k1_q[0].shape
     if kv_len is None:
         kv_len = KV_cap
+    slots = (k1_q, k2_q, v1_q, v2_q)
+    if new_kv is not None:
+        new_kv = _new_rows(new_kv, B, H_kv, D, q1.dtype, kv_len)
+        _require_in_place([x for t in slots for x in t])
+    if _common._DISABLE:
+        if new_kv is not None:
+            assert kv_len <= KV_cap, f"kv_len={kv_len} exceeds KV_cap={KV_cap}"
+            _write_rows_q_reference(slots, new_kv, kv_len, group_size, bits)
+        return gda_decode_attention_q4_reference(q1, q2, k1_q, k2_q, v1_q, v2_q, scale,
+                                                 subln_weight, lambda_full, lambda_init, gr,
+                                                 group_size, bits, eps, kv_len)
     assert n_uint * (32 // bits) == D, (
         f"k_data last axis = {n_uint} ⇒ packed D = {n_uint * (32 // bits)}, expected {D}"
     )
@@ -123,8 +183,7 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
     assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
     _q_contract(D, H_o, H_kv, group_size, bits, kv_len, KV_cap)
-    slots = (k1_q, k2_q, v1_q, v2_q)
-    dev = _native.require_device(q1, q2, *(x for t in slots for x in t))
+    dev = _native.require_device(q1, q2, *(x for t in slots for x in t), *(new_kv or ()))
     for t in slots:
         assert tuple(t[0].shape) == (B, H_kv, KV_cap, n_uint), "packed slots must match k1"
         for x in t[1:]:
@@ -140,12 +199,13 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     lib = _native.lib()
     ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
     ptrs = [x.data_ptr() for t in slots for x in t]
-    _native.check(
-        lib.motif_gda_decode_q(
-            q1.data_ptr(), q2.data_ptr(), *ptrs, w.data_ptr(), lam.data_ptr(),
-            float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q1.dtype), B,
-            H_kv, gr, D, KV_cap, kv_len, bits, group_size, float(scale), ws.data_ptr(),
-            ws.numel(), _native.stream_of(dev),
-        )
-    )
+    tail = (w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps), y.data_ptr(),
+            _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len, bits, group_size,
+            float(scale), ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    if new_kv is None:
+        rc = lib.motif_gda_decode_q(q1.data_ptr(), q2.data_ptr(), *ptrs, *tail)
+    else:
+        rc = lib.motif_gda_decode_q_append(q1.data_ptr(), q2.data_ptr(),
+                                           *(t.data_ptr() for t in new_kv), *ptrs, *tail)
+    _native.check(rc)
     return y

@@ -233,3 +233,143 @@ def test_fused_decode_q_groups_and_columns(gpu, rng, gr, gs):
 def test_fused_decode_q_poisoned_padding_and_bf16(gpu, rng):
     assert _run_q(gpu, rng, 1, 8, 4, 512, 385, 128, 4, 64, "f16", poison=True) <= 0
     assert _run_q(gpu, rng, 1, 4, 4, 256, 150, 128, 8, 64, "bf16") <= 0
+
+
+# ---------------------------------------------------------- append (write) ---
+def _append_inputs(gpu, B, Hkv, gr, cap, D, dt, seed):
+    import torch
+
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=g, device=gpu).to(dt)  # noqa: E731
+    q1, q2 = mk(B, Hkv * gr, 1, D), mk(B, Hkv, 1, D)
+    caches = [mk(B, Hkv, cap, D) for _ in range(4)]
+    rows = [mk(B, Hkv, 1, D) for _ in range(4)]
+    w = mk(2 * D)
+    lam_t = torch.tensor([0.4321], dtype=torch.float32, device=gpu)
+    return q1, q2, caches, rows, w, lam_t
+
+
+@pytest.mark.parametrize("B,Hkv,gr,cap,kv_len,D,tag", [
+    (1, 8, 4, 256, 1, 128, "f16"),       # the first token
+    (1, 8, 4, 256, 16, 128, "f16"),      # last row of the first 16-row block
+    (1, 8, 4, 256, 17, 128, "f16"),      # first row of the second block
+    (1, 8, 4, 3328, 3204, 128, "f16"),
+    (1, 8, 4, 16000, 16000, 128, "f16"),  # the last row of the capacity
+    (2, 3, 1, 301, 301, 128, "f16"),     # 2 columns, capacity not a multiple of 16
+    (1, 2, 15, 512, 385, 128, "f16"),    # 16 columns: the 4-wave kernel
+    (1, 4, 4, 256, 150, 64, "f16"),      # composed: head_dim 64
+    (1, 4, 4, 256, 150, 128, "bf16"),    # composed: bf16
+])
+def test_append_writes_row_then_attends(gpu, B, Hkv, gr, cap, kv_len, D, tag):
+    """``new_kv`` stores the token's rows at row kv_len - 1 of each slot
+    (bit-exact, nothing else touched) and the output is bit-identical to
+    writing the rows first and running the step without append."""
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention
+
+    dt = torch_dtype(tag)
+    q1, q2, caches, rows, w, lam_t = _append_inputs(gpu, B, Hkv, gr, cap, D, dt, kv_len)
+    for c in caches:
+        c[:, :, kv_len - 1] = 1e4  # stale contents of the row being written
+    expect = [c.clone() for c in caches]
+    for c, r in zip(expect, rows):
+        c[:, :, kv_len - 1:kv_len] = r
+    scale, lam_init, eps = 1.0 / np.sqrt(D), 0.2, 1e-5
+    print(f"gda_decode append B={B} Hkv={Hkv} gr={gr} cap={cap} kv_len={kv_len} D={D} {tag}",
+          flush=True)
+    y = gda_decode_attention(q1, q2, *caches, scale, w, lam_t, lam_init, gr, eps, kv_len=kv_len,
+                             new_kv=rows)
+    y_ref = gda_decode_attention(q1, q2, *expect, scale, w, lam_t, lam_init, gr, eps,
+                                 kv_len=kv_len)
+    torch.cuda.synchronize()
+    for c, e in zip(caches, expect):
+        assert torch.equal(c.view(torch.int16), e.view(torch.int16))
+    assert torch.isfinite(y).all()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
+def test_append_matches_oracle_step(gpu, rng):
+    """Oracle check of an append step: the oracle's step over the cache with
+    the new rows in place."""
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention
+
+    B, Hkv, gr, cap, kv_len, D, tag = 1, 8, 4, 512, 300, 128, "f16"
+    q1, q2, ks, w = _case(rng, B, Hkv, gr, cap, D, tag)
+    rows = [randn(rng, (B, Hkv, 1, D), tag) for _ in range(4)]
+    dt = torch_dtype(tag)
+    T = [np_to_torch(a, dt, gpu) for a in (q1, q2, *ks, w)]
+    R = [np_to_torch(a, dt, gpu) for a in rows]
+    scale, lam, lam_init, eps = 1.0 / np.sqrt(D), 0.4321, 0.2, 1e-5
+    lam_t = torch.tensor([lam], dtype=torch.float32, device=gpu)
+    y = gda_decode_attention(*T[:6], scale, T[6], lam_t, lam_init, gr, eps, kv_len=kv_len,
+                             new_kv=R)
+    torch.cuda.synchronize()
+    for k, r in zip(ks, rows):
+        k[:, :, kv_len - 1:kv_len] = r
+    ref, tol = _bar(q1, q2, *ks, w, scale, lam, lam_init, gr, eps, kv_len, tag)
+    assert float(np.max(np.abs(torch_to_np(y) - ref) - tol)) <= 0
+
+
+@pytest.mark.parametrize("bits,gs,gr,cap,kv_len,tag", [
+    (4, 64, 4, 256, 1, "f16"),
+    (4, 64, 4, 256, 17, "f16"),
+    (4, 64, 4, 3328, 3204, "f16"),
+    (8, 64, 4, 16000, 16000, "f16"),
+    (4, 32, 3, 300, 300, "f16"),      # 4 columns x 4 groups
+    (8, 128, 15, 512, 385, "f16"),    # 16 columns x 1 group
+    (4, 32, 4, 256, 200, "f16"),      # 32 columns: composed (quant_write4 first)
+    (8, 64, 4, 256, 150, "bf16"),     # composed: bf16
+])
+def test_append_q_quantises_row_then_attends(gpu, bits, gs, gr, cap, kv_len, tag):
+    """Packed cache: the token's rows are quantised into row kv_len - 1
+    bit-exactly as the oracle quantizer does (data words, scales, biases;
+    nothing else touched) and the output is bit-identical to the step without
+    append over that cache."""
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention_q4, quantize
+
+    B, Hkv, D = 1, 8 if gr <= 4 else 2, 128
+    dt = torch_dtype(tag)
+    q1, q2, caches, rows, w, lam_t = _append_inputs(gpu, B, Hkv, gr, cap, D, dt, kv_len + bits)
+    trips = []
+    for c in caches:  # the cache's other rows: any packed contents will do
+        c[:, :, kv_len - 1] = 1e3
+        trips.append(quantize(c, gs, bits))
+    expect = [tuple(x.clone() for x in t) for t in trips]
+    for t, r in zip(expect, rows):
+        for dst, src in zip(t, O.quantize(torch_to_np(r), gs, bits, out_dtype=tag)):
+            dst[:, :, kv_len - 1:kv_len] = np_to_torch(src, dst.dtype if dst.dtype != torch.uint32
+                                                       else None, gpu)
+    scale, lam_init, eps = 1.0 / np.sqrt(D), 0.2, 1e-5
+    print(f"gda_decode_q append bits={bits} gs={gs} gr={gr} cap={cap} kv_len={kv_len} {tag}",
+          flush=True)
+    y = gda_decode_attention_q4(q1, q2, *trips, scale, w, lam_t, lam_init, gr, gs, bits, eps,
+                                kv_len=kv_len, new_kv=rows)
+    y_ref = gda_decode_attention_q4(q1, q2, *expect, scale, w, lam_t, lam_init, gr, gs, bits,
+                                    eps, kv_len=kv_len)
+    torch.cuda.synchronize()
+    for t, e in zip(trips, expect):
+        assert torch.equal(t[0].view(torch.int32), e[0].view(torch.int32))
+        assert torch.equal(t[1].view(torch.int16), e[1].view(torch.int16))
+        assert torch.equal(t[2].view(torch.int16), e[2].view(torch.int16))
+    assert torch.isfinite(y).all()
+    assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16))
+
+
+def test_append_rejects_kv_len_zero_and_strided_cache(gpu):
+    import torch
+
+    from mlx_motif.kernels import gda_decode_attention
+
+    q1, q2, caches, rows, w, lam_t = _append_inputs(gpu, 1, 2, 2, 64, 128, torch.float16, 0)
+    with pytest.raises(ValueError, match="appended row"):
+        gda_decode_attention(q1, q2, *caches, 0.1, w, lam_t, 0.2, 2, kv_len=0, new_kv=rows)
+    strided = caches[0].transpose(2, 3).contiguous().transpose(2, 3)
+    with pytest.raises(ValueError, match="contiguous"):
+        gda_decode_attention(q1, q2, strided, *caches[1:], 0.1, w, lam_t, 0.2, 2, kv_len=5,
+                             new_kv=rows)

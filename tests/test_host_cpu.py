@@ -141,6 +141,63 @@ def test_disabled_epilogues_match_oracle(disabled, rng):
                                rtol=1e-4, atol=1e-4)
 
 
+def test_disabled_decode_append_writes_row_and_matches_oracle(disabled, rng):
+    """Reference path of ``new_kv``: the token's rows land at row kv_len - 1
+    of each slot and the step matches the oracle over that cache."""
+    q1, q2 = _t(rng, (1, 8, 1, 64), torch.float32), _t(rng, (1, 2, 1, 64), torch.float32)
+    caches = [_t(rng, (1, 2, 40, 64), torch.float32) for _ in range(4)]
+    rows = [_t(rng, (1, 2, 1, 64), torch.float32) for _ in range(4)]
+    before = [c.clone() for c in caches]
+    w, lam = _t(rng, (128,), torch.float32), torch.tensor([0.4321])
+    y = K.gda_decode_attention(q1, q2, *caches, 0.125, w, lam, 0.2, 4, 1e-5, kv_len=31,
+                               new_kv=rows)
+    for c, b, r in zip(caches, before, rows):
+        b[:, :, 30:31] = r
+        assert torch.equal(c, b)
+    ref = O.gda_decode_attention(q1.numpy(), q2.numpy(), *(c.numpy() for c in caches), 0.125,
+                                 w.numpy(), 0.4321, 0.2, 4, 1e-5, 31, dtype="f32")
+    np.testing.assert_allclose(y.numpy(), ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_disabled_decode_q_append_quantises_row_like_oracle(disabled, rng, bits):
+    q1, q2 = _t(rng, (1, 8, 1, 128)), _t(rng, (1, 2, 1, 128))
+    trips = [K.quantize(_t(rng, (1, 2, 24, 128)), 64, bits) for _ in range(4)]
+    rows = [_t(rng, (1, 2, 1, 128)) for _ in range(4)]
+    w, lam = _t(rng, (256,)), torch.tensor([0.4321])
+    K.gda_decode_attention_q4(q1, q2, *trips, 0.09, w, lam, 0.2, 4, 64, bits, 1e-5, kv_len=24,
+                              new_kv=rows)
+    for t, r in zip(trips, rows):
+        rd, rs, rb = O.quantize(r.float().numpy(), 64, bits, out_dtype="f16")
+        np.testing.assert_array_equal(t[0][:, :, 23:24].view(torch.int32).numpy().view(np.uint32),
+                                      rd)
+        np.testing.assert_array_equal(t[1][:, :, 23:24].float().numpy(), np.float32(rs))
+        np.testing.assert_array_equal(t[2][:, :, 23:24].float().numpy(), np.float32(rb))
+
+
+def test_decode_append_contract(enabled, rng):
+    """Checks made before any native call: kv_len counts the new row, the
+    rows' shape and dtype, and in-place (contiguous) cache buffers."""
+    q1, q2 = _t(rng, (1, 4, 1, 64)), _t(rng, (1, 2, 1, 64))
+    caches = [_t(rng, (1, 2, 16, 64)) for _ in range(4)]
+    rows = [_t(rng, (1, 2, 1, 64)) for _ in range(4)]
+    w, lam = _t(rng, (128,)), torch.tensor([0.5])
+    with pytest.raises(ValueError, match="appended row"):
+        K.gda_decode_attention(q1, q2, *caches, 0.1, w, lam, 0.2, 2, kv_len=0, new_kv=rows)
+    with pytest.raises(ValueError, match="k1_new"):
+        K.gda_decode_attention(q1, q2, *caches, 0.1, w, lam, 0.2, 2, kv_len=3, new_kv=rows[:3])
+    with pytest.raises(TypeError, match="new_kv dtype"):
+        K.gda_decode_attention(q1, q2, *caches, 0.1, w, lam, 0.2, 2, kv_len=3,
+                               new_kv=[r.float() for r in rows])
+    with pytest.raises(AssertionError, match="new_kv rows"):
+        K.gda_decode_attention(q1, q2, *caches, 0.1, w, lam, 0.2, 2, kv_len=3,
+                               new_kv=[r[:, :1] for r in rows])
+    strided = caches[0].transpose(2, 3).contiguous().transpose(2, 3)
+    with pytest.raises(ValueError, match="contiguous"):
+        K.gda_decode_attention(q1, q2, strided, *caches[1:], 0.1, w, lam, 0.2, 2, kv_len=3,
+                               new_kv=rows)
+
+
 def test_polynorm_zero_rows_returns_zeros(enabled):
     x = torch.zeros((0, 16))
     assert K.polynorm(x, torch.ones(3), torch.zeros(1)).shape == (0, 16)
