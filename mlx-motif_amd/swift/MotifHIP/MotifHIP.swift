@@ -180,6 +180,60 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// The decode step that first writes the token's rows (newKeys1 .. newValue2,
+    /// each (B, kvHeads, 1, D)) at row kvLen - 1 of the four slots, inside the
+    /// attention launch when the step is fused.  kvLen counts the new row.
+    public static func gdaDecodeAppend(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        newKeys1: UnsafeRawPointer, newKeys2: UnsafeRawPointer, newValue1: UnsafeRawPointer,
+        newValue2: UnsafeRawPointer, keys1: UnsafeMutableRawPointer,
+        keys2: UnsafeMutableRawPointer, value1: UnsafeMutableRawPointer,
+        value2: UnsafeMutableRawPointer, sublnWeight: UnsafeRawPointer,
+        lambdaFull: UnsafePointer<Float>, oneMinusLambdaInit: Float, eps: Float,
+        output: UnsafeMutableRawPointer, dtype: MotifHIPDType, batch: Int, kvHeads: Int,
+        gr: Int, headDim: Int, kvCapacity: Int, kvLen: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_append(originQueries, noiseQueries, newKeys1, newKeys2,
+                                         newValue1, newValue2, keys1, keys2, value1, value2,
+                                         sublnWeight, lambdaFull, oneMinusLambdaInit, eps,
+                                         output, dtype.rawValue, Int32(batch), Int32(kvHeads),
+                                         Int32(gr), Int32(headDim), Int32(kvCapacity),
+                                         Int32(kvLen), scale, workspace, workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// Same over the packed cache: the token's rows are quantised into row
+    /// kvLen - 1 (bit-exactly as quantWrite4 stores them).
+    public static func gdaDecodeQuantizedAppend(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        newKeys1: UnsafeRawPointer, newKeys2: UnsafeRawPointer, newValue1: UnsafeRawPointer,
+        newValue2: UnsafeRawPointer,
+        keys1: MotifHIPQuantizedTriple, keys2: MotifHIPQuantizedTriple,
+        value1: MotifHIPQuantizedTriple, value2: MotifHIPQuantizedTriple,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int, kvCapacity: Int,
+        kvLen: Int, bits: Int, groupSize: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_q_append(originQueries, noiseQueries, newKeys1, newKeys2,
+                                           newValue1, newValue2,
+                                           keys1.data, keys1.scales, keys1.biases,
+                                           keys2.data, keys2.scales, keys2.biases,
+                                           value1.data, value1.scales, value1.biases,
+                                           value2.data, value2.scales, value2.biases,
+                                           sublnWeight, lambdaFull, oneMinusLambdaInit, eps,
+                                           output, dtype.rawValue, Int32(batch),
+                                           Int32(kvHeads), Int32(gr), Int32(headDim),
+                                           Int32(kvCapacity), Int32(kvLen), Int32(bits),
+                                           Int32(groupSize), scale, workspace, workspaceBytes,
+                                           stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// PolyNorm over the last axis of x (rows, D).
     public static func polynorm(
         x: UnsafeRawPointer, weight: UnsafeRawPointer, bias: UnsafeRawPointer,
