@@ -43,6 +43,16 @@ __device__ inline void lds_copy16_rsrc(__amdgpu_buffer_rsrc_t r, unsigned voff, 
 __device__ inline unsigned lds_byte_addr(const void* p) {
   return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
+// 4 fp16 values through ds_read_b64_tr_b16 (gfx950) from an 8-byte aligned
+// LDS address: within each 16-lane group, lane i receives element i % 4 of
+// the 8 bytes addressed by lane 4*k + i/4 in slot k (k = 0..3).
+__device__ inline half4_t lds_read_tr16(const void* p) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t* lds_s4_ptr;
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(p));
+  return __builtin_bit_cast(half4_t, v);
+}
+
 // Waits on this wave's outstanding vector memory operations (at most N
 // left); also a compiler barrier for memory accesses.
 template <int N>
@@ -212,39 +222,32 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
     for (int j = 0; j < 8; ++j)
       pb[j] = (_Float16)(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
 
-    // V rows 16*h + 4*blk + r, channels 8*col .. 8*col+7 (dword t holds
-    // channels 8*col + 2t, +1).
-    uint32_t v1w[2][4][4], v2w[2][4][4];
+    // V^T fragments straight from the ring with transposing LDS reads
+    // (ds_read_b64_tr_b16).  In the 16-lane group of lanes with one blk,
+    // lane 4*jj + q points at 4 channels of row 16*h + 4*blk + jj, and group
+    // lane i receives element i % 4 of the 4 channels lane 4*jj + i/4
+    // pointed at, for jj = 0..3: four rows of one channel, the A fragment.
+    // MFMA j takes channels 32*q + 4*j .. +3 from lane 4*jj + q, so A row m
+    // is channel 32*(m/4) + 4*j + m%4 and a lane's results cover 32
+    // consecutive channels.
+    const int jj = col >> 2;
+    const int qq = col & 3;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int j = 0; j < 8; ++j) {
+      half4_t f1[2], f2[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int vr = 16 * h + 4 * blk + r;
-        const int o = vr * 256 + ((col ^ (vr % 16)) * 16);
-        const uint4 w1 = *reinterpret_cast<const uint4*>(&V1t[o]);
-        const uint4 w2 = *reinterpret_cast<const uint4*>(&V2t[o]);
-        v1w[h][r][0] = w1.x; v1w[h][r][1] = w1.y; v1w[h][r][2] = w1.z; v1w[h][r][3] = w1.w;
-        v2w[h][r][0] = w2.x; v2w[h][r][1] = w2.y; v2w[h][r][2] = w2.z; v2w[h][r][3] = w2.w;
+      for (int h = 0; h < 2; ++h) {
+        const int vr = 16 * h + 4 * blk + jj;
+        const int o = vr * 256 + (((4 * qq + j / 2) ^ (vr % 16)) * 16) + (j % 2) * 8;
+        f1[h] = lds_read_tr16(&V1t[o]);
+        f2[h] = lds_read_tr16(&V2t[o]);
       }
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const uint32_t sel = hh ? 0x07060302u : 0x05040100u;  // hi or lo halves
-        const half8_t a1 = __builtin_bit_cast(
-            half8_t, make_uint4(__builtin_amdgcn_perm(v1w[0][1][t], v1w[0][0][t], sel),
-                                __builtin_amdgcn_perm(v1w[0][3][t], v1w[0][2][t], sel),
-                                __builtin_amdgcn_perm(v1w[1][1][t], v1w[1][0][t], sel),
-                                __builtin_amdgcn_perm(v1w[1][3][t], v1w[1][2][t], sel)));
-        const half8_t a2 = __builtin_bit_cast(
-            half8_t, make_uint4(__builtin_amdgcn_perm(v2w[0][1][t], v2w[0][0][t], sel),
-                                __builtin_amdgcn_perm(v2w[0][3][t], v2w[0][2][t], sel),
-                                __builtin_amdgcn_perm(v2w[1][1][t], v2w[1][0][t], sel),
-                                __builtin_amdgcn_perm(v2w[1][3][t], v2w[1][2][t], sel)));
-        acc1[2 * t + hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb, acc1[2 * t + hh], 0, 0, 0);
-        acc2[2 * t + hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, pb, acc2[2 * t + hh], 0, 0, 0);
-      }
+      const half8_t a1 = half8_t{f1[0][0], f1[0][1], f1[0][2], f1[0][3],
+                                 f1[1][0], f1[1][1], f1[1][2], f1[1][3]};
+      const half8_t a2 = half8_t{f2[0][0], f2[0][1], f2[0][2], f2[0][3],
+                                 f2[1][0], f2[1][1], f2[1][2], f2[1][3]};
+      acc1[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb, acc1[j], 0, 0, 0);
+      acc2[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, pb, acc2[j], 0, 0, 0);
     }
     accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, accl, 0, 0, 0);
   };
@@ -276,37 +279,35 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
     st = st + 1 == NS ? 0 : st + 1;
   }
 
-  // acc[j][r] of lane (col, blk) is channel 8*(4*blk + r) + j of column col.
+  // acc[j][r] of lane (col, blk) is channel 32*blk + 4*j + r of column col.
   if (!col_ok) return;
   const long vrow = qrow0 + vh;
   const float l = accl[0];
   if (a.nsplit == 1) {
     const float inv = l == 0.f ? 1.f : 1.f / l;  // o stays 0 when no key is visible
+    uint16_t* yp = (uint16_t*)a.y + vrow * 2 * D + 32 * blk;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ch = 8 * (4 * blk + r);
+    for (int p = 0; p < 4; ++p) {  // channels 32*blk + 8*p .. +7
       uint32_t w1[4], w2[4];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const half2_t x1 = half2_t{(_Float16)(acc1[2 * p][r] * inv), (_Float16)(acc1[2 * p + 1][r] * inv)};
-        const half2_t x2 = half2_t{(_Float16)(acc2[2 * p][r] * inv), (_Float16)(acc2[2 * p + 1][r] * inv)};
-        w1[p] = __builtin_bit_cast(uint32_t, x1);
-        w2[p] = __builtin_bit_cast(uint32_t, x2);
+      for (int t = 0; t < 4; ++t) {
+        const int j = 2 * p + t / 2;
+        const int r = 2 * (t % 2);
+        const half2_t x1 = half2_t{(_Float16)(acc1[j][r] * inv), (_Float16)(acc1[j][r + 1] * inv)};
+        const half2_t x2 = half2_t{(_Float16)(acc2[j][r] * inv), (_Float16)(acc2[j][r + 1] * inv)};
+        w1[t] = __builtin_bit_cast(uint32_t, x1);
+        w2[t] = __builtin_bit_cast(uint32_t, x2);
       }
-      uint16_t* yp = (uint16_t*)a.y + vrow * 2 * D;
-      *reinterpret_cast<uint4*>(yp + ch) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-      *reinterpret_cast<uint4*>(yp + D + ch) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+      *reinterpret_cast<uint4*>(yp + 8 * p) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+      *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
     }
   } else {
     const int ns = a.nsplit;
-    float* po = a.part_o + (vrow * ns + split) * 2 * D;
+    float* po = a.part_o + (vrow * ns + split) * 2 * D + 32 * blk;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int ch = 8 * (4 * blk + r);
-      *reinterpret_cast<float4*>(po + ch) = make_float4(acc1[0][r], acc1[1][r], acc1[2][r], acc1[3][r]);
-      *reinterpret_cast<float4*>(po + ch + 4) = make_float4(acc1[4][r], acc1[5][r], acc1[6][r], acc1[7][r]);
-      *reinterpret_cast<float4*>(po + D + ch) = make_float4(acc2[0][r], acc2[1][r], acc2[2][r], acc2[3][r]);
-      *reinterpret_cast<float4*>(po + D + ch + 4) = make_float4(acc2[4][r], acc2[5][r], acc2[6][r], acc2[7][r]);
+    for (int j = 0; j < 8; ++j) {
+      *reinterpret_cast<float4*>(po + 4 * j) = make_float4(acc1[j][0], acc1[j][1], acc1[j][2], acc1[j][3]);
+      *reinterpret_cast<float4*>(po + D + 4 * j) = make_float4(acc2[j][0], acc2[j][1], acc2[j][2], acc2[j][3]);
     }
     if (blk == 0)
       *reinterpret_cast<float2*>(a.part_ml + (vrow * ns + split) * 2) = make_float2(m_run, l);
