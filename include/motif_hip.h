@@ -128,6 +128,36 @@ int motif_sdpa_dual_v_q_rows(const void* q,
                              int causal, int bits, int group_size, float scale,
                              void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same three calls under the names a port of the reference binds: the
+ * Metal kernel's name motif_sdpa_dual_v_q4 (attention.py:293) for
+ * motif_sdpa_dual_v_q, and motif_sdpa_dual_v_verify / _q4_verify for the
+ * multi-row calls of the speculative-verify caller
+ * (MotifSpeculativeDecoding.swift:204-206).  Arguments and results are
+ * those of motif_sdpa_dual_v_q, motif_sdpa_dual_v_rows and
+ * motif_sdpa_dual_v_q_rows. */
+int motif_sdpa_dual_v_q4(const void* q,
+                         const uint32_t* k_data, const void* k_scales, const void* k_biases,
+                         const uint32_t* v1_data, const void* v1_scales, const void* v1_biases,
+                         const uint32_t* v2_data, const void* v2_scales, const void* v2_biases,
+                         void* y, int dtype, int B, int Hq, int Hkv, int D, int kv_cap,
+                         int kv_len, int bits, int group_size, float scale, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+int motif_sdpa_dual_v_verify(const void* q, const void* k, const void* v1, const void* v2,
+                             void* y, int dtype, int B, int Hq, int Hkv, int S_q, int D,
+                             int kv_cap, int kv_len, int causal, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+int motif_sdpa_dual_v_q4_verify(const void* q,
+                                const uint32_t* k_data, const void* k_scales,
+                                const void* k_biases, const uint32_t* v1_data,
+                                const void* v1_scales, const void* v1_biases,
+                                const uint32_t* v2_data, const void* v2_scales,
+                                const void* v2_biases, void* y, int dtype, int B, int Hq,
+                                int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal,
+                                int bits, int group_size, float scale, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * MLX affine quantisation (mx.quantize, mode "affine") of `rows` rows of D
  * values: data (rows, D*bits/32) uint32, scales/biases (rows, D/group_size)

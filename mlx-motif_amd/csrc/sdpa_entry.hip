@@ -440,6 +440,39 @@ int motif_sdpa_dual_v_q_rows(const void* q, const uint32_t* k_data, const void* 
                     stream);
 }
 
+int motif_sdpa_dual_v_q4(const void* q, const uint32_t* k_data, const void* k_scales,
+                         const void* k_biases, const uint32_t* v1_data, const void* v1_scales,
+                         const void* v1_biases, const uint32_t* v2_data, const void* v2_scales,
+                         const void* v2_biases, void* y, int dtype, int B, int Hq, int Hkv, int D,
+                         int kv_cap, int kv_len, int bits, int group_size, float scale,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  return motif_sdpa_dual_v_q(q, k_data, k_scales, k_biases, v1_data, v1_scales, v1_biases,
+                             v2_data, v2_scales, v2_biases, y, dtype, B, Hq, Hkv, D, kv_cap,
+                             kv_len, bits, group_size, scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_verify(const void* q, const void* k, const void* v1, const void* v2,
+                             void* y, int dtype, int B, int Hq, int Hkv, int S_q, int D,
+                             int kv_cap, int kv_len, int causal, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return motif_sdpa_dual_v_rows(q, k, v1, v2, y, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len,
+                                causal, scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_q4_verify(const void* q, const uint32_t* k_data, const void* k_scales,
+                                const void* k_biases, const uint32_t* v1_data,
+                                const void* v1_scales, const void* v1_biases,
+                                const uint32_t* v2_data, const void* v2_scales,
+                                const void* v2_biases, void* y, int dtype, int B, int Hq,
+                                int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal,
+                                int bits, int group_size, float scale, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return motif_sdpa_dual_v_q_rows(q, k_data, k_scales, k_biases, v1_data, v1_scales, v1_biases,
+                                  v2_data, v2_scales, v2_biases, y, dtype, B, Hq, Hkv, S_q, D,
+                                  kv_cap, kv_len, causal, bits, group_size, scale, workspace,
+                                  workspace_bytes, stream);
+}
+
 }  // extern "C"
 
 // Same over the packed cache; new_kv rows are quantised into row kv_len - 1

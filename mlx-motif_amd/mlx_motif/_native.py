@@ -55,6 +55,18 @@ _SIGNATURES = {
         _c_int,
         [_vp] * 11 + [_c_int] * 11 + [_c_f, _vp, _c_sz, _vp],
     ),
+    "motif_sdpa_dual_v_q4": (
+        _c_int,
+        [_vp] * 11 + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],
+    ),
+    "motif_sdpa_dual_v_verify": (
+        _c_int,
+        [_vp] * 5 + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],
+    ),
+    "motif_sdpa_dual_v_q4_verify": (
+        _c_int,
+        [_vp] * 11 + [_c_int] * 11 + [_c_f, _vp, _c_sz, _vp],
+    ),
     "motif_quantize": (_c_int, [_vp] * 4 + [_c_int, _c_i64, _c_int, _c_int, _c_int, _vp]),
     "motif_dequantize": (_c_int, [_vp] * 4 + [_c_int, _c_i64, _c_int, _c_int, _c_int, _vp]),
     "motif_quant_write4": (
