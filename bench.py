@@ -90,18 +90,20 @@ def time_calls(torch, calls, steps: int, warmup: int, use_graph: bool = True):
     return start.elapsed_time(end) * 1000.0 / steps
 
 
-def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
+def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1,
+                    bf16=False):
+    """fp16-cache calls (``bf16``: the same over a bf16 cache)."""
     from mlx_motif import _native
 
+    dt, code = (torch.bfloat16, 1) if bf16 else (torch.float16, 0)
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
-    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).half()
+    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).to(dt)
     sets = []
     for _ in range(nsets):
-        k, v1, v2 = (torch.randn((B, hkv, cap, D), generator=g, device=dev).half()
+        k, v1, v2 = (torch.randn((B, hkv, cap, D), generator=g, device=dev).to(dt)
                      for _ in range(3))
-        sets.append((k, v1, v2, torch.empty((B, hq, s_q, 2 * D), dtype=torch.float16,
-                                            device=dev)))
+        sets.append((k, v1, v2, torch.empty((B, hq, s_q, 2 * D), dtype=dt, device=dev)))
     nbytes = lib.motif_sdpa_workspace_bytes(B, hq, hkv, s_q, kv_len, D)
     ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
     scale = 1.0 / D ** 0.5
@@ -111,11 +113,11 @@ def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=H
             stream = torch.cuda.current_stream().cuda_stream
             if s_q == 1:
                 st = lib.motif_sdpa_dual_v(q.data_ptr(), k.data_ptr(), v1.data_ptr(),
-                                           v2.data_ptr(), y.data_ptr(), 0, B, hq, hkv, D, cap,
+                                           v2.data_ptr(), y.data_ptr(), code, B, hq, hkv, D, cap,
                                            kv_len, scale, ws.data_ptr(), ws.numel(), stream)
             else:
                 st = lib.motif_sdpa_dual_v_rows(q.data_ptr(), k.data_ptr(), v1.data_ptr(),
-                                                v2.data_ptr(), y.data_ptr(), 0, B, hq, hkv, s_q,
+                                                v2.data_ptr(), y.data_ptr(), code, B, hq, hkv, s_q,
                                                 D, cap, kv_len, 1, scale, ws.data_ptr(),
                                                 ws.numel(), stream)
             _native.check(st)
@@ -451,6 +453,11 @@ def run_extra(torch, lib, dev, args):
                                    "gbps": round(gbps, 1),
                                    "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 1)}))
 
+    # the headline shape over a bf16 cache (bf16 matrix-core kernel)
+    calls, keep = make_fp16_calls(torch, lib, dev, 8, bf16=True)
+    report("sdpa_dual_v bf16 kv16000", time_calls(torch, calls, steps, warm), alg_bytes("f16"))
+    del calls, keep
+    torch.cuda.empty_cache()
     # 48 back-to-back layer calls at kv_len 3204 over 48 distinct layer buffers
     calls, keep = make_fp16_calls(torch, lib, dev, 48, kv_len=3204, cap=3328)
     report("sdpa_dual_v f16 kv3204 x48 layers", time_calls(torch, calls, 48 * 4, warm),

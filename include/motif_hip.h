@@ -215,7 +215,7 @@ int motif_gda_post(const void* merged, const void* subln_w, void* y, int dtype, 
  * sdpa_dual_v(q2, k2, v1, v2) and gda_post_split on their outputs.
  * Replaces the DUAL_V caller sequence of src/mlx_motif/model.py:749-768
  * (two sdpa_dual_v calls and gda_post_split); the reference has no single
- * kernel for it.  For the fp16 cache at D = 128 it runs as two launches:
+ * kernel for it.  For the fp16 or bf16 cache at D = 128 it runs as two launches:
  * one attention launch reads each KV head's k1, k2, v1 and v2 rows once for
  * both passes (4 cache streams instead of the calls' 6), and the split merge
  * applies the epilogue.  Other dtypes and head dims compose the separate

@@ -329,7 +329,8 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
     MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the appended row", name, kv_len);
   }
   hipStream_t s = (hipStream_t)stream;
-  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+  const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
+                     tuning().mfma && gr + 1 <= 16 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
                      aligned(k1, 16) && aligned(k2, 16) &&
                      aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8) &&
@@ -346,7 +347,9 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
       a.new_k1 = new_kv[0]; a.new_k2 = new_kv[1]; a.new_v1 = new_kv[2]; a.new_v2 = new_kv[3];
       a.append = 1;
     }
-    return launch_gda_decode_f16(a, gda_columns(gr), sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+    const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+    return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks, s)
+                              : launch_gda_decode_bf16(a, gda_columns(gr), nblocks, s);
   }
   if (new_kv) {  // row kv_len - 1 of each slot: B * Hkv rows of D values
     const size_t row = (size_t)D * (dtype == MOTIF_F32 ? 4 : 2);

@@ -16,10 +16,11 @@ namespace motif {
 int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan& p, int D,
                                               hipStream_t s) {
   const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
-  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
+                std::is_same<MOTIF_ELEM, bf16_t>::value) {
     if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0 &&
         a.kv_len <= kMfmaMaxRows)
-      return launch_sdpa_mfma_f16(a, p.gc, p.waves, nblocks, s);
+      return launch_sdpa_mfma_16<MOTIF_ELEM>(a, p.gc, p.waves, nblocks, s);
   }
   switch (D) {
     case 32: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 32>>(a, p.gc, p.waves, nblocks, s);
@@ -90,15 +91,16 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
 }
 
 // Fused GDA decode step: one attention launch for the origin and noise
-// passes, then the merge + gda_post_split launch.  Compiled for the fp16
-// cache at head_dim 128 only; the entry point composes the separate calls
-// otherwise.
+// passes, then the merge + gda_post_split launch.  Compiled for the fp16 and
+// bf16 caches at head_dim 128 only; the entry point composes the separate
+// calls otherwise.
 int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int nblocks,
                                                hipStream_t s) {
-  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
-    const int rc = launch_gda_decode_mfma_f16(a, gc, nblocks, s);
+  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
+                std::is_same<MOTIF_ELEM, bf16_t>::value) {
+    const int rc = launch_gda_decode_mfma_16<MOTIF_ELEM>(a, gc, nblocks, s);
     if (rc != MOTIF_OK) return rc;
-    return launch_gda_decode_merge_d<half_t, 128>(a, s);
+    return launch_gda_decode_merge_d<MOTIF_ELEM, 128>(a, s);
   }
   set_error("gda_decode: no fused variant for this element type");
   return MOTIF_ERR_UNSUPPORTED;

@@ -33,7 +33,33 @@ namespace motif {
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Matrix-core operands of a 16-bit cache element type: the 8-element A/B
+// vector of v_mfma_f32_16x16x32_{f16,bf16} and the rounding of the softmax
+// weights p to that type (both MFMA operands share it).  K, V and q enter
+// the MFMAs exactly as stored.
+template <typename T>
+struct MfmaOp;
+template <>
+struct MfmaOp<half_t> {
+  typedef half8_t V8;
+  typedef _Float16 S;
+  __device__ static inline floatx4 mma(V8 a, V8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline S from_f32(float x) { return (S)x; }
+};
+template <>
+struct MfmaOp<bf16_t> {
+  typedef bf16x8_t V8;
+  typedef __bf16 S;
+  __device__ static inline floatx4 mma(V8 a, V8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static inline S from_f32(float x) { return (S)x; }  // round to nearest even
+};
 
 // Lazy rescaling.  The reference point m_run of the online softmax is raised
 // only when a tile's max exceeds it by more than a slack (log2 units); until
@@ -41,7 +67,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 // reference point, so o / l and the split partials (m_run, l, o) are the
 // same quantities as with an exact running max, and most tiles skip the
 // rescale of the 68 accumulator registers.  The slack only bounds p, which
-// the matrix cores take as fp16: 2^8 leaves fp16 p a wide margin.
+// the matrix cores take as fp16 or bf16: 2^8 leaves p a wide margin.
 constexpr float kRescaleSlackF16 = 8.f;
 
 // Causal row limit of virtual head vh (see sdpa_dual_v_kernel).
@@ -61,9 +87,9 @@ __device__ inline bool append_owner(const SdpaArgs& a, int split, int wave) {
   return wave == t % NW && split == (t / NW) % a.nsplit;
 }
 
-// fp16 rows: lane L copies 16 bytes (chunk L % 16) of slot L / 16 (k1, k2,
-// v1, v2) into row kv_len - 1 of KV head bk.
-__device__ inline void append_rows_f16(const SdpaArgs& a, long bk, int lane) {
+// 16-bit rows of 128 values: lane L copies 16 bytes (chunk L % 16) of slot
+// L / 16 (k1, k2, v1, v2) into row kv_len - 1 of KV head bk.
+__device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
   const int slot = lane / 16;
   const int chunk = lane % 16;
   const void* src = slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
@@ -76,10 +102,13 @@ __device__ inline void append_rows_f16(const SdpaArgs& a, long bk, int lane) {
 // DUAL: fused GDA decode step.  Columns 0..G-1 are the origin heads of the
 // KV head (scores from k), column G its noise head (scores from k2); both
 // share the V1/V2 rows, and the partials go to the fused merge launch.
-template <int GC, int NW, int U, bool DUAL = false>
+// T: half_t (fp16 cache, v_mfma_f32_16x16x32_f16) or bf16_t (bf16 cache,
+// v_mfma_f32_16x16x32_bf16).
+template <typename T, int GC, int NW, int U, bool DUAL = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
-sdpa_mfma_f16_kernel(SdpaArgs a) {
-  using T = half_t;
+sdpa_mfma_kernel(SdpaArgs a) {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
   constexpr int D = 128;
   static_assert(GC <= 16, "virtual heads ride the 16 MFMA columns");
   static_assert(U % 2 == 0, "tiles are computed in pairs");
@@ -112,12 +141,12 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   bool owner = false;
   if constexpr (DUAL) {
     owner = append_owner<NW>(a, split, wave);
-    if (owner) append_rows_f16(a, bk, lane);
+    if (owner) append_rows_16bit(a, bk, lane);
   }
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds head col,
   // channels 32*s + 8*blk .. +7 for k-step s.
-  half8_t qb[4];
+  V8 qb[4];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
     if constexpr (DUAL) {
@@ -128,7 +157,7 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
-      qb[s] = __builtin_bit_cast(half8_t, w);
+      qb[s] = __builtin_bit_cast(V8, w);
     }
   }
 
@@ -141,8 +170,8 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   }
   accl = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegSentinel;
-  const half8_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
-                        (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+  const typename Op::S one = Op::from_f32(1.f);
+  const V8 ones = {one, one, one, one, one, one, one, one};
 
   // Rows are dealt to the splits in blocks of NW 16-row tiles, round robin:
   // tile k of wave w in split s is tile (k * nsplit + s) * NW + w of the KV
@@ -172,8 +201,8 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
         if (has) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new rows are stored
       }
     }
-    half8_t ka[U][4];
-    half8_t ka2[DUAL ? U : 1][4];
+    V8 ka[U][4];
+    V8 ka2[DUAL ? U : 1][4];
     uint32_t v1w[U][4][4], v2w[U][4][4];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -181,11 +210,11 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
       // K rows for S^T: row t0 + col (A operand row = lane % 16).
       const unsigned koff = (unsigned)((t0 + col) * D * 2 + 16 * blk);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(half8_t, bload4(rk, koff + 64u * s));
+      for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(V8, bload4(rk, koff + 64u * s));
       if constexpr (DUAL) {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          ka2[u][s] = __builtin_bit_cast(half8_t, bload4(rk2, koff + 64u * s));
+          ka2[u][s] = __builtin_bit_cast(V8, bload4(rk2, koff + 64u * s));
       }
       // V rows t0 + 4*blk + r: 16 bytes per lane, dwords 4*col .. 4*col+3
       // (dword 4*col + t holds channels 8*col + 2t, +1); one instruction
@@ -212,12 +241,12 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
         sacc[v] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          sacc[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[u + v][s], qb[s], sacc[v], 0, 0, 0);
+          sacc[v] = Op::mma(ka[u + v][s], qb[s], sacc[v]);
         if constexpr (DUAL) {
           floatx4 s2 = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int s = 0; s < 4; ++s)
-            s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka2[u + v][s], qb[s], s2, 0, 0, 0);
+            s2 = Op::mma(ka2[u + v][s], qb[s], s2);
           if (col == a.G) sacc[v] = s2;
         }
       }
@@ -248,31 +277,31 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
         accl *= fac;
         m_run = m_new;
       }
-      half8_t pb;
+      V8 pb;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        pb[j] = (_Float16)(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+        pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
 
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t sel = h ? 0x07060302u : 0x05040100u;  // hi or lo halves, row r in half r%2
-          const half8_t a1 = __builtin_bit_cast(
-              half8_t, make_uint4(__builtin_amdgcn_perm(v1w[u][1][t], v1w[u][0][t], sel),
+          const V8 a1 = __builtin_bit_cast(
+              V8, make_uint4(__builtin_amdgcn_perm(v1w[u][1][t], v1w[u][0][t], sel),
                                   __builtin_amdgcn_perm(v1w[u][3][t], v1w[u][2][t], sel),
                                   __builtin_amdgcn_perm(v1w[u + 1][1][t], v1w[u + 1][0][t], sel),
                                   __builtin_amdgcn_perm(v1w[u + 1][3][t], v1w[u + 1][2][t], sel)));
-          const half8_t a2 = __builtin_bit_cast(
-              half8_t, make_uint4(__builtin_amdgcn_perm(v2w[u][1][t], v2w[u][0][t], sel),
+          const V8 a2 = __builtin_bit_cast(
+              V8, make_uint4(__builtin_amdgcn_perm(v2w[u][1][t], v2w[u][0][t], sel),
                                   __builtin_amdgcn_perm(v2w[u][3][t], v2w[u][2][t], sel),
                                   __builtin_amdgcn_perm(v2w[u + 1][1][t], v2w[u + 1][0][t], sel),
                                   __builtin_amdgcn_perm(v2w[u + 1][3][t], v2w[u + 1][2][t], sel)));
-          acc1[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb, acc1[2 * t + h], 0, 0, 0);
-          acc2[2 * t + h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, pb, acc2[2 * t + h], 0, 0, 0);
+          acc1[2 * t + h] = Op::mma(a1, pb, acc1[2 * t + h]);
+          acc2[2 * t + h] = Op::mma(a2, pb, acc2[2 * t + h]);
         }
       }
-      accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, accl, 0, 0, 0);
+      accl = Op::mma(ones, pb, accl);
     }
   }
 
@@ -304,33 +333,35 @@ sdpa_mfma_f16_kernel(SdpaArgs a) {
   wg_epilogue<T, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
-// fp16 cache, head_dim 128, <= 8 virtual heads per workgroup.
-inline int launch_sdpa_mfma_f16(const SdpaArgs& a, int gc, int waves, int nblocks,
-                                hipStream_t stream) {
+// 16-bit cache (T = half_t or bf16_t), head_dim 128, <= 8 virtual heads per
+// workgroup.
+template <typename T>
+inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks,
+                               hipStream_t stream) {
   switch (gc) {
     case 1:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<1, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<1, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 2:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 4:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 8:
-      hipLaunchKernelGGL((sdpa_mfma_f16_kernel<8, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       break;
     default:
       set_error("sdpa_dual_v: no MFMA variant for %d heads per workgroup", gc);
@@ -339,14 +370,15 @@ inline int launch_sdpa_mfma_f16(const SdpaArgs& a, int gc, int waves, int nblock
   return check_launch("sdpa_dual_v (mfma)");
 }
 
-// Fused GDA decode step, fp16 cache, head_dim 128: gc = columns (G + 1,
+// Fused GDA decode step, 16-bit cache, head_dim 128: gc = columns (G + 1,
 // rounded up to 2, 4, 8 or 16).
-inline int launch_gda_decode_mfma_f16(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
+template <typename T>
+inline int launch_gda_decode_mfma_16(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
   switch (gc) {
-    case 2: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<2, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<4, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<8, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
-    case 16: hipLaunchKernelGGL((sdpa_mfma_f16_kernel<16, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 16: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 16, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a); break;
     default:
       set_error("gda_decode: no fused variant for %d columns", gc);
       return MOTIF_ERR_UNSUPPORTED;

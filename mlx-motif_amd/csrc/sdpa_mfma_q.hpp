@@ -229,7 +229,7 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
 // chunks (a.nchunk > 1: more virtual heads than one pass holds, e.g. a
 // verify slab) read each row in several workgroups and use cached loads, so
 // all but the first find the rows in L2 or the Infinity Cache.
-// DUAL: fused GDA decode step, as in sdpa_mfma_f16_kernel: head h < G of a
+// DUAL: fused GDA decode step, as in sdpa_mfma_kernel: head h < G of a
 // column scores against k, head G (the noise head) against k2.
 // NB: column blocks per wave.  Block bb holds heads bb*GC .. bb*GC+GC-1 of
 // the workgroup's NB*GC; the K and V codes of a tile are unpacked once and
@@ -291,7 +291,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   int max_lim = 0;
   for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
   // Rows are dealt to the splits in blocks of NW 16-row tiles, round robin,
-  // as in sdpa_mfma_f16_kernel: tile k of wave w in split s is tile
+  // as in sdpa_mfma_kernel: tile k of wave w in split s is tile
   // (k * nsplit + s) * NW + w of the KV head.  The resources cover rows
   // [0, max_lim) of the KV head (scales: whole 4-row groups, inside the
   // cache since kv_cap % 4 == 0); rows past them read 0.

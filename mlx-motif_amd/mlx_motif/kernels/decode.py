@@ -8,8 +8,8 @@ The reference runs this as three kernel calls (DUAL_V path of
     attn_noise = sdpa_dual_v(q2, k2, v1, v2, scale, kv_len=kv_seq)
     out = gda_post_split(attn_origin, attn_noise, subln.weight, lam, lambda_init, gr, eps)
 
-``gda_decode_attention`` returns the same ``out``.  On the fp16 cache at
-head_dim 128, ``motif_gda_decode`` serves both passes from one attention
+``gda_decode_attention`` returns the same ``out``.  On the fp16 or bf16 cache
+at head_dim 128, ``motif_gda_decode`` serves both passes from one attention
 launch that reads each KV head's k1, k2, v1 and v2 rows once (the separate
 calls read v1 and v2 twice), and applies the epilogue in the split merge.
 Other shapes compose the separate native calls inside the library.

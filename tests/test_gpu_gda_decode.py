@@ -4,9 +4,9 @@ sdpa_dual_v for the origin heads, sdpa_dual_v for the noise heads, both
 returned in the activation dtype, then gda_post_split), and against the
 separately validated native calls.
 
-The fused path runs for fp16 at head_dim 128 (columns G + 1 = 2 .. 16 per KV
-head, both the 8-wave and the 4-wave variants); bf16, fp32, other head dims
-and mfma=0 take the composed path inside the library.
+The fused path runs for fp16 and bf16 at head_dim 128 (columns G + 1 = 2 ..
+16 per KV head, both the 8-wave and the 4-wave variants); fp32, other head
+dims and mfma=0 take the composed path inside the library.
 
 Bar: the attention outputs carry the dual-V kernels' own bar (max |o -
 o_exact| <= 2e-3 for fp16, 1e-2 bf16, 1e-5 fp32; tests/test_gpu_sdpa.py),
@@ -111,7 +111,15 @@ def test_fused_decode_kv_len_zero(gpu, rng):
     assert not torch_to_np(y).any()
 
 
-@pytest.mark.parametrize("D,tag", [(64, "f16"), (128, "bf16"), (128, "f32"), (256, "f16")])
+@pytest.mark.parametrize("kv_len,gr", [(1, 4), (300, 4), (3204, 4), (200, 15), (200, 1)])
+def test_fused_decode_bf16(gpu, rng, kv_len, gr):
+    """The bf16 cache on the bf16 matrix-core kernel (p rounded to bf16)."""
+    cap = (kv_len + 255) // 256 * 256
+    excess, *_ = _run(gpu, rng, 1, 8 if gr == 4 else 2, gr, cap, kv_len, 128, "bf16")
+    assert excess <= 0, f"bf16 kv_len={kv_len} gr={gr}: exceeds the bar by {excess:.3e}"
+
+
+@pytest.mark.parametrize("D,tag", [(64, "f16"), (64, "bf16"), (128, "f32"), (256, "f16")])
 def test_composed_path_other_shapes(gpu, rng, D, tag):
     excess, *_ = _run(gpu, rng, 1, 4, 4, 256, 150, D, tag)
     assert excess <= 0, f"D={D} {tag}: exceeds the bar by {excess:.3e}"
@@ -259,7 +267,8 @@ def _append_inputs(gpu, B, Hkv, gr, cap, D, dt, seed):
     (2, 3, 1, 301, 301, 128, "f16"),     # 2 columns, capacity not a multiple of 16
     (1, 2, 15, 512, 385, 128, "f16"),    # 16 columns: the 4-wave kernel
     (1, 4, 4, 256, 150, 64, "f16"),      # composed: head_dim 64
-    (1, 4, 4, 256, 150, 128, "bf16"),    # composed: bf16
+    (1, 4, 4, 256, 150, 128, "bf16"),    # bf16 kernel
+    (1, 4, 4, 256, 150, 128, "f32"),     # composed: fp32
 ])
 def test_append_writes_row_then_attends(gpu, B, Hkv, gr, cap, kv_len, D, tag):
     """``new_kv`` stores the token's rows at row kv_len - 1 of each slot

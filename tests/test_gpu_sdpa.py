@@ -225,6 +225,26 @@ def test_valu_formulation_matches_oracle(gpu, rng, valu_only, B, Hq, Hkv, cap, k
     assert err <= 2e-3, f"{(B, Hq, Hkv, cap, kv_len)}: {err:.3e}"
 
 
+@pytest.mark.parametrize("kv_len,cap", [(4000, 4096), (16000, 16128)])
+def test_bf16_matrix_core_kernel_matches_oracle_and_valu(gpu, rng, kv_len, cap):
+    """bf16 cache at head_dim 128 (12.7B heads): the bf16 matrix-core kernel
+    (softmax weights rounded to bf16 for the MFMAs) against the oracle and
+    against the VALU formulation."""
+    from mlx_motif import _native
+
+    out = []
+    for mfma in (1, 0):
+        _native.set_tuning("mfma", mfma)
+        try:
+            out.append(_run(gpu, np.random.default_rng(kv_len), 1, 32, 8, cap, kv_len, 128,
+                            "bf16"))
+        finally:
+            _native.set_tuning("mfma", 1)
+    (e1, y1, _), (e0, y0, _) = out
+    assert e1 <= TOL["bf16"] and e0 <= TOL["bf16"], (e1, e0)
+    assert np.max(np.abs(torch_to_np(y1) - torch_to_np(y0))) <= TOL["bf16"]
+
+
 def test_mfma_and_valu_formulations_agree(gpu, rng):
     """Same inputs through both formulations (fp16, head_dim 128, GQA 4)."""
     from mlx_motif import _native
