@@ -109,7 +109,7 @@ int motif_sdpa_dual_v_q(const void* q,
  * the reference has no kernel for it.
  * The _q variant reads the packed cache like motif_sdpa_dual_v_q (the
  * reference dequantises through cache.py:448-465 first).
- * With an fp16 cache at D = 128 and >= 64 virtual heads (query heads x rows)
+ * With an fp16 or bf16 cache at D = 128 and >= 64 virtual heads (query heads x rows)
  * per KV head -- a prefill chunk or a long slab -- the call runs the kernel
  * whose workgroups share each K/V tile through LDS among up to 128 virtual
  * heads; motif_sdpa_workspace_bytes() covers its row splits.

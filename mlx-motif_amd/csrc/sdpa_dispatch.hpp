@@ -35,8 +35,8 @@ int launch_gda_decode_q_f16(const SdpaArgs& a, int bits, int gc, int nblocks, hi
 int launch_gda_decode_q_bf16(const SdpaArgs& a, int bits, int gc, int nblocks, hipStream_t s);
 int launch_gda_decode_q_f32(const SdpaArgs& a, int bits, int gc, int nblocks, hipStream_t s);
 
-// Multi-row attention with LDS-shared K/V tiles; only the f16 instance has
-// a kernel (head_dim 128).
+// Multi-row attention with LDS-shared K/V tiles; the f16 and bf16 instances
+// have a kernel (head_dim 128).
 int launch_sdpa_prefill_f16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
 int launch_sdpa_prefill_bf16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
 int launch_sdpa_prefill_f32(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);

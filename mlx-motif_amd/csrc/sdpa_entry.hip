@@ -102,7 +102,8 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // Many virtual heads per KV head (a prefill chunk or a long verify slab):
   // the kernel with LDS-shared K/V tiles reads the cache once per block of
   // up to 128 heads instead of once per 8.
-  if (dtype == MOTIF_F16 && D == 128 && tuning().mfma && a.GV >= kPrefillMinHeads &&
+  if ((dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
+      a.GV >= kPrefillMinHeads &&
       aligned(q, 16) && aligned(y, 16) && aligned(k, 16) && aligned(v1, 16) &&
       aligned(v2, 16)) {
     const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
@@ -124,7 +125,9 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
       a.part_o = (float*)(w + cbytes);
       a.part_ml = (float*)(w + cbytes + obytes);
     }
-    rc = launch_sdpa_prefill_f16(a, pp.waves, sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit), s);
+    const int nblocks = sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit);
+    rc = dtype == MOTIF_F16 ? launch_sdpa_prefill_f16(a, pp.waves, nblocks, s)
+                            : launch_sdpa_prefill_bf16(a, pp.waves, nblocks, s);
     return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
   }
   switch (dtype) {

@@ -43,14 +43,15 @@ __device__ inline void lds_copy16_rsrc(__amdgpu_buffer_rsrc_t r, unsigned voff, 
 __device__ inline unsigned lds_byte_addr(const void* p) {
   return (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
-// 4 fp16 values through ds_read_b64_tr_b16 (gfx950) from an 8-byte aligned
-// LDS address: within each 16-lane group, lane i receives element i % 4 of
-// the 8 bytes addressed by lane 4*k + i/4 in slot k (k = 0..3).
-__device__ inline half4_t lds_read_tr16(const void* p) {
+// 4 16-bit values through ds_read_b64_tr_b16 (gfx950) from an 8-byte
+// aligned LDS address: within each 16-lane group, lane i receives element
+// i % 4 of the 8 bytes addressed by lane 4*k + i/4 in slot k (k = 0..3).
+// Returned as their 64 bits (slot k in bits 16k .. 16k + 15).
+__device__ inline uint2 lds_read_tr16(const void* p) {
   typedef short short4_t __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) short4_t* lds_s4_ptr;
   const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4_ptr)(p));
-  return __builtin_bit_cast(half4_t, v);
+  return __builtin_bit_cast(uint2, v);
 }
 
 // Waits on this wave's outstanding vector memory operations (at most N
@@ -92,9 +93,12 @@ __device__ inline bool prefill_block_coords(const SdpaArgs& a, int bid, int& qbl
 
 // The ring's LDS holds one workgroup per CU: two waves per SIMD at 8 waves,
 // one at 4.
-template <int NW, int NS = kPrefillStages>
+// T: half_t (fp16 cache) or bf16_t (bf16 cache, bf16 matrix cores).
+template <typename T, int NW, int NS = kPrefillStages>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
-sdpa_prefill_f16_kernel(SdpaArgs a) {
+sdpa_prefill_kernel(SdpaArgs a) {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
   constexpr int D = 128;
   constexpr int TR = kPrefillTileRows;
   const int lane = threadIdx.x & 63;
@@ -119,13 +123,13 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds its column's
   // channels 32*s + 8*blk .. +7 for k-step s.
-  half8_t qb[4];
+  V8 qb[4];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? vh : 0)) * D + 8 * blk;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
-      qb[s] = __builtin_bit_cast(half8_t, w);
+      qb[s] = __builtin_bit_cast(V8, w);
     }
     // q is waited for here, before the first tile copies are issued: the
     // compiler's own wait would otherwise sit inside the tile loop and, as
@@ -171,8 +175,8 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
   }
   accl = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = kNegSentinel;
-  const half8_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
-                        (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+  const typename Op::S one = Op::from_f32(1.f);
+  const V8 ones = {one, one, one, one, one, one, one, one};
 
   // One 32-row tile from ring stage st: rows t0 + 16*h + 4*blk + r hold
   // k index 8*blk + 4*h + r of the PV products (as in the decode kernel).
@@ -187,9 +191,9 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int kr = 16 * h + col;
-        const half8_t ka = __builtin_bit_cast(
-            half8_t, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
-        sacc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[s], sacc[h], 0, 0, 0);
+        const V8 ka = __builtin_bit_cast(
+            V8, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
+        sacc[h] = Op::mma(ka, qb[s], sacc[h]);
       }
     }
     float sc[8];
@@ -217,10 +221,10 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
       accl *= fac;
       m_run = m_new;
     }
-    half8_t pb;
+    V8 pb;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      pb[j] = (_Float16)(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+      pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
 
     // V^T fragments straight from the ring with transposing LDS reads
     // (ds_read_b64_tr_b16).  In the 16-lane group of lanes with one blk,
@@ -234,7 +238,7 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
     const int qq = col & 3;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      half4_t f1[2], f2[2];
+      uint2 f1[2], f2[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int vr = 16 * h + 4 * blk + jj;
@@ -242,14 +246,12 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
         f1[h] = lds_read_tr16(&V1t[o]);
         f2[h] = lds_read_tr16(&V2t[o]);
       }
-      const half8_t a1 = half8_t{f1[0][0], f1[0][1], f1[0][2], f1[0][3],
-                                 f1[1][0], f1[1][1], f1[1][2], f1[1][3]};
-      const half8_t a2 = half8_t{f2[0][0], f2[0][1], f2[0][2], f2[0][3],
-                                 f2[1][0], f2[1][1], f2[1][2], f2[1][3]};
-      acc1[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, pb, acc1[j], 0, 0, 0);
-      acc2[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, pb, acc2[j], 0, 0, 0);
+      const V8 a1 = __builtin_bit_cast(V8, make_uint4(f1[0].x, f1[0].y, f1[1].x, f1[1].y));
+      const V8 a2 = __builtin_bit_cast(V8, make_uint4(f2[0].x, f2[0].y, f2[1].x, f2[1].y));
+      acc1[j] = Op::mma(a1, pb, acc1[j]);
+      acc2[j] = Op::mma(a2, pb, acc2[j]);
     }
-    accl = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb, accl, 0, 0, 0);
+    accl = Op::mma(ones, pb, accl);
   };
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
@@ -293,10 +295,10 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
       for (int t = 0; t < 4; ++t) {
         const int j = 2 * p + t / 2;
         const int r = 2 * (t % 2);
-        const half2_t x1 = half2_t{(_Float16)(acc1[j][r] * inv), (_Float16)(acc1[j][r + 1] * inv)};
-        const half2_t x2 = half2_t{(_Float16)(acc2[j][r] * inv), (_Float16)(acc2[j][r + 1] * inv)};
-        w1[t] = __builtin_bit_cast(uint32_t, x1);
-        w2[t] = __builtin_bit_cast(uint32_t, x2);
+        w1[t] = (uint32_t)Elem<T>::from_f32(acc1[j][r] * inv) |
+                ((uint32_t)Elem<T>::from_f32(acc1[j][r + 1] * inv) << 16);
+        w2[t] = (uint32_t)Elem<T>::from_f32(acc2[j][r] * inv) |
+                ((uint32_t)Elem<T>::from_f32(acc2[j][r + 1] * inv) << 16);
       }
       *reinterpret_cast<uint4*>(yp + 8 * p) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
       *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
@@ -314,11 +316,12 @@ sdpa_prefill_f16_kernel(SdpaArgs a) {
   }
 }
 
-inline int launch_prefill_kernel_f16(const SdpaArgs& a, int waves, int nblocks, hipStream_t st) {
+template <typename T>
+inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int nblocks, hipStream_t st) {
   if (waves == 8) {
-    hipLaunchKernelGGL((sdpa_prefill_f16_kernel<8>), dim3(nblocks), dim3(512), 0, st, a);
+    hipLaunchKernelGGL((sdpa_prefill_kernel<T, 8>), dim3(nblocks), dim3(512), 0, st, a);
   } else {
-    hipLaunchKernelGGL((sdpa_prefill_f16_kernel<4>), dim3(nblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((sdpa_prefill_kernel<T, 4>), dim3(nblocks), dim3(256), 0, st, a);
   }
   return check_launch("sdpa_dual_v_rows (prefill)");
 }

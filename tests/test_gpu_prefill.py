@@ -1,9 +1,10 @@
-"""Parity of the multi-row kernel with LDS-shared K/V tiles (fp16 cache,
-head_dim 128), which ``motif_sdpa_dual_v_rows`` uses once a KV head has at
+"""Parity of the multi-row kernel with LDS-shared K/V tiles (fp16 and bf16
+caches, head_dim 128), which ``motif_sdpa_dual_v_rows`` uses once a KV head has at
 least 64 virtual heads (query heads x query rows): chunked prefill and long
 verify slabs.  Against the oracle with the bottom-right causal mask of the
 multi-row fallback (model.py:769-807) or no mask; max |gpu - oracle| <= 2e-3
-(fp32 accumulation, fp16 output).
+for fp16 (fp32 accumulation, fp16 output) and 1e-2 for bf16 (the softmax
+weights enter the bf16 matrix cores rounded to bf16; bf16 output).
 
 Cases: query blocks of 4 and 8 waves, row splits with the merge launch (few
 query blocks) and without (many), causal rows that see no key (kv_len < S),
@@ -22,20 +23,21 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal, poison=False, scale_qk=1.0):
+def _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal, poison=False, scale_qk=1.0, tag="f16"):
     import torch
 
+    from conftest import torch_dtype
     from mlx_motif.kernels import sdpa_dual_v_rows
 
     D = 128
-    q = randn(rng, (B, Hq, S, D), "f16", scale_qk)
-    k, v1, v2 = (randn(rng, (B, Hkv, cap, D), "f16") for _ in range(3))
+    q = randn(rng, (B, Hq, S, D), tag, scale_qk)
+    k, v1, v2 = (randn(rng, (B, Hkv, cap, D), tag) for _ in range(3))
     if poison and kv_len < cap:
         for t in (k, v1, v2):
             t[:, :, kv_len:] = 1e4
-    T = lambda a: np_to_torch(a, torch.float16, gpu)  # noqa: E731
-    print(f"prefill B={B} Hq={Hq} Hkv={Hkv} S={S} cap={cap} kv_len={kv_len} causal={causal}",
-          flush=True)
+    T = lambda a: np_to_torch(a, torch_dtype(tag), gpu)  # noqa: E731
+    print(f"prefill B={B} Hq={Hq} Hkv={Hkv} S={S} cap={cap} kv_len={kv_len} causal={causal} "
+          f"{tag}", flush=True)
     y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(D), kv_len=kv_len, causal=causal)
     torch.cuda.synchronize()
     assert y.shape == (B, Hq, S, 2 * D)
@@ -56,6 +58,16 @@ def _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal, poison=False, scale_qk=1.
 def test_prefill_matches_oracle(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal):
     err, *_ = _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, causal)
     assert err <= 2e-3, f"S={S} kv_len={kv_len} causal={causal}: {err:.3e}"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,cap,kv_len", [
+    (1, 32, 8, 16, 3328, 3204),    # 4-wave blocks, row splits
+    (1, 32, 8, 200, 1024, 1000),   # ragged last block
+    (1, 32, 8, 512, 3840, 3716),   # 8-wave blocks, the 512-row chunk
+])
+def test_prefill_bf16_matches_oracle(gpu, rng, B, Hq, Hkv, S, cap, kv_len):
+    err, *_ = _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, True, poison=True, tag="bf16")
+    assert err <= 1e-2, f"bf16 S={S} kv_len={kv_len}: {err:.3e}"
 
 
 def test_prefill_long_chunk(gpu, rng):
