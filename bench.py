@@ -487,6 +487,12 @@ def run_extra(torch, lib, dev, args):
                    time_calls(torch, calls, steps, warm), nbytes)
             del calls, keep
             torch.cuda.empty_cache()
+    # verify slab: 5 rows over an fp16 cache of 32768 rows (16 + 4 columns)
+    calls, keep = make_fp16_calls(torch, lib, dev, 6, kv_len=32768, cap=32768, s_q=5)
+    report("verify slab f16 5 rows kv32768", time_calls(torch, calls, steps, warm),
+           alg_bytes("f16", 32768, s_q=5))
+    del calls, keep
+    torch.cuda.empty_cache()
     # verify slab: 5 rows over a q8 cache of 32768 rows
     calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
     report("verify slab q8 5 rows kv32768", time_calls(torch, calls, steps, warm),

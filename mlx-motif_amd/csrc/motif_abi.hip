@@ -169,6 +169,9 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
   // VALU plans and the packed-cache matrix-core plans of each group size.
   size_t ws = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0).workspace_bytes;
   if (D == kSdpaMfmaQD) {
+    const size_t w16 =
+        plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 0, 0).workspace_bytes;
+    if (w16 > ws) ws = w16;
     for (int gs = 32; gs <= 128; gs *= 2) {
       const int nb = sdpa_q_blocks((Hkv > 0 ? Hq / Hkv : 1) * S_q, D, gs);
       const SdpaPlan p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),

@@ -86,8 +86,13 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   clear_error();
   SdpaArgs a{};
   SdpaPlan p{};
+  // The matrix-core kernel takes up to 16 virtual heads per workgroup (a
+  // verify slab's 5 rows x GQA 4 in two head chunks instead of three); the
+  // conditions are those under which the dispatch picks that kernel.
+  const bool mfma16 = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
+                      tuning().mfma && aligned(q, 16) && kv_len <= kMfmaMaxRows;
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes, sdpa_gc_max(D), 0, 0);
+                       ws_bytes, mfma16 ? kSdpaMfmaGcMax : sdpa_gc_max(D), 0, 0);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
   const int al = sdpa_fp_align(dtype, D);

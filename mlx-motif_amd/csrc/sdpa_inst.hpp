@@ -18,7 +18,7 @@ int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan
   const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
                 std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    if (D == 128 && tuning().mfma && p.gc <= 8 && ((uintptr_t)a.q & 15u) == 0 &&
+    if (D == 128 && tuning().mfma && p.gc <= kSdpaMfmaGcMax && ((uintptr_t)a.q & 15u) == 0 &&
         a.kv_len <= kMfmaMaxRows)
       return launch_sdpa_mfma_16<MOTIF_ELEM>(a, p.gc, p.waves, nblocks, s);
   }

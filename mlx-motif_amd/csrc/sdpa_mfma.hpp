@@ -333,8 +333,8 @@ sdpa_mfma_kernel(SdpaArgs a) {
   wg_epilogue<T, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
-// 16-bit cache (T = half_t or bf16_t), head_dim 128, <= 8 virtual heads per
-// workgroup.
+// 16-bit cache (T = half_t or bf16_t), head_dim 128, <= 16 virtual heads per
+// workgroup (16: 4 waves, for the cross-wave LDS merge).
 template <typename T>
 inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks,
                                hipStream_t stream) {
@@ -362,6 +362,9 @@ inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks
       break;
     case 8:
       hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      break;
+    case 16:
+      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 16, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       break;
     default:
       set_error("sdpa_dual_v: no MFMA variant for %d heads per workgroup", gc);

@@ -127,6 +127,10 @@ constexpr int kSdpaMfmaQWgsPerCu = 1;
 // Largest head chunk compiled for head dim D (register budget).
 inline int sdpa_gc_max(int D) { return D <= 128 ? 8 : 4; }
 
+// Largest head chunk of the fp16/bf16 matrix-core kernel (head_dim 128):
+// the 16 MFMA columns, with 4-wave workgroups for the cross-wave LDS merge.
+constexpr int kSdpaMfmaGcMax = 16;
+
 // Largest head chunk for the packed cache's matrix-core kernel: heads times
 // scale groups share the 16 MFMA columns.
 inline int sdpa_gc_max_q(int D, int group_size) {

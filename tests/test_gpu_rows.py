@@ -40,6 +40,27 @@ def test_rows_fp16(gpu, rng, B, Hq, Hkv, S, cap, kv_len, d, causal):
     assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
 
 
+@pytest.mark.parametrize("tag,S,Hq,cap,kv_len", [
+    ("f16", 4, 32, 1024, 1000),    # 16 virtual heads per KV head: one 16-column chunk
+    ("f16", 5, 32, 32768, 32768),  # the 5-row verify slab at 32k rows: chunks of 16 + 4
+    ("bf16", 5, 32, 512, 300),     # bf16 matrix cores, 16 + 4
+    ("bf16", 3, 40, 640, 600),     # GQA 5 x 3 rows = 15 columns
+])
+def test_rows_sixteen_column_chunks(gpu, rng, tag, S, Hq, cap, kv_len):
+    """fp16/bf16 slabs at head_dim 128 run the matrix-core kernel with up to
+    16 virtual heads per workgroup."""
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    q = randn(rng, (1, Hq, S, 128), tag)
+    k, v1, v2 = (randn(rng, (1, 8, cap, 128), tag) for _ in range(3))
+    T = lambda a: np_to_torch(a, torch_dtype(tag), gpu)  # noqa: E731
+    print(f"rows {tag} S={S} Hq={Hq} kv_len={kv_len}", flush=True)
+    y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=kv_len, causal=True)
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128), kv_len, causal=True)
+    err = float(np.max(np.abs(torch_to_np(y) - ref)))
+    assert err <= (2e-3 if tag == "f16" else 1e-2), f"{tag} S={S}: {err:.3e}"
+
+
 def test_rows_single_row_equals_decode(gpu, rng):
     """S_q = 1 with the causal mask is the decode kernel's computation."""
     from mlx_motif.kernels import sdpa_dual_v, sdpa_dual_v_rows
