@@ -530,6 +530,17 @@ def run_extra(torch, lib, dev, args):
     report("polynorm [3204,13824]", time_calls(torch, calls, steps, warm),
            2 * 3204 * 13824 * 2)
     del xs, calls
+    # RoPE + head split + 4-slot write of a 512-row prefill chunk (12.7B
+    # heads: 40 q, 16 k, 16 v heads of 128) into an fp16 cache at offset 3204
+    from mlx_motif.kernels import rope_split4
+    qp = torch.randn((1, 512, 40 * 128), device=dev).half()
+    kp = torch.randn((1, 512, 16 * 128), device=dev).half()
+    vp = torch.randn((1, 512, 16 * 128), device=dev).half()
+    slots = [torch.zeros((1, 8, 3840, 128), device=dev).half() for _ in range(4)]
+    report("rope_split4 512 rows into the 4-slot cache",
+           time_calls(torch, [lambda: rope_split4(qp, kp, vp, 8, 4, 8, 1, 3204, caches=slots)],
+                      steps, warm), 2 * 512 * 72 * 128 * 2)
+    del qp, kp, vp, slots
     # decode write of one token into four q4 slots at row 15999
     cache = MotifGroupedQuantizedKVCache(group_size=64, bits=4)
     big = torch.randn((1, 8, 15999, 128), device=dev).half()

@@ -159,6 +159,31 @@ int motif_sdpa_dual_v_q4_verify(const void* q,
                                 size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ *
+ * RoPE, head split and 4-slot write of one attention step in one launch.
+ * Replaces, for a layer's step, the two self.rope calls on q and k
+ * (src/mlx_motif/model.py:590-594; initialize_rope with traditional=False
+ * and no scaling, i.e. channel pairs (i, i + D/2) rotated by
+ * (pos0 + s) * theta^(-2i/D)), the k1/k2 and v1/v2 split with
+ * update_and_fetch_4 (model.py:620-629, cache.py:337) and the q1/q2 split
+ * (model.py:669-679).
+ *   q (B, S, q_groups*(gr+1)*D), k (B, S, k_groups*(kr+1)*D),
+ *   v (B, S, 2*k_groups*D)                            projection outputs
+ *   q1 (B, q_groups*gr, S, D), q2 (B, q_groups, S, D)  roped, rows 0..S-1
+ *   k1 (B, k_groups*kr, cap, D), k2 (B, k_groups, cap, D) roped, and
+ *   v1, v2 (B, k_groups, cap, D): rows row0 .. row0 + S - 1.
+ * q head h of group g is h = g*(gr+1) + j (j < gr: q1, j == gr: q2), or with
+ * origin_first the q1 heads first; k likewise with kr; v head 2n -> v1[n],
+ * 2n+1 -> v2[n].  With cap/row0 the cache capacity/offset the rows go
+ * straight into the 4-slot fp cache; with cap = S, row0 = 0 they are plain
+ * (B, H, S, D) tensors (e.g. for motif_quant_write4 or the *_append entries).
+ * fp32 math, outputs rounded once to dtype.  D % 32 == 0, D <= 256.
+ * ------------------------------------------------------------------------ */
+int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, void* q2, void* k1,
+                      void* k2, void* v1, void* v2, int dtype, int B, int S, int q_groups, int gr,
+                      int k_groups, int kr, int D, int cap, int row0, int pos0, float theta,
+                      int origin_first, void* stream);
+
+/* ------------------------------------------------------------------------ *
  * MLX affine quantisation (mx.quantize, mode "affine") of `rows` rows of D
  * values: data (rows, D*bits/32) uint32, scales/biases (rows, D/group_size)
  * in dtype.  The reference calls mx.quantize at cache.py:498 and

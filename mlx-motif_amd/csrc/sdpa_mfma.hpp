@@ -103,9 +103,11 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
 // KV head (scores from k), column G its noise head (scores from k2); both
 // share the V1/V2 rows, and the partials go to the fused merge launch.
 // T: half_t (fp16 cache, v_mfma_f32_16x16x32_f16) or bf16_t (bf16 cache,
-// v_mfma_f32_16x16x32_bf16).
+// v_mfma_f32_16x16x32_bf16).  The 16-column single-pass variant keeps the
+// in-kernel merge's LDS (104 KB): one workgroup, one wave per SIMD, per CU.
 template <typename T, int GC, int NW, int U, bool DUAL = false>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(GC == 16 && !DUAL ? 1 : 2)))
 sdpa_mfma_kernel(SdpaArgs a) {
   using Op = MfmaOp<T>;
   using V8 = typename Op::V8;

@@ -11,6 +11,8 @@ import) routes every wrapper to its reference.
                    gda_post_split in one call; the reference composes three)
     mlp.py       — polynorm, _dequant_probe (test helper)
     quant.py     — quantize / dequantize (MLX affine format of the KV cache)
+    rope.py      — rope_split4 (RoPE + q/k/v head split + 4-slot cache write
+                   in one launch; the reference uses rope() and reshapes)
 """
 
 from .attention import (
@@ -39,6 +41,7 @@ from .mlp import (
     polynorm_reference,
 )
 from .quant import dequantize, dequantize_reference, quantize, quantize_reference
+from .rope import rope_split4, rope_split4_reference
 
 __all__ = [
     "polynorm",
@@ -61,4 +64,6 @@ __all__ = [
     "quantize_reference",
     "dequantize",
     "dequantize_reference",
+    "rope_split4",
+    "rope_split4_reference",
 ]

@@ -47,6 +47,14 @@ How each function is pinned (tests/test_oracle.py):
   polynorm           the reference's only numeric golden vector
                      (tests/fixtures/motif_parity_cases.json,
                      component_checks[0]).
+  rope / rope_split4 the rotation's closed form on D = 2 (angle = position),
+                     position 0 is the identity, every channel pair keeps
+                     its norm, and q(m).k(n) depends on m - n only; the split
+                     is checked against an explicit per-head index loop.
+                     The exact cos/sin and angle rounding of mlx_lm's
+                     initialize_rope / mx.fast.rope (not in this tree, not
+                     importable here) are PARITY UNPINNED: the restatement
+                     is the textbook non-traditional RoPE in float64.
 """
 
 from __future__ import annotations
@@ -293,3 +301,49 @@ def lambda_full(lq1, lk1, lq2, lk2, lam_init: float) -> float:
     l1 = np.exp(np.sum(np.asarray(lq1, np.float64) * np.asarray(lk1, np.float64)))
     l2 = np.exp(np.sum(np.asarray(lq2, np.float64) * np.asarray(lk2, np.float64)))
     return float(l1 - l2 + lam_init)
+
+
+# ----------------------------------------------------------------- RoPE ---
+
+
+def rope(x, pos0: int, theta: float = 10000.0) -> np.ndarray:
+    """Non-traditional RoPE (model.py:413-419: initialize_rope(head_dim,
+    traditional=False, no scaling); applied at model.py:590-594) on x
+    (B, S, H, D) in float64: channel pairs (i, i + D/2) rotated by
+    (pos0 + s) * theta^(-2i/D)."""
+    x = np.asarray(x, np.float64)
+    B, S, H, D = x.shape
+    half = D // 2
+    inv = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / D)
+    ang = (pos0 + np.arange(S, dtype=np.float64))[:, None] * inv[None, :]  # (S, half)
+    c = np.cos(ang)[None, :, None, :]
+    s_ = np.sin(ang)[None, :, None, :]
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s_, x2 * c + x1 * s_], axis=-1)
+
+
+def rope_split4(q, k, v, q_groups: int, gr: int, k_groups: int, kr: int, pos0: int,
+                theta: float = 10000.0, origin_first: bool = False):
+    """model.py:580-594 (reshape to heads, rope q and k), 620-629 (k1/k2 and
+    v1/v2 split of the 4-slot cache write) and 669-679 (q1/q2 split).  q (B,
+    S, HQ*D), k (B, S, HK*D), v (B, S, 2*k_groups*D).  Returns float64
+    (q1, q2, k1, k2, v1, v2), each (B, H, S, D)."""
+    q = np.asarray(q, np.float64)
+    B, S, _ = q.shape
+    HQ = q_groups * (gr + 1)
+    HK = k_groups * (kr + 1)
+    D = q.shape[-1] // HQ
+    qr = rope(q.reshape(B, S, HQ, D), pos0, theta).transpose(0, 2, 1, 3)  # (B, HQ, S, D)
+    kr_ = rope(np.asarray(k, np.float64).reshape(B, S, HK, D), pos0, theta).transpose(0, 2, 1, 3)
+    vv = np.asarray(v, np.float64).reshape(B, S, 2 * k_groups, D).transpose(0, 2, 1, 3)
+    if origin_first:
+        q1, q2 = qr[:, : q_groups * gr], qr[:, q_groups * gr:]
+    else:
+        q_ = qr.reshape(B, q_groups, gr + 1, S, D)
+        q1 = q_[:, :, :gr].reshape(B, q_groups * gr, S, D)
+        q2 = q_[:, :, gr:].reshape(B, q_groups, S, D)
+    k_ = kr_.reshape(B, k_groups, kr + 1, S, D)
+    k1 = k_[:, :, :kr].reshape(B, k_groups * kr, S, D)
+    k2 = k_[:, :, kr:].reshape(B, k_groups, S, D)
+    v_ = vv.reshape(B, k_groups, 2, S, D)
+    return q1, q2, k1, k2, v_[:, :, 0], v_[:, :, 1]

@@ -198,6 +198,31 @@ def test_decode_append_contract(enabled, rng):
                                new_kv=rows)
 
 
+def test_disabled_rope_split4_reference_matches_oracle(disabled, rng):
+    qg, gr, kg, kr, D, B, S = 2, 4, 2, 1, 64, 1, 6
+    q = _t(rng, (B, S, qg * (gr + 1) * D), torch.float32)
+    k = _t(rng, (B, S, kg * (kr + 1) * D), torch.float32)
+    v = _t(rng, (B, S, 2 * kg * D), torch.float32)
+    caches = [torch.full((B, kg, 32, D), 7.0) for _ in range(4)]
+    out = K.rope_split4(q, k, v, qg, gr, kg, kr, 20, caches=caches)
+    ref = O.rope_split4(q.numpy(), k.numpy(), v.numpy(), qg, gr, kg, kr, 20)
+    np.testing.assert_allclose(out[0].numpy(), ref[0], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(out[1].numpy(), ref[1], rtol=1e-5, atol=1e-5)
+    for c, r in zip(caches, ref[2:]):
+        np.testing.assert_allclose(c[:, :, 20:26].numpy(), r, rtol=1e-5, atol=1e-5)
+        assert (c[:, :, :20] == 7.0).all() and (c[:, :, 26:] == 7.0).all()
+
+
+def test_rope_split4_contract(enabled, rng):
+    q, k, v = _t(rng, (1, 2, 5 * 64)), _t(rng, (1, 2, 2 * 64)), _t(rng, (1, 2, 2 * 64))
+    with pytest.raises(AssertionError, match="q width"):
+        K.rope_split4(q[..., :-1], k, v, 1, 4, 1, 1, 0)
+    with pytest.raises(AssertionError, match="k must be"):
+        K.rope_split4(q, k[..., :-64], v, 1, 4, 1, 1, 0)
+    with pytest.raises(AssertionError, match="v must be"):
+        K.rope_split4(q, k, v[..., :-64], 1, 4, 1, 1, 0)
+
+
 def test_polynorm_zero_rows_returns_zeros(enabled):
     x = torch.zeros((0, 16))
     assert K.polynorm(x, torch.ones(3), torch.zeros(1)).shape == (0, 16)

@@ -299,3 +299,61 @@ def test_lambda_formulas():
     assert abs(O.lambda_init(1000) - 0.8) < 1e-12
     lq1, lk1, lq2, lk2 = (np.full(4, 0.1), np.full(4, 0.2), np.zeros(4), np.zeros(4))
     assert abs(O.lambda_full(lq1, lk1, lq2, lk2, 0.2) - (math.exp(0.08) - 1 + 0.2)) < 1e-15
+
+
+# ----------------------------------------------------------------- RoPE ---
+def test_rope_closed_form_on_two_channels(rng):
+    """D = 2: one pair rotated by angle = position (theta^0 = 1)."""
+    x = rng.standard_normal((1, 5, 3, 2))
+    y = O.rope(x, 7, 10000.0)
+    ang = 7 + np.arange(5)
+    c, s = np.cos(ang)[None, :, None], np.sin(ang)[None, :, None]
+    np.testing.assert_allclose(y[..., 0], x[..., 0] * c - x[..., 1] * s, atol=1e-12)
+    np.testing.assert_allclose(y[..., 1], x[..., 1] * c + x[..., 0] * s, atol=1e-12)
+
+
+def test_rope_identity_norms_and_relative_position(rng):
+    D = 128
+    x = rng.standard_normal((2, 1, 4, D))
+    np.testing.assert_array_equal(O.rope(x, 0), x)  # position 0: identity
+    y = O.rope(x, 1234)
+    half = D // 2
+    n_x = x[..., :half] ** 2 + x[..., half:] ** 2
+    n_y = y[..., :half] ** 2 + y[..., half:] ** 2
+    np.testing.assert_allclose(n_y, n_x, rtol=1e-12)  # each pair keeps its norm
+    q, k = rng.standard_normal((1, 1, 1, D)), rng.standard_normal((1, 1, 1, D))
+    d1 = np.sum(O.rope(q, 500) * O.rope(k, 480))
+    d2 = np.sum(O.rope(q, 9020) * O.rope(k, 9000))
+    assert abs(d1 - d2) < 1e-9 * (1 + abs(d1))  # depends on m - n only
+    # the frequency of pair i is theta^(-2i/D): pair 1 at position 1
+    e = np.zeros((1, 1, 1, D))
+    e[..., 1] = 1.0
+    r = O.rope(e, 1)
+    w = 10000.0 ** (-2.0 / D)
+    np.testing.assert_allclose([r[0, 0, 0, 1], r[0, 0, 0, half + 1]], [np.cos(w), np.sin(w)])
+
+
+def test_rope_split4_head_mapping_explicit_loop(rng):
+    """The split against a per-head index loop (model.py:620-629, 669-679)."""
+    B, S, qg, gr, kg, kr, D = 2, 3, 2, 3, 2, 1, 32
+    q = rng.standard_normal((B, S, qg * (gr + 1) * D))
+    k = rng.standard_normal((B, S, kg * (kr + 1) * D))
+    v = rng.standard_normal((B, S, 2 * kg * D))
+    q1, q2, k1, k2, v1, v2 = O.rope_split4(q, k, v, qg, gr, kg, kr, 5)
+    qr = O.rope(q.reshape(B, S, -1, D), 5)
+    kr_ = O.rope(k.reshape(B, S, -1, D), 5)
+    vv = v.reshape(B, S, -1, D)
+    for b in range(B):
+        for s in range(S):
+            for g in range(qg):
+                for j in range(gr):
+                    np.testing.assert_array_equal(q1[b, g * gr + j, s], qr[b, s, g * (gr + 1) + j])
+                np.testing.assert_array_equal(q2[b, g, s], qr[b, s, g * (gr + 1) + gr])
+            for g in range(kg):
+                np.testing.assert_array_equal(k1[b, g, s], kr_[b, s, 2 * g])
+                np.testing.assert_array_equal(k2[b, g, s], kr_[b, s, 2 * g + 1])
+                np.testing.assert_array_equal(v1[b, g, s], vv[b, s, 2 * g])
+                np.testing.assert_array_equal(v2[b, g, s], vv[b, s, 2 * g + 1])
+    o1, o2, *_ = O.rope_split4(q, k, v, qg, gr, kg, kr, 5, origin_first=True)
+    np.testing.assert_array_equal(o1, qr.transpose(0, 2, 1, 3)[:, : qg * gr])
+    np.testing.assert_array_equal(o2, qr.transpose(0, 2, 1, 3)[:, qg * gr:])
