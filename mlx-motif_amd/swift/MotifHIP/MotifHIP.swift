@@ -234,6 +234,27 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// RoPE on q and k, the q1/q2, k1/k2, v1/v2 head split and the 4-slot
+    /// write in one launch: k1..v2 rows row0 ..< row0 + seqLen of buffers of
+    /// `capacity` rows (the cache, or capacity = seqLen, row0 = 0 for plain
+    /// tensors), positions pos0 + s.
+    public static func ropeSplit4(
+        qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
+        q1: UnsafeMutableRawPointer, q2: UnsafeMutableRawPointer,
+        k1: UnsafeMutableRawPointer, k2: UnsafeMutableRawPointer,
+        v1: UnsafeMutableRawPointer, v2: UnsafeMutableRawPointer, dtype: MotifHIPDType,
+        batch: Int, seqLen: Int, qGroups: Int, gr: Int, kGroups: Int, kRatio: Int,
+        headDim: Int, capacity: Int, row0: Int, pos0: Int, theta: Float, originFirst: Bool,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_rope_split4(qProj, kProj, vProj, q1, q2, k1, k2, v1, v2, dtype.rawValue,
+                                   Int32(batch), Int32(seqLen), Int32(qGroups), Int32(gr),
+                                   Int32(kGroups), Int32(kRatio), Int32(headDim),
+                                   Int32(capacity), Int32(row0), Int32(pos0), theta,
+                                   originFirst ? 1 : 0, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// PolyNorm over the last axis of x (rows, D).
     public static func polynorm(
         x: UnsafeRawPointer, weight: UnsafeRawPointer, bias: UnsafeRawPointer,
