@@ -530,6 +530,34 @@ def run_extra(torch, lib, dev, args):
     report("polynorm [3204,13824]", time_calls(torch, calls, steps, warm),
            2 * 3204 * 13824 * 2)
     del xs, calls
+    # a layer's whole decode attention from the projections at kv_len 16000:
+    # rope_split4 (q1/q2 roped, the token's k1/k2/v1/v2 rows into the cache)
+    # then the fused step (attention + merge/epilogue): three launches
+    from mlx_motif.kernels import gda_decode_attention, rope_split4 as _rope
+    g2 = torch.Generator(device=dev)
+    g2.manual_seed(5)
+    layers = []
+    for _ in range(6):
+        slots = [torch.randn((B, HKV, CAP, D), generator=g2, device=dev).half() for _ in range(4)]
+        layers.append(slots)
+    qp1 = torch.randn((B, 1, 40 * D), generator=g2, device=dev).half()
+    kp1 = torch.randn((B, 1, 16 * D), generator=g2, device=dev).half()
+    vp1 = torch.randn((B, 1, 16 * D), generator=g2, device=dev).half()
+    wsub = torch.rand(2 * D, generator=g2, device=dev).half()
+    lam1 = torch.tensor([0.37], dtype=torch.float32, device=dev)
+
+    def layer_step(slots):
+        def call():
+            q1, q2, *_ = _rope(qp1, kp1, vp1, 8, 4, 8, 1, KV_LEN - 1, caches=slots)
+            gda_decode_attention(q1, q2, *slots, D ** -0.5, wsub, lam1, 0.2, 4, 1e-5,
+                                 kv_len=KV_LEN)
+        return call
+
+    report("decode layer attention f16 kv16000 (rope_split4 + fused step)",
+           time_calls(torch, [layer_step(sl) for sl in layers], steps, warm),
+           decode_bytes(KV_LEN, True))
+    del layers
+    torch.cuda.empty_cache()
     # RoPE + head split + 4-slot write of a 512-row prefill chunk (12.7B
     # heads: 40 q, 16 k, 16 v heads of 128) into an fp16 cache at offset 3204
     from mlx_motif.kernels import rope_split4
