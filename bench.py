@@ -556,6 +556,15 @@ def run_extra(torch, lib, dev, args):
     report("decode layer attention f16 kv16000 (rope_split4 + fused step)",
            time_calls(torch, [layer_step(sl) for sl in layers], steps, warm),
            decode_bytes(KV_LEN, True))
+    from mlx_motif.kernels import gda_decode_attention_from_proj
+
+    def layer_proj(slots):
+        return lambda: gda_decode_attention_from_proj(qp1, kp1, vp1, *slots, D ** -0.5, wsub,
+                                                      lam1, 0.2, 4, KV_LEN - 1)
+
+    report("decode layer attention f16 kv16000 (from projections, RoPE in the step)",
+           time_calls(torch, [layer_proj(sl) for sl in layers], steps, warm),
+           decode_bytes(KV_LEN, True))
     del layers
     torch.cuda.empty_cache()
     # RoPE + head split + 4-slot write of a 512-row prefill chunk (12.7B

@@ -299,6 +299,27 @@ int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
                             int kv_len, float scale, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* The same decode step from the projection outputs, RoPE included: the
+ * layer's whole decode attention in the attention launch plus the merge.
+ * Replaces, for one decode token, the rope calls (model.py:590-594), the
+ * q/k/v head splits (model.py:620-629, 669-679), update_and_fetch_4
+ * (cache.py:337) and the three calls (model.py:749-768).
+ *   q_proj (B, 1, Hkv*(gr+1)*D): heads g*(gr+1)+j (origin j < gr, noise
+ *          j = gr), or with origin_first the Hkv*gr origin heads first
+ *   k_proj (B, 1, 2*Hkv*D): k1[g] = head 2g, k2[g] = head 2g+1 (k_ratio 1)
+ *   v_proj (B, 1, 2*Hkv*D): v1[g] = head 2g, v2[g] = head 2g+1
+ * q and the k rows are roped at position kv_len - 1 exactly as
+ * motif_rope_split4 does (same rounding), the four rows are written at row
+ * kv_len - 1, and y is what motif_rope_split4 + motif_gda_decode give, bit
+ * for bit.  fp16/bf16 cache at D = 128 with gr + 1 <= 16 only; other shapes
+ * return MOTIF_ERR_UNSUPPORTED (compose those two calls instead). */
+int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                          void* k2, void* v1, void* v2, const void* subln_w,
+                          const float* lambda_full, float one_minus_lambda_init, float eps,
+                          void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                          int kv_len, float scale, float theta, int origin_first,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
                               const void* k2_new, const void* v1_new, const void* v2_new,
                               uint32_t* k1_data, void* k1_scales, void* k1_biases,

@@ -1,0 +1,19 @@
+// Non-traditional RoPE of one channel pair (i, i + D/2), shared by the
+// rope_split4 kernel and the decode step that ropes its own inputs, so both
+// round identically: angle = pos * theta^(-2i/D) in fp32, rotation with
+// explicit fmas (no contraction left to the compiler).
+#pragma once
+
+namespace motif {
+
+__device__ inline void rope_angle(int p, int D, int pos, float log2_theta, float& cs, float& sn) {
+  const float inv_freq = exp2f(-(2.f * (float)p / (float)D) * log2_theta);
+  sincosf((float)pos * inv_freq, &sn, &cs);
+}
+
+__device__ inline void rope_rotate(float x1, float x2, float cs, float sn, float& y1, float& y2) {
+  y1 = fmaf(x1, cs, -(x2 * sn));
+  y2 = fmaf(x2, cs, x1 * sn);
+}
+
+}  // namespace motif

@@ -411,6 +411,51 @@ int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
                        scale, workspace, workspace_bytes, nk, stream);
 }
 
+int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                          void* k2, void* v1, void* v2, const void* subln_w,
+                          const float* lambda_full, float one_minus_lambda_init, float eps,
+                          void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                          int kv_len, float scale, float theta, int origin_first,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* name = "gda_decode_proj";
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+                             workspace_bytes);
+  if (rc != MOTIF_OK) return rc;
+  MOTIF_REQUIRE(q_proj && k_proj && v_proj && k1 && k2 && v1 && v2 && y && subln_w &&
+                    lambda_full,
+                "%s: null pointer", name);
+  MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the new token's row", name, kv_len);
+  MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
+                     tuning().mfma && gr + 1 <= 16 && kv_len <= kMfmaMaxRows &&
+                     aligned(q_proj, 16) && aligned(k_proj, 16) && aligned(v_proj, 16) &&
+                     aligned(k1, 16) && aligned(k2, 16) && aligned(v1, 16) && aligned(v2, 16) &&
+                     aligned(y, 8);
+  if (!fused) {
+    set_error("%s: no fused variant for this shape (dtype %d, D=%d, gr=%d); use "
+              "motif_rope_split4 and motif_gda_decode", name, dtype, D, gr);
+    return MOTIF_ERR_UNSUPPORTED;
+  }
+  SdpaArgs a = gda_decode_args(L, L.plan, q_proj, q_proj, y, B, Hkv, gr, kv_cap, kv_len, scale,
+                               subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
+  a.k = k1;
+  a.k2 = k2;
+  a.v1 = v1;
+  a.v2 = v2;
+  a.new_k1 = k_proj; a.new_k2 = k_proj; a.new_v1 = v_proj; a.new_v2 = v_proj;
+  a.append = 1;
+  a.from_proj = 1;
+  a.q_origin_first = origin_first != 0;
+  a.rope_log2_theta = log2f(theta);
+  const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+  return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks,
+                                                    (hipStream_t)stream)
+                            : launch_gda_decode_bf16(a, gda_columns(gr), nblocks,
+                                                     (hipStream_t)stream);
+}
+
 int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
                       int dtype, int B, int Hq, int Hkv, int D, int kv_cap, int kv_len,
                       float scale, void* workspace, size_t workspace_bytes, void* stream) {

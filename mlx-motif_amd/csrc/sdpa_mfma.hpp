@@ -27,6 +27,7 @@
 // the VALU kernel.
 #pragma once
 
+#include "rope_impl.hpp"
 #include "sdpa_impl.hpp"
 
 namespace motif {
@@ -88,13 +89,49 @@ __device__ inline bool append_owner(const SdpaArgs& a, int split, int wave) {
 }
 
 // 16-bit rows of 128 values: lane L copies 16 bytes (chunk L % 16) of slot
-// L / 16 (k1, k2, v1, v2) into row kv_len - 1 of KV head bk.
+// L / 16 (k1, k2, v1, v2) into row kv_len - 1 of KV head bk.  From the
+// projections (a.from_proj), the k rows are roped first: chunk c < 8 holds
+// the first halves of the pairs whose second halves are in chunk c + 8,
+// i.e. in lane L ^ 8.  Called by a whole wave.
+template <typename T>
 __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
   const int slot = lane / 16;
   const int chunk = lane % 16;
-  const void* src = slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
   const void* dst = slot == 0 ? a.k : slot == 1 ? a.k2 : slot == 2 ? a.v1 : a.v2;
-  const uint4 w = *reinterpret_cast<const uint4*>((const uint8_t*)src + bk * 256 + chunk * 16);
+  uint4 w;
+  if (!a.from_proj) {
+    const void* src =
+        slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
+    w = *reinterpret_cast<const uint4*>((const uint8_t*)src + bk * 256 + chunk * 16);
+  } else {
+    // head 2 * kvh + (slot & 1) of position b: row 2 * bk + (slot & 1)
+    const void* src = slot < 2 ? a.new_k1 : a.new_v1;
+    w = *reinterpret_cast<const uint4*>((const uint8_t*)src + (2 * bk + (slot & 1)) * 256 +
+                                        chunk * 16);
+    uint32_t x[4] = {w.x, w.y, w.z, w.w}, o[4];
+    uint32_t y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = (uint32_t)__shfl_xor((int)x[i], 8);  // partner chunk
+    const bool first = chunk < 8;
+    const int pos = a.kv_len - 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t r = 0;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint16_t mine = (uint16_t)(e ? x[i] >> 16 : x[i] & 0xFFFFu);
+        const uint16_t other = (uint16_t)(e ? o[i] >> 16 : o[i] & 0xFFFFu);
+        const float x1 = Elem<T>::to_f32(first ? mine : other);
+        const float x2 = Elem<T>::to_f32(first ? other : mine);
+        float cs, sn, y1, y2;
+        rope_angle(8 * (chunk & 7) + 2 * i + e, 128, pos, a.rope_log2_theta, cs, sn);
+        rope_rotate(x1, x2, cs, sn, y1, y2);
+        r |= (uint32_t)Elem<T>::from_f32(first ? y1 : y2) << (16 * e);
+      }
+      y[i] = slot < 2 ? r : x[i];  // v rows are copied
+    }
+    w = make_uint4(y[0], y[1], y[2], y[3]);
+  }
   *reinterpret_cast<uint4*>((uint8_t*)const_cast<void*>(dst) +
                             (bk * a.kv_cap + a.kv_len - 1) * 256 + chunk * 16) = w;
 }
@@ -143,7 +180,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
   bool owner = false;
   if constexpr (DUAL) {
     owner = append_owner<NW>(a, split, wave);
-    if (owner) append_rows_16bit(a, bk, lane);
+    if (owner) append_rows_16bit<T>(a, bk, lane);
   }
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds head col,
@@ -152,14 +189,43 @@ sdpa_mfma_kernel(SdpaArgs a) {
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
     if constexpr (DUAL) {
-      qp = col < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + col) * D
-                     : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      if (a.from_proj) {  // q_proj heads: stripe g*(G+1)+j, or origin-first
+        const int head = a.q_origin_first
+                             ? (col < a.G ? kvh * a.G + col : a.Hkv * a.G + kvh)
+                             : kvh * (a.G + 1) + (col < a.G ? col : a.G);
+        qp = (const uint16_t*)a.q + ((long)b * a.Hkv * (a.G + 1) + head) * D;
+      } else {
+        qp = col < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + col) * D
+                       : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      }
       qp += 8 * blk;
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
       qb[s] = __builtin_bit_cast(V8, w);
+    }
+    if constexpr (DUAL) {
+      if (a.from_proj) {  // RoPE at kv_len - 1: channel 32s + 8blk + j pairs with s + 2
+        // The 16 angles of a row block are the same for its 16 columns: lane
+        // (col, blk) computes angle (s, j) = (col / 8, col % 8) and the
+        // others are read from the lanes of its block.
+        float cs0, sn0;
+        rope_angle(32 * (col >> 3) + 8 * blk + (col & 7), 128, a.kv_len - 1, a.rope_log2_theta,
+                   cs0, sn0);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float cs = __shfl(cs0, 16 * blk + 8 * s + j);
+            const float sn = __shfl(sn0, 16 * blk + 8 * s + j);
+            float y1, y2;
+            rope_rotate((float)qb[s][j], (float)qb[s + 2][j], cs, sn, y1, y2);
+            qb[s][j] = Op::from_f32(y1);
+            qb[s + 2][j] = Op::from_f32(y2);
+          }
+        }
+      }
     }
   }
 

@@ -65,6 +65,15 @@ struct SdpaArgs {
   const void* new_v1;
   const void* new_v2;
   int append;
+  // Decode step from the projection outputs (from_proj != 0, with append):
+  // q is q_proj (B, 1, Hkv*(G+1)*D), heads g*(G+1)+j (origin j < G, noise
+  // j = G), or origin-first (q_origin_first); new_k1 is k_proj (B, 1,
+  // 2*Hkv*D: k1[g] = head 2g, k2[g] = 2g+1) and new_v1 v_proj (same head
+  // pairing for v1/v2).  q and the new k rows are roped at position
+  // kv_len - 1 (rope_impl.hpp) before use.
+  int from_proj;
+  int q_origin_first;
+  float rope_log2_theta;
 };
 
 struct SdpaPlan {

@@ -25,6 +25,7 @@ from .attention import (
 )
 from .decode import (
     gda_decode_attention,
+    gda_decode_attention_from_proj,
     gda_decode_attention_q4,
     gda_decode_attention_q4_reference,
     gda_decode_attention_reference,
@@ -52,6 +53,7 @@ __all__ = [
     "gda_post_split_reference",
     "gda_decode_attention",
     "gda_decode_attention_reference",
+    "gda_decode_attention_from_proj",
     "gda_decode_attention_q4",
     "gda_decode_attention_q4_reference",
     "sdpa_dual_v",

@@ -209,3 +209,60 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
                                            *(t.data_ptr() for t in new_kv), *ptrs, *tail)
     _native.check(rc)
     return y
+
+
+def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale: float,
+                                   subln_weight, lambda_full, lambda_init: float, gr: int,
+                                   offset: int, theta: float = 10000.0, eps: float = 1e-5,
+                                   origin_first: bool = False):
+    """A layer's whole decode attention from the projection outputs:
+    ``q_proj`` (B, 1, H_kv*(gr+1)*D), ``k_proj`` and ``v_proj`` (B, 1,
+    2*H_kv*D) (k_ratio 1).  RoPE at position ``offset`` (``rope_split4``'s
+    rounding), the token's rows written at row ``offset`` of the 4-slot fp
+    cache ``k1, k2, v1, v2``, then the step over ``offset + 1`` rows.  On the
+    fp16/bf16 cache at head_dim 128 this is ``motif_gda_decode_proj`` (the
+    attention launch ropes and writes; then the merge); otherwise
+    ``rope_split4`` followed by ``gda_decode_attention``."""
+    from .rope import rope_split4, rope_split4_reference
+
+    B, S, nq = q_proj.shape
+    H_kv = k1.shape[1]
+    assert S == 1, "gda_decode_attention_from_proj is decode-only"
+    D = nq // (H_kv * (gr + 1))
+    assert nq == H_kv * (gr + 1) * D, "q width must be H_kv*(gr+1)*D"
+    kv_len = offset + 1
+    if _common._DISABLE:
+        q1, q2, *_ = rope_split4_reference(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset,
+                                           theta, origin_first, caches=(k1, k2, v1, v2))
+        return gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale, subln_weight,
+                                              lambda_full, lambda_init, gr, eps, kv_len)
+    assert k_proj.shape == (B, 1, 2 * H_kv * D) and v_proj.shape == (B, 1, 2 * H_kv * D), (
+        "k_proj and v_proj must be (B, 1, 2*H_kv*D)")
+    KV_cap = k1.shape[2]
+    for t in (k1, k2, v1, v2):
+        assert t.shape == (B, H_kv, KV_cap, D), "cache slots must be (B, H_kv, KV_cap, D)"
+    _require_in_place((k1, k2, v1, v2))
+    assert 0 <= offset < KV_cap, f"offset={offset} must be in [0, {KV_cap})"
+    dev = _native.require_device(q_proj, k_proj, v_proj, k1, k2, v1, v2)
+    for t in (k_proj, v_proj, k1, k2, v1, v2):
+        if t.dtype != q_proj.dtype:
+            raise TypeError(f"dtype {t.dtype} must match q dtype {q_proj.dtype}")
+    q_proj, k_proj, v_proj = (_common.contiguous(t) for t in (q_proj, k_proj, v_proj))
+    w = subln_weight.to(device=dev, dtype=q_proj.dtype).contiguous()
+    lam = _common.f32_scalar_tensor(lambda_full, dev)
+    y = torch.empty((B, H_kv * gr, 1, 2 * D), dtype=q_proj.dtype, device=dev)
+    lib = _native.lib()
+    ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
+    rc = lib.motif_gda_decode_proj(
+        q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(), k1.data_ptr(), k2.data_ptr(),
+        v1.data_ptr(), v2.data_ptr(), w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init),
+        float(eps), y.data_ptr(), _native.dtype_code(q_proj.dtype), B, H_kv, gr, D, KV_cap,
+        kv_len, float(scale), float(theta), int(bool(origin_first)), ws.data_ptr(), ws.numel(),
+        _native.stream_of(dev))
+    if rc == _native.MOTIF_ERR_UNSUPPORTED:  # the two native calls
+        q1, q2, *_ = rope_split4(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset, theta,
+                                 origin_first, caches=(k1, k2, v1, v2))
+        return gda_decode_attention(q1, q2, k1, k2, v1, v2, scale, subln_weight, lambda_full,
+                                    lambda_init, gr, eps, kv_len=kv_len)
+    _native.check(rc)
+    return y
