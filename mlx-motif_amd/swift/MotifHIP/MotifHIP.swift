@@ -255,6 +255,30 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// A layer's decode attention from the projection outputs: RoPE at
+    /// position kvLen - 1, the head split and the token's cache rows inside
+    /// the attention launch (fp16/bf16 cache, head_dim 128; other shapes
+    /// return .unsupported: compose ropeSplit4 and gdaDecode).
+    public static func gdaDecodeFromProjections(
+        qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
+        keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
+        value1: UnsafeMutableRawPointer, value2: UnsafeMutableRawPointer,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int,
+        kvCapacity: Int, kvLen: Int, scale: Float, theta: Float, originFirst: Bool,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_proj(qProj, kProj, vProj, keys1, keys2, value1, value2,
+                                       sublnWeight, lambdaFull, oneMinusLambdaInit, eps, output,
+                                       dtype.rawValue, Int32(batch), Int32(kvHeads), Int32(gr),
+                                       Int32(headDim), Int32(kvCapacity), Int32(kvLen), scale,
+                                       theta, originFirst ? 1 : 0, workspace, workspaceBytes,
+                                       stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// PolyNorm over the last axis of x (rows, D).
     public static func polynorm(
         x: UnsafeRawPointer, weight: UnsafeRawPointer, bias: UnsafeRawPointer,
