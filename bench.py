@@ -565,6 +565,19 @@ def run_extra(torch, lib, dev, args):
     report("decode layer attention f16 kv16000 (from projections, RoPE in the step)",
            time_calls(torch, [layer_proj(sl) for sl in layers], steps, warm),
            decode_bytes(KV_LEN, True))
+    from mlx_motif.kernels import gda_decode_attention_q4_from_proj, quantize as _quant
+    qlayers = [[_quant(t, GS, 4) for t in sl] for sl in layers]
+    del layers
+    torch.cuda.synchronize()
+
+    def layer_q_proj(slots):
+        return lambda: gda_decode_attention_q4_from_proj(qp1, kp1, vp1, *slots, D ** -0.5, wsub,
+                                                         lam1, 0.2, 4, KV_LEN - 1, GS, 4)
+
+    report("decode layer attention q4 kv16000 (from projections, RoPE in the step)",
+           time_calls(torch, [layer_q_proj(sl) for sl in qlayers], steps, warm),
+           decode_bytes(KV_LEN, True, bits=4))
+    layers = qlayers
     del layers
     torch.cuda.empty_cache()
     # RoPE + head split + 4-slot write of a 512-row prefill chunk (12.7B

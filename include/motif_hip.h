@@ -320,6 +320,23 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
                           int kv_len, float scale, float theta, int origin_first,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same from the projection outputs over the packed cache: q and the k
+ * rows roped as motif_rope_split4 rounds them (fp16), the four rows
+ * quantised into row kv_len - 1 as motif_quant_write4 does; y equals
+ * motif_rope_split4 + motif_gda_decode_q_append bit for bit.  fp16 scales,
+ * D = 128, (gr + 1 columns) x (D / group_size) <= 16; other shapes return
+ * MOTIF_ERR_UNSUPPORTED. */
+int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* v_proj,
+                            uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                            uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                            uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                            uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                            const void* subln_w, const float* lambda_full,
+                            float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                            int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                            int group_size, float scale, float theta, int origin_first,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
                               const void* k2_new, const void* v1_new, const void* v2_new,
                               uint32_t* k1_data, void* k1_scales, void* k1_biases,

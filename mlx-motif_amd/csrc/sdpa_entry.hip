@@ -655,4 +655,64 @@ int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new
                       workspace_bytes, nk, stream);
 }
 
+int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* v_proj,
+                            uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                            uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                            uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                            uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                            const void* subln_w, const float* lambda_full,
+                            float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                            int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                            int group_size, float scale, float theta, int origin_first,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  const char* name = "gda_decode_q_proj";
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+                             workspace_bytes);
+  if (rc != MOTIF_OK) return rc;
+  MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
+  MOTIF_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+                "%s: group_size=%d must be 32, 64 or 128", name, group_size);
+  MOTIF_REQUIRE(q_proj && k_proj && v_proj && y && subln_w && lambda_full && k1_data &&
+                    k1_scales && k1_biases && k2_data && k2_scales && k2_biases && v1_data &&
+                    v1_scales && v1_biases && v2_data && v2_scales && v2_biases,
+                "%s: null pointer", name);
+  MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the new token's row", name, kv_len);
+  MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  const int gc = gda_columns(gr);
+  const int ng = D > 0 ? D / group_size : 1;
+  const uintptr_t data_bits = (uintptr_t)k1_data | (uintptr_t)k2_data | (uintptr_t)v1_data |
+                              (uintptr_t)v2_data;
+  const uintptr_t scale_bits = (uintptr_t)k1_scales | (uintptr_t)k1_biases |
+                               (uintptr_t)k2_scales | (uintptr_t)k2_biases |
+                               (uintptr_t)v1_scales | (uintptr_t)v1_biases |
+                               (uintptr_t)v2_scales | (uintptr_t)v2_biases;
+  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+                     gc * ng <= 16 && (data_bits & 15u) == 0 &&
+                     (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
+                     kv_len <= kMfmaMaxRows && aligned(q_proj, 16) && aligned(k_proj, 16) &&
+                     aligned(v_proj, 16) && aligned(y, 8);
+  if (!fused) {
+    set_error("%s: no fused variant for this shape (dtype %d, D=%d, gr=%d, group_size=%d); use "
+              "motif_rope_split4 and motif_gda_decode_q_append", name, dtype, D, gr, group_size);
+    return MOTIF_ERR_UNSUPPORTED;
+  }
+  SdpaArgs a = gda_decode_args(L, L.plan_q, q_proj, q_proj, y, B, Hkv, gr, kv_cap, kv_len,
+                               scale, subln_w, lambda_full, one_minus_lambda_init, eps,
+                               workspace);
+  a.kd = k1_data; a.ks = k1_scales; a.kb = k1_biases;
+  a.k2d = k2_data; a.k2s = k2_scales; a.k2b = k2_biases;
+  a.v1d = v1_data; a.v1s = v1_scales; a.v1b = v1_biases;
+  a.v2d = v2_data; a.v2s = v2_scales; a.v2b = v2_biases;
+  a.group_size = group_size;
+  a.new_k1 = k_proj; a.new_k2 = k_proj; a.new_v1 = v_proj; a.new_v2 = v_proj;
+  a.append = 1;
+  a.from_proj = 1;
+  a.q_origin_first = origin_first != 0;
+  a.rope_log2_theta = log2f(theta);
+  return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit),
+                                 (hipStream_t)stream);
+}
+
 }  // extern "C"

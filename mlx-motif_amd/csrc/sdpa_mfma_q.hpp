@@ -27,6 +27,7 @@
 #pragma once
 
 #include "quant_impl.hpp"
+#include "rope_impl.hpp"
 #include "sdpa_mfma.hpp"
 
 namespace motif {
@@ -208,12 +209,31 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
   constexpr int WPR = D * BITS / 32;
   const int slot = lane / 16;
   const int chunk = lane % 16;
-  const void* src = slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
   const uint32_t* data = slot == 0 ? a.kd : slot == 1 ? a.k2d : slot == 2 ? a.v1d : a.v2d;
   const void* sc = slot == 0 ? a.ks : slot == 1 ? a.k2s : slot == 2 ? a.v1s : a.v2s;
   const void* bi = slot == 0 ? a.kb : slot == 1 ? a.k2b : slot == 2 ? a.v1b : a.v2b;
   float v[8];
-  load8<half_t>(src, bk * D + (long)chunk * 8, v);
+  if (!a.from_proj) {
+    const void* src =
+        slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
+    load8<half_t>(src, bk * D + (long)chunk * 8, v);
+  } else {
+    // From the projections: head 2 * kvh + (slot & 1), row 2 * bk + (slot & 1);
+    // k rows are roped (pair partner in lane L ^ 8) and rounded to fp16 as
+    // rope_split4 stores them, then quantised.
+    load8<half_t>(slot < 2 ? a.new_k1 : a.new_v1, (2 * bk + (slot & 1)) * D + (long)chunk * 8,
+                  v);
+    const bool first = chunk < 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float other = __shfl_xor(v[e], 8);
+      float cs, sn, y1, y2;
+      rope_angle(8 * (chunk & 7) + e, D, a.kv_len - 1, a.rope_log2_theta, cs, sn);
+      rope_rotate(first ? v[e] : other, first ? other : v[e], cs, sn, y1, y2);
+      const float y = (float)(half_t)(first ? y1 : y2);
+      if (slot < 2) v[e] = y;
+    }
+  }
   uint32_t w[2];
   float scale, bias;
   quantize8<BITS, LPG>(v, w, scale, bias);
@@ -316,12 +336,17 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 
   // Append: the owner quantises and stores the new rows first, and waits for
   // the stores before it loads the tile that holds row kv_len - 1.
+  // (If that tile is not among the first U, the store is issued after the
+  // first tiles' loads instead, so that it does not delay them.)
   bool owner = false;
+  bool append_early = false;
+  const int append_tile = (a.kv_len - 1) / 16 * 16;  // first row of that tile
   if constexpr (DUAL) {
     owner = append_owner<NW>(a, split, wave);
-    if (owner) append_rows_q<BITS, GS>(a, bk, lane);
+#pragma unroll
+    for (int u = 0; u < U; ++u) append_early |= tile_row(u) == append_tile;
+    if (owner && append_early) append_rows_q<BITS, GS>(a, bk, lane);
   }
-  const int append_tile = (a.kv_len - 1) / 16 * 16;  // first row of that tile
 
   // All loads of this wave's tiles k0 .. k0 + U - 1 (rows past max_lim read 0).
   auto load_tiles = [&](Tile (&T)[U], int k0) {
@@ -374,14 +399,57 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     const uint16_t* qp =
         (const uint16_t*)a.q + (qrow0 + (hb[bb] < nvh ? hb[bb] : 0)) * D + 32 * blk;
     if constexpr (DUAL) {
-      qp = h < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + h) * D
-                   : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      if (a.from_proj) {  // q_proj heads: stripe g*(G+1)+j, or origin-first
+        const int head = a.q_origin_first ? (h < a.G ? kvh * a.G + h : a.Hkv * a.G + kvh)
+                                          : kvh * (a.G + 1) + (h < a.G ? h : a.G);
+        qp = (const uint16_t*)a.q + ((long)b * a.Hkv * (a.G + 1) + head) * D;
+      } else {
+        qp = h < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + h) * D
+                     : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      }
       qp += 32 * blk;
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) qraw[bb][s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
   load_tiles(ta, k0);
+  if constexpr (DUAL) {
+    if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
+  }
+  if constexpr (DUAL) {
+    if (a.from_proj) {
+      // RoPE at kv_len - 1, rounded to fp16 as rope_split4 does (after the
+      // first tiles' loads are issued, so their latency covers it).  Lane (col,
+      // blk) holds channels 32*blk + 8*s + e; the pair partner of blk is blk ^ 2
+      // (lane L ^ 32).  Lane L computes the angle of pair L, which the
+      // others read with __shfl.
+      float cs0, sn0;
+      rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, cs0, sn0);
+      const bool first = blk < 2;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        uint32_t w[4] = {qraw[0][s].x, qraw[0][s].y, qraw[0][s].z, qraw[0][s].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t o = (uint32_t)__shfl_xor((int)w[i], 32);
+          uint32_t r = 0;
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int p = 32 * (blk & 1) + 8 * s + 2 * i + e;
+            const float cs = __shfl(cs0, p);
+            const float sn = __shfl(sn0, p);
+            const float mine = (float)__builtin_bit_cast(half_t, (uint16_t)(e ? w[i] >> 16 : w[i] & 0xFFFFu));
+            const float oth = (float)__builtin_bit_cast(half_t, (uint16_t)(e ? o >> 16 : o & 0xFFFFu));
+            float y1, y2;
+            rope_rotate(first ? mine : oth, first ? oth : mine, cs, sn, y1, y2);
+            r |= (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(first ? y1 : y2)) << (16 * e);
+          }
+          w[i] = r;
+        }
+        qraw[0][s] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
 
   // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
   // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the

@@ -98,6 +98,11 @@ _SIGNATURES = {
         _c_int,
         [_vp] * 9 + [_c_f, _c_f, _vp] + [_c_int] * 7 + [_c_f, _c_f, _c_int, _vp, _c_sz, _vp],
     ),
+    "motif_gda_decode_q_proj": (
+        _c_int,
+        [_vp] * 17 + [_c_f, _c_f, _vp] + [_c_int] * 9
+        + [_c_f, _c_f, _c_int, _vp, _c_sz, _vp],
+    ),
     "motif_gda_decode_q_append": (
         _c_int,
         [_vp] * 20 + [_c_f, _c_f, _vp] + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],

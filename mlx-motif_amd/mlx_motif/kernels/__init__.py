@@ -26,6 +26,7 @@ from .attention import (
 from .decode import (
     gda_decode_attention,
     gda_decode_attention_from_proj,
+    gda_decode_attention_q4_from_proj,
     gda_decode_attention_q4,
     gda_decode_attention_q4_reference,
     gda_decode_attention_reference,
@@ -54,6 +55,7 @@ __all__ = [
     "gda_decode_attention",
     "gda_decode_attention_reference",
     "gda_decode_attention_from_proj",
+    "gda_decode_attention_q4_from_proj",
     "gda_decode_attention_q4",
     "gda_decode_attention_q4_reference",
     "sdpa_dual_v",

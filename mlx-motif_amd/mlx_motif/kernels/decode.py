@@ -266,3 +266,57 @@ def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale
                                     lambda_init, gr, eps, kv_len=kv_len)
     _native.check(rc)
     return y
+
+
+def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q: tuple,
+                                      v1_q: tuple, v2_q: tuple, scale: float, subln_weight,
+                                      lambda_full, lambda_init: float, gr: int, offset: int,
+                                      group_size: int = 64, bits: int = 4,
+                                      theta: float = 10000.0, eps: float = 1e-5,
+                                      origin_first: bool = False):
+    """``gda_decode_attention_from_proj`` over the packed cache: the token's
+    roped k rows and v rows are quantised into row ``offset`` of the packed
+    slots.  ``motif_gda_decode_q_proj`` when the fused kernel takes the
+    shape, else ``rope_split4`` then ``gda_decode_attention_q4(new_kv=...)``
+    (the same values bit for bit)."""
+    from .rope import rope_split4, rope_split4_reference
+
+    B, S, nq = q_proj.shape
+    H_kv = k1_q[0].shape[1]
+    assert S == 1, "gda_decode_attention_q4_from_proj is decode-only"
+    D = nq // (H_kv * (gr + 1))
+    assert nq == H_kv * (gr + 1) * D, "q width must be H_kv*(gr+1)*D"
+    kv_len = offset + 1
+    slots = (k1_q, k2_q, v1_q, v2_q)
+    if _common._DISABLE:
+        q1, q2, *rows = rope_split4_reference(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset,
+                                              theta, origin_first)
+        return gda_decode_attention_q4(q1, q2, *slots, scale, subln_weight, lambda_full,
+                                       lambda_init, gr, group_size, bits, eps, kv_len=kv_len,
+                                       new_kv=rows)
+    KV_cap = k1_q[0].shape[2]
+    _q_contract(D, H_kv * gr, H_kv, group_size, bits, kv_len, KV_cap)
+    assert k_proj.shape == (B, 1, 2 * H_kv * D) and v_proj.shape == (B, 1, 2 * H_kv * D), (
+        "k_proj and v_proj must be (B, 1, 2*H_kv*D)")
+    _require_in_place([x for t in slots for x in t])
+    dev = _native.require_device(q_proj, k_proj, v_proj, *(x for t in slots for x in t))
+    q_proj, k_proj, v_proj = (_common.contiguous(t) for t in (q_proj, k_proj, v_proj))
+    w = subln_weight.to(device=dev, dtype=q_proj.dtype).contiguous()
+    lam = _common.f32_scalar_tensor(lambda_full, dev)
+    y = torch.empty((B, H_kv * gr, 1, 2 * D), dtype=q_proj.dtype, device=dev)
+    lib = _native.lib()
+    ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
+    rc = lib.motif_gda_decode_q_proj(
+        q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(),
+        *(x.data_ptr() for t in slots for x in t), w.data_ptr(), lam.data_ptr(),
+        float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q_proj.dtype), B,
+        H_kv, gr, D, KV_cap, kv_len, bits, group_size, float(scale), float(theta),
+        int(bool(origin_first)), ws.data_ptr(), ws.numel(), _native.stream_of(dev))
+    if rc == _native.MOTIF_ERR_UNSUPPORTED:  # the two native calls
+        q1, q2, *rows = rope_split4(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset, theta,
+                                    origin_first)
+        return gda_decode_attention_q4(q1, q2, *slots, scale, subln_weight, lambda_full,
+                                       lambda_init, gr, group_size, bits, eps, kv_len=kv_len,
+                                       new_kv=rows)
+    _native.check(rc)
+    return y
