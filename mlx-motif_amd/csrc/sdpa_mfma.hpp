@@ -114,6 +114,10 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
     for (int i = 0; i < 4; ++i) o[i] = (uint32_t)__shfl_xor((int)x[i], 8);  // partner chunk
     const bool first = chunk < 8;
     const int pos = a.kv_len - 1;
+    // Lane L computes the angle of pair L (0..63) once; the lanes read the
+    // eight they need with __shfl (one slow-path sincosf per lane, not eight).
+    float cs0, sn0;
+    rope_angle((int)(threadIdx.x & 63u), 128, pos, a.rope_log2_theta, cs0, sn0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t r = 0;
@@ -123,8 +127,9 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
         const uint16_t other = (uint16_t)(e ? o[i] >> 16 : o[i] & 0xFFFFu);
         const float x1 = Elem<T>::to_f32(first ? mine : other);
         const float x2 = Elem<T>::to_f32(first ? other : mine);
-        float cs, sn, y1, y2;
-        rope_angle(8 * (chunk & 7) + 2 * i + e, 128, pos, a.rope_log2_theta, cs, sn);
+        const float cs = __shfl(cs0, 8 * (chunk & 7) + 2 * i + e);
+        const float sn = __shfl(sn0, 8 * (chunk & 7) + 2 * i + e);
+        float y1, y2;
         rope_rotate(x1, x2, cs, sn, y1, y2);
         r |= (uint32_t)Elem<T>::from_f32(first ? y1 : y2) << (16 * e);
       }

@@ -223,12 +223,17 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
     // rope_split4 stores them, then quantised.
     load8<half_t>(slot < 2 ? a.new_k1 : a.new_v1, (2 * bk + (slot & 1)) * D + (long)chunk * 8,
                   v);
+    // Lane L computes the angle of pair L (0..63) once; the lanes read the
+    // eight they need with __shfl (one slow-path sincosf per lane, not eight).
     const bool first = chunk < 8;
+    float cs0, sn0;
+    rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, cs0, sn0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float other = __shfl_xor(v[e], 8);
-      float cs, sn, y1, y2;
-      rope_angle(8 * (chunk & 7) + e, D, a.kv_len - 1, a.rope_log2_theta, cs, sn);
+      const float cs = __shfl(cs0, 8 * (chunk & 7) + e);
+      const float sn = __shfl(sn0, 8 * (chunk & 7) + e);
+      float y1, y2;
       rope_rotate(first ? v[e] : other, first ? other : v[e], cs, sn, y1, y2);
       const float y = (float)(half_t)(first ? y1 : y2);
       if (slot < 2) v[e] = y;
@@ -412,10 +417,10 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qraw[bb][s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
+  // Keep the q loads ahead of the tile loads: the q RoPE below then waits for
+  // q alone, not for the first tiles too.
+  __builtin_amdgcn_sched_barrier(0);
   load_tiles(ta, k0);
-  if constexpr (DUAL) {
-    if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
-  }
   if constexpr (DUAL) {
     if (a.from_proj) {
       // RoPE at kv_len - 1, rounded to fp16 as rope_split4 does (after the
@@ -449,6 +454,10 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         qraw[0][s] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
+    // The deferred append comes after the q RoPE: its loads would otherwise
+    // make every wave's RoPE wait for the first tiles (register reuse
+    // across the branch).
+    if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
   }
 
   // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
