@@ -367,6 +367,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * default: matrix-core kernels where compiled; 0: VALU kernels only),
  * "fused_merge" (0, the default: a second launch combines the splits; 1: the
  * last workgroup to finish combines them inside the attention launch),
+ * "qpair" (packed caches at head_dim 128, group size 64/128: 1, the
+ * default, decodes 4-bit caches with the paired-tile kernel; 2 also 8-bit
+ * caches; 0 keeps the per-tile kernel for both),
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
  * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.

@@ -219,6 +219,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     tuning().fused_merge = value;
+  } else if (!strcmp(key, "qpair")) {
+    if (value < 0 || value > 2) {
+      set_error("motif_set_tuning: qpair must be 0, 1 or 2");
+      return MOTIF_ERR_CONTRACT;
+    }
+    tuning().qpair = value;
   } else if (!strcmp(key, "poly_rows")) {
     tuning().poly_rows = value;
   } else {

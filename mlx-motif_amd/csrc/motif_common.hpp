@@ -38,6 +38,7 @@ struct Tuning {
   int mfma = 1;            // 1 = matrix-core kernels where compiled, 0 = VALU kernels
   int fused_merge = 0;     // 1 = last-arriving workgroup merges splits, 0 = merge kernel
   int poly_rows = 0;       // persistent PolyNorm workgroups per CU (0 = by register use)
+  int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 q4, 2 q4+q8
 };
 Tuning& tuning();
 

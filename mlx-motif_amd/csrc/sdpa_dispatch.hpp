@@ -19,6 +19,12 @@ int dispatch_sdpa_q_f16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, h
 int dispatch_sdpa_q_bf16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 
+// Packed cache, fp16 scales, head_dim 128, group size 64 or 128: the
+// paired-tile matrix-core kernel (sdpa_qpair.hip).  gc heads per workgroup
+// with gc * 128 / gs <= 16, waves 4 or 8.
+int launch_sdpa_qpair(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
+                      hipStream_t s);
+
 // Split merge (second launch when a.fused_merge == 0 and nsplit > 1) for
 // outputs of the given element type.
 int launch_sdpa_merge_f16(const SdpaArgs& a, int D, hipStream_t s);

@@ -67,8 +67,13 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
     const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;
     const bool aligned = (data_bits & 15u) == 0 && (scale_bits & (ng == 1 ? 7u : 15u)) == 0 &&
                          a.kv_cap % 4 == 0 && a.kv_len <= kMfmaMaxRows;
-    if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16)
+    if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16) {
+      // Paired-tile kernel: 4-bit by default (qpair 1); 8-bit too with
+      // qpair 2 (slower than the per-tile kernel there).
+      if (tuning().qpair >= (bits == 4 ? 1 : 2) && ng <= 2 && ((uintptr_t)a.q & 15u) == 0)
+        return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
+    }
   }
   if (bits == 4) {
     switch (D) {
