@@ -79,6 +79,28 @@ def _write_rows_q_reference(slots, new_kv, kv_len, group_size, bits):
             dst[:, :, kv_len - 1:kv_len, :] = src
 
 
+def _check_q_slots(slots, B, H_kv, KV_cap, D, bits, group_size, dtype):
+    """Checks the four packed ``(data, scales, biases)`` slots against the
+    step's shape: data (B, H_kv, KV_cap, D*bits/32) uint32, scales and biases
+    (B, H_kv, KV_cap, D/group_size) of the query dtype.  The native entry
+    points take bare pointers, so this is the only shape check they get."""
+    n_uint = D * bits // 32
+    if len(slots) != 4 or any(len(t) != 3 for t in slots):
+        raise ValueError("packed slots must be four (data, scales, biases) triples")
+    for t in slots:
+        assert tuple(t[0].shape) == (B, H_kv, KV_cap, n_uint), (
+            f"packed data {tuple(t[0].shape)} must be (B, H_kv, KV_cap, D*bits/32) = "
+            f"{(B, H_kv, KV_cap, n_uint)}")
+        if t[0].dtype not in (torch.uint32, torch.int32):
+            raise TypeError(f"packed data dtype {t[0].dtype} must be uint32")
+        for x in t[1:]:
+            assert tuple(x.shape) == (B, H_kv, KV_cap, D // group_size), (
+                f"scales/biases {tuple(x.shape)} must be (B, H_kv, KV_cap, D/group_size) = "
+                f"{(B, H_kv, KV_cap, D // group_size)}")
+            if x.dtype != dtype:
+                raise TypeError(f"scales/biases dtype {x.dtype} must match q dtype {dtype}")
+
+
 def _require_in_place(tensors):
     for t in tensors:
         if not t.is_contiguous():
@@ -183,12 +205,8 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
     assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
     _q_contract(D, H_o, H_kv, group_size, bits, kv_len, KV_cap)
+    _check_q_slots(slots, B, H_kv, KV_cap, D, bits, group_size, q1.dtype)
     dev = _native.require_device(q1, q2, *(x for t in slots for x in t), *(new_kv or ()))
-    for t in slots:
-        assert tuple(t[0].shape) == (B, H_kv, KV_cap, n_uint), "packed slots must match k1"
-        for x in t[1:]:
-            if x.dtype != q1.dtype:
-                raise TypeError(f"scales/biases dtype {x.dtype} must match q1 dtype {q1.dtype}")
     if q2.dtype != q1.dtype:
         raise TypeError(f"q2 dtype {q2.dtype} must match q1 dtype {q1.dtype}")
     q1, q2 = _common.contiguous(q1), _common.contiguous(q2)
@@ -214,7 +232,7 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
 def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale: float,
                                    subln_weight, lambda_full, lambda_init: float, gr: int,
                                    offset: int, theta: float = 10000.0, eps: float = 1e-5,
-                                   origin_first: bool = False):
+                                   origin_first: bool = False, rope_scaling=None):
     """A layer's whole decode attention from the projection outputs:
     ``q_proj`` (B, 1, H_kv*(gr+1)*D), ``k_proj`` and ``v_proj`` (B, 1,
     2*H_kv*D) (k_ratio 1).  RoPE at position ``offset`` (``rope_split4``'s
@@ -222,8 +240,11 @@ def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale
     cache ``k1, k2, v1, v2``, then the step over ``offset + 1`` rows.  On the
     fp16/bf16 cache at head_dim 128 this is ``motif_gda_decode_proj`` (the
     attention launch ropes and writes; then the merge); otherwise
-    ``rope_split4`` followed by ``gda_decode_attention``."""
-    from .rope import rope_split4, rope_split4_reference
+    ``rope_split4`` followed by ``gda_decode_attention``.  ``rope_scaling``
+    must be ``None``: only unscaled RoPE is built."""
+    from .rope import require_unscaled, rope_split4, rope_split4_reference
+
+    require_unscaled(rope_scaling)
 
     B, S, nq = q_proj.shape
     H_kv = k1.shape[1]
@@ -273,13 +294,15 @@ def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q:
                                       lambda_full, lambda_init: float, gr: int, offset: int,
                                       group_size: int = 64, bits: int = 4,
                                       theta: float = 10000.0, eps: float = 1e-5,
-                                      origin_first: bool = False):
+                                      origin_first: bool = False, rope_scaling=None):
     """``gda_decode_attention_from_proj`` over the packed cache: the token's
     roped k rows and v rows are quantised into row ``offset`` of the packed
     slots.  ``motif_gda_decode_q_proj`` when the fused kernel takes the
     shape, else ``rope_split4`` then ``gda_decode_attention_q4(new_kv=...)``
-    (the same values bit for bit)."""
-    from .rope import rope_split4, rope_split4_reference
+    (the same values bit for bit).  ``rope_scaling`` must be ``None``."""
+    from .rope import require_unscaled, rope_split4, rope_split4_reference
+
+    require_unscaled(rope_scaling)
 
     B, S, nq = q_proj.shape
     H_kv = k1_q[0].shape[1]
@@ -298,6 +321,10 @@ def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q:
     _q_contract(D, H_kv * gr, H_kv, group_size, bits, kv_len, KV_cap)
     assert k_proj.shape == (B, 1, 2 * H_kv * D) and v_proj.shape == (B, 1, 2 * H_kv * D), (
         "k_proj and v_proj must be (B, 1, 2*H_kv*D)")
+    for t in (k_proj, v_proj):
+        if t.dtype != q_proj.dtype:
+            raise TypeError(f"k_proj/v_proj dtype {t.dtype} must match q dtype {q_proj.dtype}")
+    _check_q_slots(slots, B, H_kv, KV_cap, D, bits, group_size, q_proj.dtype)
     _require_in_place([x for t in slots for x in t])
     dev = _native.require_device(q_proj, k_proj, v_proj, *(x for t in slots for x in t))
     q_proj, k_proj, v_proj = (_common.contiguous(t) for t in (q_proj, k_proj, v_proj))

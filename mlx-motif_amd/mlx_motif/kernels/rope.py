@@ -9,6 +9,13 @@ calls (``src/mlx_motif/model.py:590-594``; ``initialize_rope`` with
 (``motif_rope_split4``) from the projection outputs; with ``caches`` the
 k1/k2/v1/v2 rows are written straight into the full-capacity 4-slot fp cache
 at rows ``offset .. offset + S - 1``.
+
+Only unscaled RoPE is built: the reference model also accepts a
+``rope_scaling`` config (``initialize_rope(..., scaling_config=...)``,
+``model.py:414-419``; e.g. linear with factor 2, which divides positions by
+2).  Every wrapper here takes ``rope_scaling`` and raises
+``NotImplementedError`` for anything but ``None``, so a scaled config fails
+instead of getting unscaled positions.
 """
 
 from __future__ import annotations
@@ -67,15 +74,27 @@ def rope_split4_reference(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_grou
     return (q1.contiguous(), q2.contiguous(), *caches)
 
 
+def require_unscaled(rope_scaling) -> None:
+    """Rejects a RoPE scaling config (``ModelArgs.rope_scaling``): the kernels
+    rope at the unscaled positions ``offset + s``."""
+    if rope_scaling is not None:
+        raise NotImplementedError(
+            f"rope_scaling={rope_scaling!r}: only unscaled RoPE (rope_scaling=None) is "
+            "supported; a scaled config would get unscaled positions")
+
+
 def rope_split4(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_groups: int, kr: int,
-                offset: int, theta: float = 10000.0, origin_first: bool = False, caches=None):
+                offset: int, theta: float = 10000.0, origin_first: bool = False, caches=None,
+                rope_scaling=None):
     """``q_proj`` (B, S, q_groups*(gr+1)*D), ``k_proj`` (B, S,
     k_groups*(kr+1)*D), ``v_proj`` (B, S, 2*k_groups*D): projection outputs.
     Returns ``(q1, q2, k1, k2, v1, v2)``: q1 (B, q_groups*gr, S, D) and q2
     (B, q_groups, S, D) roped at positions ``offset + s``; k1/k2 (roped) and
     v1/v2 either new (B, H, S, D) tensors or, with ``caches=(k1, k2, v1,
     v2)`` full-capacity (B, H, cap, D) buffers, those buffers with rows
-    ``offset .. offset + S - 1`` written."""
+    ``offset .. offset + S - 1`` written.  ``rope_scaling`` must be ``None``
+    (``require_unscaled``)."""
+    require_unscaled(rope_scaling)
     if _common._DISABLE:
         return rope_split4_reference(q_proj, k_proj, v_proj, q_groups, gr, k_groups, kr, offset,
                                      theta, origin_first, caches)

@@ -258,7 +258,8 @@ public enum MotifHIP {
     /// A layer's decode attention from the projection outputs: RoPE at
     /// position kvLen - 1, the head split and the token's cache rows inside
     /// the attention launch (fp16/bf16 cache, head_dim 128; other shapes
-    /// return .unsupported: compose ropeSplit4 and gdaDecode).
+    /// return .unsupported: compose ropeSplit4 and gdaDecode).  Only
+    /// unscaled RoPE: check the model's rope_scaling is nil first.
     public static func gdaDecodeFromProjections(
         qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
         keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
@@ -276,6 +277,37 @@ public enum MotifHIP {
                                        Int32(headDim), Int32(kvCapacity), Int32(kvLen), scale,
                                        theta, originFirst ? 1 : 0, workspace, workspaceBytes,
                                        stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// The same from the projection outputs over the packed q4/q8 cache: the
+    /// token's roped k rows and v rows are quantised into row kvLen - 1 of
+    /// the four triples inside the attention launch (fp16 scales, head_dim
+    /// 128; other shapes return .unsupported: compose ropeSplit4 and
+    /// gdaDecodeQuantizedAppend, which give the same values bit for bit).
+    /// Only unscaled RoPE: check the model's rope_scaling is nil first.
+    public static func gdaDecodeQuantizedFromProjections(
+        qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
+        keys1: MotifHIPQuantizedTriple, keys2: MotifHIPQuantizedTriple,
+        value1: MotifHIPQuantizedTriple, value2: MotifHIPQuantizedTriple,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int,
+        kvCapacity: Int, kvLen: Int, bits: Int, groupSize: Int, scale: Float, theta: Float,
+        originFirst: Bool, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_q_proj(qProj, kProj, vProj,
+                                         keys1.data, keys1.scales, keys1.biases,
+                                         keys2.data, keys2.scales, keys2.biases,
+                                         value1.data, value1.scales, value1.biases,
+                                         value2.data, value2.scales, value2.biases,
+                                         sublnWeight, lambdaFull, oneMinusLambdaInit, eps,
+                                         output, dtype.rawValue, Int32(batch), Int32(kvHeads),
+                                         Int32(gr), Int32(headDim), Int32(kvCapacity),
+                                         Int32(kvLen), Int32(bits), Int32(groupSize), scale,
+                                         theta, originFirst ? 1 : 0, workspace, workspaceBytes,
+                                         stream)
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 

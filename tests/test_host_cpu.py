@@ -367,3 +367,82 @@ def test_quantized_cache_state_roundtrip_and_growth(disabled, rng, bits):
             np.testing.assert_array_equal(x.numpy(), y[:, :, :3].numpy())
     rd, _, _ = O.quantize(tb.numpy(), 64, bits)
     np.testing.assert_array_equal(grown[0][0][:, :, 3:].view(torch.int32).numpy().view(np.uint32), rd)
+
+
+def _q_trips(B, H_kv, cap, D, bits, gs, dtype=torch.float16):
+    return [(torch.zeros((B, H_kv, cap, D * bits // 32), dtype=torch.uint32),
+             torch.ones((B, H_kv, cap, D // gs), dtype=dtype),
+             torch.zeros((B, H_kv, cap, D // gs), dtype=dtype)) for _ in range(4)]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_decode_q_slot_contract(enabled, rng, bits):
+    """Packed-slot checks both packed-cache decode wrappers make before any
+    native call: data (B, H_kv, KV_cap, D*bits/32), scales and biases
+    (B, H_kv, KV_cap, D/gs) in the query dtype, projections in one dtype."""
+    B, H_kv, gr, D, cap, gs = 1, 2, 4, 128, 24, 64
+    q1, q2 = _t(rng, (B, H_kv * gr, 1, D)), _t(rng, (B, H_kv, 1, D))
+    q_proj = _t(rng, (B, 1, H_kv * (gr + 1) * D))
+    k_proj, v_proj = _t(rng, (B, 1, 2 * H_kv * D)), _t(rng, (B, 1, 2 * H_kv * D))
+    w, lam = _t(rng, (2 * D,)), torch.tensor([0.5])
+
+    def step(trips):
+        K.gda_decode_attention_q4(q1, q2, *trips, 0.1, w, lam, 0.2, gr, gs, bits, kv_len=8)
+
+    def from_proj(trips, kp=k_proj, vp=v_proj):
+        K.gda_decode_attention_q4_from_proj(q_proj, kp, vp, *trips, 0.1, w, lam, 0.2, gr, 7,
+                                            gs, bits)
+
+    for call in (step, from_proj):
+        t = _q_trips(B, H_kv, cap, D, bits, gs)
+        t[2] = (t[2][0][:, :, :16], t[2][1], t[2][2])  # one slot with another capacity
+        with pytest.raises(AssertionError, match="packed data"):
+            call(t)
+        t = _q_trips(B, H_kv, cap, D, bits, gs)
+        t[1] = (t[1][0], t[1][1][..., :1], t[1][2])  # scales of the wrong group count
+        with pytest.raises(AssertionError, match="scales/biases"):
+            call(t)
+        t = _q_trips(B, H_kv, cap, D, bits, gs)
+        t[3] = (t[3][0], t[3][1], t[3][2].float())
+        with pytest.raises(TypeError, match="scales/biases dtype"):
+            call(t)
+        with pytest.raises(TypeError, match="packed data dtype"):
+            t = _q_trips(B, H_kv, cap, D, bits, gs)
+            t[0] = (t[0][0].float(), t[0][1], t[0][2])
+            call(t)
+    # The projection path takes D from the q width: a packed width of the
+    # other bit count does not match it.
+    other = _q_trips(B, H_kv, cap, D, 12 - bits, gs)
+    with pytest.raises(AssertionError, match="packed data"):
+        from_proj(other)
+    with pytest.raises(TypeError, match="k_proj/v_proj dtype"):
+        from_proj(_q_trips(B, H_kv, cap, D, bits, gs), kp=k_proj.float())
+    with pytest.raises(TypeError, match="k_proj/v_proj dtype"):
+        from_proj(_q_trips(B, H_kv, cap, D, bits, gs), vp=v_proj.bfloat16())
+    # In contract, the CPU tensors reach the device check (no CPU fallback).
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        from_proj(_q_trips(B, H_kv, cap, D, bits, gs))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        step(_q_trips(B, H_kv, cap, D, bits, gs))
+
+
+def test_rope_scaling_is_rejected(rng, monkeypatch):
+    """A scaled RoPE config (the reference's grouped fixture uses linear
+    scaling, factor 2) is refused by every RoPE wrapper, kernels or not,
+    instead of roping at unscaled positions."""
+    scaling = {"rope_type": "linear", "factor": 2.0, "original_max_position_embeddings": 64}
+    q_proj, k_proj, v_proj = _t(rng, (1, 1, 640)), _t(rng, (1, 1, 256)), _t(rng, (1, 1, 256))
+    caches = [_t(rng, (1, 2, 8, 64)) for _ in range(4)]
+    w, lam = _t(rng, (128,)), torch.tensor([0.5])
+    for flag in (True, False):
+        monkeypatch.setattr(_common, "_DISABLE", flag)
+        with pytest.raises(NotImplementedError, match="rope_scaling"):
+            K.rope_split4(q_proj, k_proj, v_proj, 2, 4, 2, 1, 3, rope_scaling=scaling)
+        with pytest.raises(NotImplementedError, match="rope_scaling"):
+            K.gda_decode_attention_from_proj(q_proj, k_proj, v_proj, *caches, 0.1, w, lam, 0.2, 4,
+                                             3, rope_scaling=scaling)
+        with pytest.raises(NotImplementedError, match="rope_scaling"):
+            K.gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj,
+                                                *_q_trips(1, 2, 8, 64, 4, 64), 0.1, w, lam, 0.2,
+                                                4, 3, rope_scaling=scaling)
+    K.rope_split4_reference(q_proj, k_proj, v_proj, 2, 4, 2, 1, 3)  # unscaled still runs
