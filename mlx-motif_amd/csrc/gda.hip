@@ -164,6 +164,7 @@ int motif_gda_post_split(const void* attn_o, const void* attn_n, const void* sub
                          int dtype, int B, int q_origin, int q_groups, int gr, int S, int C,
                          const float* lambda_full, float one_minus_lambda_init, float eps,
                          void* stream) {
+  CallScope scope;
   clear_error();
   MOTIF_REQUIRE(B >= 0 && q_origin >= 0 && q_groups >= 0 && gr >= 1 && S >= 0 && C >= 0,
                 "gda_post_split: negative extent");
@@ -191,6 +192,7 @@ int motif_gda_post_split(const void* attn_o, const void* attn_n, const void* sub
 int motif_gda_post(const void* merged, const void* subln_w, void* y, int dtype, int B,
                    int q_groups, int gr, int S, int C, const float* lambda_full,
                    float one_minus_lambda_init, float eps, void* stream) {
+  CallScope scope;
   clear_error();
   MOTIF_REQUIRE(B >= 0 && q_groups >= 0 && gr >= 1 && S >= 0 && C >= 0,
                 "gda_post: negative extent");

@@ -47,9 +47,32 @@ int device_cu_count() {
   return cus[dev];
 }
 
-Tuning& tuning() {
-  static Tuning t;
-  return t;
+static std::mutex g_tuning_mu;
+static Tuning g_tuning;                    // written only under g_tuning_mu
+static thread_local Tuning tl_tuning;      // this thread's snapshot
+static thread_local int tl_scope_depth = 0;
+
+static void snapshot_tuning() {
+  std::lock_guard<std::mutex> lock(g_tuning_mu);
+  tl_tuning = g_tuning;
+}
+
+const Tuning& tuning() {
+  if (tl_scope_depth == 0) snapshot_tuning();
+  return tl_tuning;
+}
+
+CallScope::CallScope() {
+  if (tl_scope_depth++ == 0) snapshot_tuning();
+}
+
+CallScope::~CallScope() { --tl_scope_depth; }
+
+// motif_set_tuning: applies f to the shared knobs under their lock.
+template <typename F>
+static void update_tuning(F f) {
+  std::lock_guard<std::mutex> lock(g_tuning_mu);
+  f(g_tuning);
 }
 
 static size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -165,6 +188,7 @@ size_t motif_sdpa_counter_bytes(int B, int Hq, int Hkv, int S_q) {
 
 size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || S_q <= 0 || D <= 0 || kv_len < 0) return 0;
+  CallScope scope;  // one tuning snapshot for every plan below
   // Enough for every kernel family a call may take: the fp16/bf16/fp32 and
   // VALU plans and the packed-cache matrix-core plans of each group size.
   size_t ws = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0).workspace_bytes;
@@ -198,35 +222,35 @@ int motif_set_tuning(const char* key, int value) {
     return MOTIF_ERR_CONTRACT;
   }
   if (!strcmp(key, "rows_per_split")) {
-    tuning().rows_per_split = value;
+    update_tuning([&](Tuning& t) { t.rows_per_split = value; });
   } else if (!strcmp(key, "waves_per_wg")) {
     if (value != 0 && value != 4 && value != 8) {
       set_error("motif_set_tuning: waves_per_wg must be 0, 4 or 8");
       return MOTIF_ERR_CONTRACT;
     }
-    tuning().waves_per_wg = value;
+    update_tuning([&](Tuning& t) { t.waves_per_wg = value; });
   } else if (!strcmp(key, "min_wgs")) {
-    tuning().min_wgs = value;
+    update_tuning([&](Tuning& t) { t.min_wgs = value; });
   } else if (!strcmp(key, "mfma")) {
     if (value != 0 && value != 1) {
       set_error("motif_set_tuning: mfma must be 0 or 1");
       return MOTIF_ERR_CONTRACT;
     }
-    tuning().mfma = value;
+    update_tuning([&](Tuning& t) { t.mfma = value; });
   } else if (!strcmp(key, "fused_merge")) {
     if (value != 0 && value != 1) {
       set_error("motif_set_tuning: fused_merge must be 0 or 1");
       return MOTIF_ERR_CONTRACT;
     }
-    tuning().fused_merge = value;
+    update_tuning([&](Tuning& t) { t.fused_merge = value; });
   } else if (!strcmp(key, "qpair")) {
     if (value < 0 || value > 2) {
       set_error("motif_set_tuning: qpair must be 0, 1 or 2");
       return MOTIF_ERR_CONTRACT;
     }
-    tuning().qpair = value;
+    update_tuning([&](Tuning& t) { t.qpair = value; });
   } else if (!strcmp(key, "poly_rows")) {
-    tuning().poly_rows = value;
+    update_tuning([&](Tuning& t) { t.poly_rows = value; });
   } else {
     set_error("motif_set_tuning: unknown key '%s'", key);
     return MOTIF_ERR_CONTRACT;

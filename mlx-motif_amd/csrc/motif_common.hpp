@@ -40,7 +40,20 @@ struct Tuning {
   int poly_rows = 0;       // persistent PolyNorm workgroups per CU (0 = by register use)
   int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 q4, 2 q4+q8
 };
-Tuning& tuning();
+// The calling thread's snapshot of the process-wide knobs.  Inside a
+// CallScope it is the copy taken when the outermost scope opened, so every
+// read of one call (plan, workspace carving, dispatch) sees the same values
+// and a concurrent motif_set_tuning affects the next call only.  Outside a
+// scope each read takes a fresh copy.
+const Tuning& tuning();
+// Opened first thing by every extern "C" entry point that reads tuning()
+// (nested entry points share the outer snapshot).
+struct CallScope {
+  CallScope();
+  ~CallScope();
+  CallScope(const CallScope&) = delete;
+  CallScope& operator=(const CallScope&) = delete;
+};
 
 // ------------------------------------------------------------ elements ----
 // bf16 is carried as its 16 storage bits; conversion is exact (to f32) and

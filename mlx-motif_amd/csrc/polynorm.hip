@@ -333,6 +333,7 @@ using namespace motif;
 
 extern "C" int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
                               int dtype, int64_t rows, int D, float eps, void* stream) {
+  CallScope scope;
   clear_error();
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "polynorm: unknown dtype code %d", dtype);

@@ -180,6 +180,7 @@ extern "C" {
 
 int motif_quantize(const void* x, uint32_t* data, void* scales, void* biases, int dtype,
                    int64_t rows, int D, int bits, int group_size, void* stream) {
+  CallScope scope;
   clear_error();
   int rc = quant_checks("quantize", dtype, D, bits, group_size);
   if (rc != MOTIF_OK) return rc;
@@ -197,6 +198,7 @@ int motif_quantize(const void* x, uint32_t* data, void* scales, void* biases, in
 
 int motif_dequantize(const uint32_t* data, const void* scales, const void* biases, void* y,
                      int dtype, int64_t rows, int D, int bits, int group_size, void* stream) {
+  CallScope scope;
   clear_error();
   int rc = quant_checks("dequantize", dtype, D, bits, group_size);
   if (rc != MOTIF_OK) return rc;
@@ -212,6 +214,7 @@ int motif_quant_write4(const void* k1, const void* k2, const void* v1, const voi
                        uint32_t* const data[4], void* const scales[4], void* const biases[4],
                        int dtype, int B, int H, int S, int D, int kv_cap, int offset, int bits,
                        int group_size, void* stream) {
+  CallScope scope;
   clear_error();
   int rc = quant_checks("quant_write4", dtype, D, bits, group_size);
   if (rc != MOTIF_OK) return rc;

@@ -192,6 +192,7 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
                       void* k2, void* v1, void* v2, int dtype, int B, int S, int q_groups, int gr,
                       int k_groups, int kr, int D, int cap, int row0, int pos0, float theta,
                       int origin_first, void* stream) {
+  CallScope scope;
   clear_error();
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "rope_split4: unknown dtype code %d", dtype);

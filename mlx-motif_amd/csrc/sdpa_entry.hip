@@ -83,6 +83,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
                        const void* v2, void* y, int dtype, int B, int Hq, int Hkv, int S_q, int D,
                        int kv_cap, int kv_len, int causal, float scale, void* ws,
                        size_t ws_bytes, void* stream) {
+  CallScope scope;
   clear_error();
   SdpaArgs a{};
   SdpaPlan p{};
@@ -148,6 +149,7 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
                       const uint32_t* v2d, const void* v2s, const void* v2b, void* y, int dtype,
                       int B, int Hq, int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal,
                       int bits, int gs, float scale, void* ws, size_t ws_bytes, void* stream) {
+  CallScope scope;
   clear_error();
   // Packed-layout contract, attention.py:556-608.
   MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
@@ -309,6 +311,7 @@ extern "C" {
 
 size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int D) {
   if (B <= 0 || Hkv <= 0 || gr <= 0 || D <= 0 || kv_len < 0) return 0;
+  CallScope scope;
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
   return L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
 }
@@ -324,6 +327,7 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
                          void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
                          int kv_len, float scale, void* workspace, size_t workspace_bytes,
                          const void* const* new_kv, void* stream) {
+  CallScope scope;
   clear_error();
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
   int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
@@ -417,6 +421,7 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
                           void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
                           int kv_len, float scale, float theta, int origin_first,
                           void* workspace, size_t workspace_bytes, void* stream) {
+  CallScope scope;
   clear_error();
   const char* name = "gda_decode_proj";
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
@@ -543,6 +548,7 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
                         int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
                         int group_size, float scale, void* workspace, size_t workspace_bytes,
                         const void* const* new_kv, void* stream) {
+  CallScope scope;
   clear_error();
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
   int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
@@ -665,6 +671,7 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
                             int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
                             int group_size, float scale, float theta, int origin_first,
                             void* workspace, size_t workspace_bytes, void* stream) {
+  CallScope scope;
   clear_error();
   const char* name = "gda_decode_q_proj";
   const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);

@@ -192,23 +192,42 @@ def stream_of(device: torch.device) -> int:
 # ------------------------------------------------------------ workspace ---
 _ws_lock = threading.Lock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Buffers a larger call superseded.  A HIP graph captured earlier on that
+# stream still holds their addresses, so they are kept (not returned to the
+# allocator, where another tensor could take the memory a replay writes).
+_retired: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per (device, stream) split-KV workspace; counters start at zero.
 
     Calls on one stream are ordered, so they can share it; the kernels leave
-    the counters zero.  Growing replaces the buffer with a fresh zeroed one.
+    the counters zero.  Growing allocates a fresh zeroed buffer of at least
+    twice the old size and retires the old one without freeing it (graphs
+    captured before the growth replay into it), so the retired memory stays
+    below the live buffer's size.  ``release_retired_workspaces`` frees it
+    once no such graph is alive.
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            stream_of(device))
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _workspaces[key] = buf
+            size = max(nbytes, 1 << 20, 2 * buf.numel() if buf is not None else 0)
+            new = torch.zeros(size, dtype=torch.uint8, device=device)
+            if buf is not None:
+                _retired.append(buf)
+            _workspaces[key] = buf = new
         return buf
+
+
+def release_retired_workspaces() -> int:
+    """Frees the workspaces that growth superseded; returns their bytes.
+    Only safe when no HIP graph captured before a growth is still replayed."""
+    with _ws_lock:
+        n = sum(t.numel() for t in _retired)
+        _retired.clear()
+        return n
 
 
 def set_tuning(key: str, value: int) -> None:

@@ -132,3 +132,38 @@ def test_gda_decode_rejections_and_workspace():
     assert 0 < small <= big
     assert big >= 8 * 5 * 32 * (2 * 128 + 2) * 4
     assert lib.motif_gda_decode_workspace_bytes(0, 8, 4, 16, 128) == 0
+
+
+def test_tuning_changes_while_other_threads_size_calls():
+    """motif_set_tuning from one thread while others size calls: each call
+    reads one snapshot of the knobs, so every size is the one of either
+    setting (ctypes drops the GIL around the foreign calls, so the threads
+    run in the library at once)."""
+    import threading
+
+    lib = _native.lib()
+    args = (1, 32, 8, 1, 16000, 128)
+    default = lib.motif_sdpa_workspace_bytes(*args)
+    _native.set_tuning("rows_per_split", 64)
+    forced = lib.motif_sdpa_workspace_bytes(*args)
+    _native.set_tuning("rows_per_split", 0)
+    seen, stop = set(), threading.Event()
+
+    def size():
+        while not stop.is_set():
+            seen.add(lib.motif_sdpa_workspace_bytes(*args))
+
+    threads = [threading.Thread(target=size) for _ in range(4)]
+    for t in threads:
+        t.start()
+    try:
+        for i in range(2000):
+            _native.set_tuning("rows_per_split", 64 if i % 2 == 0 else 0)
+    finally:
+        _native.set_tuning("rows_per_split", 0)
+        stop.set()
+        for t in threads:
+            t.join()
+    assert seen <= {default, forced}, seen
+    assert lib.motif_sdpa_workspace_bytes(*args) == default
+

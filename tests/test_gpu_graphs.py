@@ -183,3 +183,68 @@ def test_graph_epilogues(gpu):
         assert _same(yp, ref_p), f"replay {i}: polynorm"
 
     _replay_and_check(gpu, graph, before, check)
+
+
+def test_graph_survives_workspace_growth(gpu):
+    """A decode step captured on a stream, then a larger call on the same
+    stream grows that stream's workspace.  The superseded buffer must stay
+    allocated: tensors made afterwards on the stream (filled with a marker)
+    must not receive the graph's partials, and every replay still equals
+    the eager step."""
+    import torch
+
+    from mlx_motif import _native
+    from mlx_motif.kernels import gda_decode_attention, sdpa_dual_v
+
+    mk = _gen(gpu, 21)
+    kv_len, cap, gr = 16000, 16128, 4
+    q1, q2 = mk(1, 32, 1, 128), mk(1, 8, 1, 128)
+    cache = [mk(1, 8, cap, 128) for _ in range(4)]
+    w = mk(256)
+    lam = torch.tensor([0.4321], dtype=torch.float32, device=gpu)
+
+    def step():
+        return gda_decode_attention(q1, q2, *cache, 0.0884, w, lam, 0.2, gr, 1e-5,
+                                    kv_len=kv_len)
+
+    print("graph gda_decode, then workspace growth on the capture stream", flush=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ref = step().clone()
+        old = _native.workspace(gpu, 0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = step()
+    torch.cuda.synchronize()
+    n_retired = len(_native._retired)
+    _native.set_tuning("rows_per_split", 16)  # ~1000 splits: a workspace far past the old one
+    try:
+        with torch.cuda.stream(s):
+            sdpa_dual_v(q1, cache[0], cache[2], cache[3], 0.0884, kv_len=kv_len)
+            grown = _native.workspace(gpu, 0)
+    finally:
+        _native.set_tuning("rows_per_split", 0)
+    torch.cuda.synchronize()
+    assert grown.numel() >= 2 * old.numel() and len(_native._retired) == n_retired + 1
+    old_ptr, old_bytes = old.data_ptr(), old.numel()
+    del old
+    with torch.cuda.stream(s):
+        marks = [torch.full((old_bytes,), 0x5A, dtype=torch.uint8, device=gpu) for _ in range(4)]
+    torch.cuda.synchronize()
+    assert all(m.data_ptr() != old_ptr for m in marks)
+
+    def before():
+        out.fill_(0)
+
+    def check(i):
+        assert _same(out, ref), f"replay {i}"
+        for m in marks:
+            assert bool((m == 0x5A).all()), f"replay {i} wrote into memory of a later tensor"
+
+    with torch.cuda.stream(s):
+        _replay_and_check(gpu, graph, before, check)
+    del graph, out
+    torch.cuda.synchronize()
+    assert _native.release_retired_workspaces() >= old_bytes
