@@ -79,6 +79,24 @@ int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* 
                       float scale, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ *
+ * motif_sdpa_dual_v without a workspace argument: it allocates nothing.
+ * No counterpart in the reference (whose kernels need no workspace); it is
+ * for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split partials and
+ * counters live in a static device array of 8 MiB per device (held until
+ * the process ends), whose first 64 KiB of counters are cleared by one fill
+ * kernel on the device's first call.  A call needing more
+ * (motif_sdpa_workspace_bytes > 8 MiB, or more than 16384 B*Hq rows)
+ * returns MOTIF_ERR_WORKSPACE before touching the GPU.  All calls on one
+ * device share the array: calls that may overlap on a device (several
+ * streams, or several threads) race, so order them; results equal
+ * motif_sdpa_dual_v's bit for bit.
+ * ------------------------------------------------------------------------ */
+int motif_sdpa_dual_v_noalloc(const void* q, const void* k, const void* v1, const void* v2,
+                              void* y, int dtype, int B, int Hq, int Hkv, int D, int kv_cap,
+                              int kv_len, float scale, void* stream);
+
+/* ------------------------------------------------------------------------ *
  * Same, reading the packed MLX-affine q4/q8 cache directly.
  * Replaces sdpa_dual_v_q4 (attention.py:510-645) and its Metal kernel
  * motif_sdpa_dual_v_q4 (attention.py:293-445).

@@ -1,5 +1,7 @@
 // extern "C" entry points of the dual-V attention path: contract checks,
 // launch plan, workspace carving, dispatch by element type.
+#include <mutex>
+
 #include "sdpa_dispatch.hpp"
 
 namespace motif {
@@ -301,6 +303,55 @@ static SdpaArgs gda_decode_args(const GdaDecodeLayout& L, const SdpaPlan& p, con
   return a;
 }
 
+// Scratch of motif_sdpa_dual_v_noalloc (its split partials and counters):
+// one copy per device, held until the process ends.  `scratch` names the
+// host-side stand-in; kernels get the device address that
+// hipGetSymbolAddress returns for the current device (scratch_for_device).
+static constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+// Leading bytes cleared once per device: the merge counters (the kernels
+// leave them zero after every call).
+static constexpr size_t kScratchClearBytes = (size_t)64 << 10;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+__global__ void __launch_bounds__(256) scratch_clear_kernel(uint4* p, unsigned n) {
+  for (unsigned i = blockIdx.x * 256u + threadIdx.x; i < n; i += gridDim.x * 256u)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up (and its counters
+// cleared, stream-ordered before the caller's kernels) on the device's
+// first call.
+static int scratch_for_device(void** out, hipStream_t s) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("sdpa_dual_v_noalloc: hipGetDevice failed (%s, device %d)",
+              hipGetErrorString(e), dev);
+    return MOTIF_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("sdpa_dual_v_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return MOTIF_ERR_HIP;
+    }
+    const unsigned n = (unsigned)(kScratchClearBytes / sizeof(uint4));
+    hipLaunchKernelGGL(scratch_clear_kernel, dim3(16), dim3(256), 0, s, (uint4*)p, n);
+    const int rc = check_launch("sdpa_dual_v_noalloc (scratch clear)");
+    if (rc != MOTIF_OK) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOTIF_OK;
+}
+
 static int gda_columns(int gr) { return gr + 1 <= 2 ? 2 : gr + 1 <= 4 ? 4 : gr + 1 <= 8 ? 8 : 16; }
 
 }  // namespace motif
@@ -466,6 +517,31 @@ int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* 
                       float scale, void* workspace, size_t workspace_bytes, void* stream) {
   return sdpa_fp_run("sdpa_dual_v", q, k, v1, v2, y, dtype, B, Hq, Hkv, 1, D, kv_cap, kv_len, 0,
                      scale, workspace, workspace_bytes, stream);
+}
+
+int motif_sdpa_dual_v_noalloc(const void* q, const void* k, const void* v1, const void* v2,
+                              void* y, int dtype, int B, int Hq, int Hkv, int D, int kv_cap,
+                              int kv_len, float scale, void* stream) {
+  CallScope scope;
+  clear_error();
+  // Size first (host arithmetic only): a call that needs more than the
+  // static scratch is refused before any HIP call.
+  const size_t need = motif_sdpa_workspace_bytes(B, Hq, Hkv, 1, kv_len, D);
+  if (need > kNoAllocScratchBytes || motif_sdpa_counter_bytes(B, Hq, Hkv, 1) > kScratchClearBytes) {
+    set_error("sdpa_dual_v_noalloc: this call needs %zu bytes of scratch (%zu bytes of "
+              "counters); the static scratch holds %zu (%zu of counters): use "
+              "motif_sdpa_dual_v with a workspace",
+              need, motif_sdpa_counter_bytes(B, Hq, Hkv, 1), kNoAllocScratchBytes,
+              kScratchClearBytes);
+    return MOTIF_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_for_device(&ws, (hipStream_t)stream);
+    if (rc != MOTIF_OK) return rc;
+  }
+  return sdpa_fp_run("sdpa_dual_v_noalloc", q, k, v1, v2, y, dtype, B, Hq, Hkv, 1, D, kv_cap,
+                     kv_len, 0, scale, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
 int motif_sdpa_dual_v_rows(const void* q, const void* k, const void* v1, const void* v2, void* y,

@@ -43,6 +43,10 @@ _SIGNATURES = {
         _c_int,
         [_vp] * 5 + [_c_int] * 7 + [_c_f, _vp, _c_sz, _vp],
     ),
+    "motif_sdpa_dual_v_noalloc": (
+        _c_int,
+        [_vp] * 5 + [_c_int] * 7 + [_c_f, _vp],
+    ),
     "motif_sdpa_dual_v_rows": (
         _c_int,
         [_vp] * 5 + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],

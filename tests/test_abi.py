@@ -167,3 +167,19 @@ def test_tuning_changes_while_other_threads_size_calls():
     assert seen <= {default, forced}, seen
     assert lib.motif_sdpa_workspace_bytes(*args) == default
 
+
+def test_noalloc_refuses_calls_past_its_scratch_before_the_gpu():
+    """motif_sdpa_dual_v_noalloc sizes the call on the host first: one that
+    needs more than the static scratch is refused with no HIP call."""
+    lib = _native.lib()
+    _native.set_tuning("rows_per_split", 16)  # 256 splits per KV head, B=8: about 66 MB
+    try:
+        st = lib.motif_sdpa_dual_v_noalloc(1, 1, 1, 1, 1, 0, 8, 32, 8, 128, 16128, 16000, 0.1,
+                                           None)
+        msg = _err()
+    finally:
+        _native.set_tuning("rows_per_split", 0)
+    assert st == _native.MOTIF_ERR_WORKSPACE and "static scratch holds 8388608" in msg
+    # more B*Hq rows than counters the scratch clears
+    st = lib.motif_sdpa_dual_v_noalloc(1, 1, 1, 1, 1, 0, 1024, 32, 8, 128, 64, 64, 0.1, None)
+    assert st == _native.MOTIF_ERR_WORKSPACE and "counters" in _err()
