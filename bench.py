@@ -30,6 +30,8 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import csv
+import hashlib
 import json
 import os
 import pathlib
@@ -275,8 +277,19 @@ def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hk
     return [mk(*s) for s in sets], (q, sets)
 
 
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline():
-    """The oracle's C/OpenMP port timed on the host: one full fp16 call."""
+    """The oracle's C/OpenMP port timed on the host: one full fp16 call and
+    one full q4 call, on every OpenMP thread and on one thread."""
     import numpy as np
 
     from oracle import c_oracle
@@ -284,34 +297,92 @@ def cpu_baseline():
     rng = np.random.default_rng(99)
     q = rng.standard_normal((B, HQ, 1, D)).astype(np.float16)
     k, v1, v2 = (rng.standard_normal((B, HKV, CAP, D)).astype(np.float16) for _ in range(3))
+    trips = [c_oracle.quantize_f16(t, GS, 4) for t in (k, v1, v2)]
     threads = c_oracle.max_threads()
-    times = []
-    for i in range(7):
-        t0 = time.perf_counter()
-        c_oracle.sdpa_dual_v_f16(q, k, v1, v2, 1 / np.sqrt(D), KV_LEN, nthreads=threads)
-        t1 = time.perf_counter()
-        if i >= 2:
-            times.append((t1 - t0) * 1e6)
-    us = statistics.median(times)
+    scale = 1 / np.sqrt(D)
+
+    def median_us(fn, reps):
+        times = []
+        for i in range(reps + 2):
+            t0 = time.perf_counter()
+            fn()
+            t1 = time.perf_counter()
+            if i >= 2:
+                times.append((t1 - t0) * 1e6)
+        return statistics.median(times)
+
+    f16 = lambda n: c_oracle.sdpa_dual_v_f16(q, k, v1, v2, scale, KV_LEN, nthreads=n)  # noqa: E731
+    q4 = lambda n: c_oracle.sdpa_dual_v_q_f16(q, *trips, scale, GS, 4, KV_LEN,  # noqa: E731
+                                              nthreads=n)
+    us = median_us(lambda: f16(threads), 5)
+    us_q4 = median_us(lambda: q4(threads), 5)
+    us_1 = median_us(lambda: f16(1), 3)
+    us_q4_1 = median_us(lambda: q4(1), 3)
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
     return {
         "value": round(us, 1),
         "unit": "us/call",
         "cores": threads,
         "kind": "port",
-        "sample": "one full fp16 sdpa_dual_v call (32 heads x 16000 rows, D 128) of the "
-                  "C/OpenMP port oracle/motif_oracle.c, median of 5 after 2 warm-ups",
+        "sample": "one full sdpa_dual_v call (32 heads x 16000 rows, D 128) of the C/OpenMP "
+                  "port oracle/motif_oracle.c (gcc -O2, scalar), fp16 cache (value) and q4 "
+                  "cache, on `cores` OpenMP threads (median of 5 after 2 warm-ups) and on one "
+                  "thread (median of 3)",
         "gbps": round(alg_bytes("f16") / us / 1e3, 2),
+        "one_thread_us": round(us_1, 1),
+        "q4_us": round(us_q4, 1),
+        "q4_gbps": round(alg_bytes("q4") / us_q4 / 1e3, 2),
+        "q4_one_thread_us": round(us_q4_1, 1),
+        "cpu_model": _cpu_model(),
+        "nproc": os.cpu_count(),
+        "affinity_cpus": affinity,
     }
 
 
-def load_traffic(name: str):
-    p = ROOT / "profiles" / f"traffic_{name}.json"
-    if p.is_file():
-        try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            return None
-    return None
+# Files whose content decides the kernels' code: a traffic profile records
+# their digest, and the JSON line says whether the tree it runs from matches.
+SOURCE_GLOBS = ("mlx-motif_amd/csrc/*.hip", "mlx-motif_amd/csrc/*.hpp",
+                "mlx-motif_amd/csrc/Makefile", "include/motif_hip.h")
+
+
+def sources_digest() -> str:
+    h = hashlib.sha256()
+    for p in sorted({f for g in SOURCE_GLOBS for f in ROOT.glob(g)}):
+        h.update(p.relative_to(ROOT).as_posix().encode() + b"\0" + p.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def load_traffic(kind: str):
+    """HBM bytes per call from profiles/traffic_sdpa_dual_v_<kind>_kv16000.json
+    (two rocprofv3 --pmc passes, summarised by --summarize-traffic), with the
+    commit and source digest it was measured at."""
+    p = ROOT / "profiles" / f"traffic_sdpa_dual_v_{kind}_kv16000.json"
+    try:
+        prof = json.loads(p.read_text())
+    except (OSError, ValueError):
+        return None
+    return {"bytes": prof.get("hbm_bytes_per_launch"), "file": p.relative_to(ROOT).as_posix(),
+            "commit": prof.get("commit"),
+            "matches_sources": prof.get("sources_digest") == sources_digest()}
+
+
+def roofline(kind: str, r: dict, basis: str) -> dict:
+    prof = load_traffic(kind)
+    return {
+        "bound": "hbm",
+        "achieved": r["gbps"],
+        "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s",
+        "frac": round(r["gbps"] / PEAK_HBM_GBPS, 4),
+        "traffic": prof["bytes"] if prof else None,
+        "traffic_profile": None if prof is None else {
+            "file": prof["file"], "commit": prof["commit"],
+            "matches_sources": prof["matches_sources"]},
+        "basis": basis,
+    }
 
 
 def main() -> int:
@@ -329,7 +400,12 @@ def main() -> int:
                     help="counter pass: one 256 MiB copy, then 16 eager decode calls on the "
                          "given cache (default f16), or 6 prefill-chunk calls (512 rows over "
                          "3716, fp16); no timing, no JSON; run under rocprofv3 --pmc")
+    ap.add_argument("--summarize-traffic", nargs=3, metavar=("KIND", "FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic_sdpa_dual_v_<KIND>_kv16000.json from the CSV "
+                         "directories of the FETCH_SIZE and WRITE_SIZE passes (no GPU)")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        return summarize_traffic(*args.summarize_traffic)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -368,6 +444,8 @@ def main() -> int:
         run_extra(torch, lib, dev, args)
 
     f16 = res["f16"]
+    basis = ("algorithmic bytes / us per call; a call is the attention launch plus the "
+             "split-merge launch (HIP events around graph-replayed calls)")
     out = {
         "metric": METRIC,
         "value": f16["us_per_call"],
@@ -392,18 +470,10 @@ def main() -> int:
         },
         "gbps": f16["gbps"],
         "pct_peak": f16["pct_peak"],
-        "q4": dict(res["q4"], traffic=load_traffic("sdpa_dual_v_q4_kv16000")),
-        "q8": res["q8"],
-        "roofline": {
-            "bound": "hbm",
-            "achieved": f16["gbps"],
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(f16["gbps"] / PEAK_HBM_GBPS, 4),
-            "traffic": load_traffic("sdpa_dual_v_f16_kv16000"),
-            "basis": "algorithmic bytes / us per call; a call is the attention launch "
-                     "plus the split-merge launch (HIP events around graph-replayed calls)",
-        },
+        "q4": dict(res["q4"], roofline=roofline("q4", res["q4"], basis)),
+        "q8": dict(res["q8"], roofline=roofline("q8", res["q8"], basis)),
+        "roofline": roofline("f16", f16, basis),
+        "sources_digest": sources_digest(),
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
     print(json.dumps(out), flush=True)
@@ -437,6 +507,76 @@ def traffic_pass(torch, lib, dev, kind: str = "f16") -> int:
     torch.cuda.synchronize()
     log(f"traffic pass: copy 268435456 B + 16 {kind} decode calls of {alg_bytes(kind)} B")
     del calls, keep
+    return 0
+
+
+def summarize_traffic(kind: str, fetch_dir: str, write_dir: str) -> int:
+    """Writes profiles/traffic_sdpa_dual_v_<kind>_kv16000.json from the CSV
+    output of the two counter passes over ``bench.py --traffic <kind>``:
+    per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the attention and merge
+    kernels, scaled by what the same counters read for the 256 MiB copy."""
+    import subprocess
+    from collections import defaultdict
+
+    def per_kernel(d: str):
+        vals = defaultdict(list)
+        files = sorted(pathlib.Path(d).rglob("*counter_collection.csv"))
+        if not files:
+            raise SystemExit(f"no *counter_collection.csv under {d}")
+        for row in csv.DictReader(open(files[0])):
+            vals[row["Kernel_Name"]].append(float(row["Counter_Value"]))
+        return vals
+
+    F, W = per_kernel(fetch_dir), per_kernel(write_dir)
+    copy = next(k for k in F if "copyBuffer" in k)
+    ff, wf = 262144.0 / F[copy][0], 262144.0 / W[copy][0]
+    att = next(k for k in F if "sdpa_" in k and "merge" not in k)
+    mer = next(k for k in F if "sdpa_merge" in k)
+    mean = lambda v: sum(v) / len(v)  # noqa: E731
+    rd = round((mean(F[att]) + mean(F[mer])) * ff * 1024)
+    wr = round((mean(W[att]) + mean(W[mer])) * wf * 1024)
+    alg = alg_bytes(kind)
+    try:
+        commit = subprocess.run(["git", "rev-parse", "--short", "HEAD"], cwd=ROOT,
+                                capture_output=True, text=True, check=True).stdout.strip()
+        dirty = bool(subprocess.run(["git", "status", "--porcelain", "--"] + list(SOURCE_GLOBS),
+                                    cwd=ROOT, capture_output=True, text=True).stdout.strip())
+    except (OSError, subprocess.CalledProcessError):
+        commit, dirty = "unknown", None
+    flag = "" if kind == "f16" else f" {kind}"
+    out = {
+        "workload": "B=1, 32 q-heads over 8 KV heads, head_dim 128, kv_len 16000, cap 16128"
+                    + ("" if kind == "f16" else f"; {kind}, group_size 64"),
+        "commit": commit, "sources_dirty": dirty, "sources_digest": sources_digest(),
+        "commands": [
+            f"timeout -s KILL 120 rocprofv3 --pmc FETCH_SIZE --output-format csv -d {fetch_dir} "
+            f"-o fetch -- python3 bench.py --traffic{flag}",
+            f"timeout -s KILL 120 rocprofv3 --pmc WRITE_SIZE --output-format csv -d {write_dir} "
+            f"-o write -- python3 bench.py --traffic{flag}",
+            f"python3 bench.py --summarize-traffic {kind} {fetch_dir} {write_dir}"],
+        "calibration": {"kernel": copy.split("(")[0] + " (torch copy_ of 268435456 B)",
+                        "fetch_kib": F[copy][0], "write_kib": W[copy][0],
+                        "expected_kib": 262144, "fetch_factor": round(ff, 5),
+                        "write_factor": round(wf, 5)},
+        "dispatches_per_kernel": len(F[att]),
+        "attention_kernel": {"name": att, "fetch_kib": round(mean(F[att]), 1),
+                             "write_kib": round(mean(W[att]), 1),
+                             "read_bytes": round(mean(F[att]) * ff * 1024),
+                             "write_bytes": round(mean(W[att]) * wf * 1024)},
+        "merge_kernel": {"name": mer, "fetch_kib": round(mean(F[mer]), 1),
+                         "write_kib": round(mean(W[mer]), 1),
+                         "read_bytes": round(mean(F[mer]) * ff * 1024),
+                         "write_bytes": round(mean(W[mer]) * wf * 1024)},
+        "hbm_read_bytes_per_launch": rd, "hbm_write_bytes_per_launch": wr,
+        "hbm_bytes_per_launch": rd + wr, "algorithmic_bytes_per_launch": alg,
+        "traffic_over_algorithmic": round((rd + wr) / alg, 4),
+        "note": "per call (attention + merge kernel). Above the algorithmic bytes: the split "
+                "partials (32 virtual heads x 32 splits x 258 floats = 1.06 MB) written by the "
+                "attention kernel and read back once by the merge kernel.",
+    }
+    dst = ROOT / "profiles" / f"traffic_sdpa_dual_v_{kind}_kv16000.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    log(f"{dst.name}: {rd + wr} B per call, {out['traffic_over_algorithmic']}x algorithmic")
     return 0
 
 

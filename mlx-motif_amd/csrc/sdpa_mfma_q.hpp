@@ -417,9 +417,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) qraw[bb][s] = *reinterpret_cast<const uint4*>(qp + 8 * s);
   }
-  // Keep the q loads ahead of the tile loads: the q RoPE below then waits for
-  // q alone, not for the first tiles too.
-  __builtin_amdgcn_sched_barrier(0);
+  // Fused step: keep the q loads ahead of the tile loads, so the q RoPE below
+  // waits for q alone, not for the first tiles too.
+  if constexpr (DUAL) __builtin_amdgcn_sched_barrier(0);
   load_tiles(ta, k0);
   if constexpr (DUAL) {
     if (a.from_proj) {
