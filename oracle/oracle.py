@@ -84,7 +84,21 @@ def round_to(x, dtype: str) -> np.ndarray:
 # ------------------------------------------------------------ quantizer ---
 
 
-def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "f16"):
+def _round_ties(t: np.ndarray, ties: str) -> np.ndarray:
+    """Round float32 t to integers: ``"even"`` is round-half-even (rint);
+    ``"away"`` sends exact halves away from zero (C ``round``).  Only exact
+    halves differ; they are found as t - trunc(t) == +-0.5, which is exact in
+    float32."""
+    r = np.rint(t).astype(np.float32)
+    if ties == "even":
+        return r
+    assert ties == "away", ties
+    f = np.trunc(t).astype(np.float32)
+    half = np.abs(t - f) == np.float32(0.5)
+    return np.where(half, f + np.sign(t), r).astype(np.float32)
+
+
+def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "f16", ties: str = "even"):
     """MLX affine quantisation of the last axis (what ``mx.quantize`` computes
     for cache.py:498 and cache.py:399-402), in float32 step by step:
 
@@ -94,6 +108,10 @@ def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "f16"):
         edge   = side ? min : max;  q0 = rint(edge / scale)
         if q0 != 0: scale = edge / q0; bias = edge   else bias = 0
         code   = clamp(rint((w - bias) / scale), 0, n_bins)
+
+    ``ties`` picks the rounding of exact halves in both rint steps: "even"
+    (the default, MLX's CPU quantizer) or "away" (C ``round``), so tests can
+    bound what an unknown tie rule would change.
 
     Returns (data uint32 (..., D*bits/32), scales, biases (..., D/gs)) with
     scales/biases rounded to ``out_dtype``.  Codes are packed little-endian:
@@ -112,12 +130,12 @@ def quantize(w, group_size: int = 64, bits: int = 4, out_dtype: str = "f16"):
     side = np.abs(w_min) > np.abs(w_max)
     scale = np.where(side, scale, -scale).astype(np.float32)
     edge = np.where(side, w_min, w_max).astype(np.float32)
-    q0 = np.rint(edge / scale).astype(np.float32)
+    q0 = _round_ties((edge / scale).astype(np.float32), ties)
     nz = q0 != 0
     safe_q0 = np.where(nz, q0, np.float32(1)).astype(np.float32)
     scale = np.where(nz, edge / safe_q0, scale).astype(np.float32)
     bias = np.where(nz, edge, np.float32(0)).astype(np.float32)
-    codes = np.rint((x - bias[..., None]) / scale[..., None]).astype(np.float32)
+    codes = _round_ties(((x - bias[..., None]) / scale[..., None]).astype(np.float32), ties)
     codes = np.clip(codes, np.float32(0), n_bins).astype(np.uint32)
     codes = codes.reshape(-1, D // el, el)
     words = np.zeros(codes.shape[:-1], dtype=np.uint32)

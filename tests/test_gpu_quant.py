@@ -85,6 +85,25 @@ def test_quantize_special_groups(gpu):
         assert np.array_equal(torch_to_np(b), rb.astype(np.float64), equal_nan=True), bits
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("unit", [1.0, 0.25])
+def test_quantize_exact_ties_half_to_even(gpu, bits, unit):
+    """Groups whose codes all land on exact halves (tests/test_quant_ties.py
+    builds them and writes the codes out): the GPU kernel resolves every tie
+    to even, as the numpy and C oracles and the torch statement do."""
+    import torch
+
+    from mlx_motif.kernels import quantize
+    from test_quant_ties import tie_groups
+
+    x, even, _ = tie_groups(bits, unit)
+    d, s, b = quantize(np_to_torch(x, torch.float16, gpu), group_size=64, bits=bits)
+    assert np.array_equal(O.unpack_codes(torch_to_np(d).astype(np.uint32), bits), even)
+    rd, rs, rb = O.quantize(x, 64, bits)
+    assert np.array_equal(torch_to_np(d), rd)
+    assert _bits_equal(s, rs, "f16") and _bits_equal(b, rb, "f16")
+
+
 def _cache_steps(rng, B, H, D, sizes, tag="f16"):
     return [tuple(randn(rng, (B, H, S, D), tag) for _ in range(4)) for S in sizes]
 
