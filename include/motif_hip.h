@@ -387,7 +387,11 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * last workgroup to finish combines them inside the attention launch),
  * "qpair" (packed caches at head_dim 128, group size 64/128: 1, the
  * default, decodes 4-bit caches with the paired-tile kernel; 2 also 8-bit
- * caches; 0 keeps the per-tile kernel for both),
+ * caches; 0 keeps the per-tile kernel for both), "qslab" (packed-cache
+ * verify slabs of 17..64 virtual heads per KV head: 1, the default, runs 8-bit
+ * slabs on the kernel that dequantises each tile once into LDS; 2 also
+ * 4-bit slabs; 0 neither), "waves_per_wg" 4 also selects that kernel's
+ * 4-wave variant,
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
  * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.

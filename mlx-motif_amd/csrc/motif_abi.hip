@@ -170,6 +170,37 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   return p;
 }
 
+QSlabPlan plan_qslab(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
+  QSlabPlan p{};
+  const int G = Hkv > 0 ? Hq / Hkv : 1;
+  const int GV = G * S_q;
+  p.ncb = GV <= 32 ? 2 : 4;
+  p.nchunk = (GV + 16 * p.ncb - 1) / (16 * p.ncb);
+  p.waves = tuning().waves_per_wg == 4 ? 4 : 8;
+  const int step = 32 * (p.waves / p.ncb);  // rows per step of the workgroup
+  const long units = (long)B * Hkv * p.nchunk;
+  const int rows = kv_len > 0 ? kv_len : 1;
+  const int cus = tuning().min_wgs > 0 ? tuning().min_wgs : device_cu_count();
+  int nsplit = units >= cus ? 1 : (int)((cus + units - 1) / units);
+  const int max_split = (rows + step - 1) / step;  // at least one step each
+  if (nsplit > max_split) nsplit = max_split;
+  if (nsplit > kMaxSplits) nsplit = kMaxSplits;
+  if (nsplit < 1) nsplit = 1;
+  int rps = (int)round_up((size_t)((rows + nsplit - 1) / nsplit), (size_t)step);
+  if (tuning().rows_per_split > 0) rps = (int)round_up((size_t)tuning().rows_per_split, (size_t)step);
+  const int min_rps = (rows + kMaxSplits - 1) / kMaxSplits;
+  if (rps < min_rps) rps = (int)round_up((size_t)min_rps, (size_t)step);
+  p.rows_per_split = rps;
+  p.nsplit = (rows + rps - 1) / rps;
+  if (p.nsplit < 1) p.nsplit = 1;
+  const size_t vrows = (size_t)B * Hq * S_q;
+  p.workspace_bytes = round_up(vrows * sizeof(unsigned), 256);
+  if (p.nsplit > 1)
+    p.workspace_bytes += round_up(vrows * p.nsplit * 2 * D * sizeof(float), 256) +
+                         round_up(vrows * p.nsplit * 2 * sizeof(float), 256);
+  return p;
+}
+
 }  // namespace motif
 
 using namespace motif;
@@ -206,6 +237,11 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
     if ((Hq / Hkv) * S_q >= kPrefillMinHeads) {
       const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
       if (pp.workspace_bytes > ws) ws = pp.workspace_bytes;
+    }
+    const int gv = (Hq / Hkv) * S_q;
+    if (gv >= kQSlabMinHeads && gv <= kQSlabMaxHeads) {
+      const QSlabPlan qp = plan_qslab(B, Hq, Hkv, S_q, kv_len, D);
+      if (qp.workspace_bytes > ws) ws = qp.workspace_bytes;
     }
   }
   return ws;
@@ -249,6 +285,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.qpair = value; });
+  } else if (!strcmp(key, "qslab")) {
+    if (value < 0 || value > 2) {
+      set_error("motif_set_tuning: qslab must be 0, 1 or 2");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.qslab = value; });
   } else if (!strcmp(key, "poly_rows")) {
     update_tuning([&](Tuning& t) { t.poly_rows = value; });
   } else {

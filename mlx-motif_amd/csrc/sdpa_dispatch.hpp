@@ -25,6 +25,12 @@ int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, h
 int launch_sdpa_qpair(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
                       hipStream_t s);
 
+// Packed cache (fp16 scales, head dim 128), a verify slab of 17..64 virtual
+// heads per KV head: tiles dequantised once per workgroup into LDS
+// (sdpa_qslab.hip); ncb column blocks of 16 heads (2 or 4), 4 or 8 waves.
+int launch_sdpa_qslab(const SdpaArgs& a, int bits, int gs, int ncb, int waves, int nblocks,
+                      hipStream_t s);
+
 // Split merge (second launch when a.fused_merge == 0 and nsplit > 1) for
 // outputs of the given element type.
 int launch_sdpa_merge_f16(const SdpaArgs& a, int D, hipStream_t s);

@@ -121,6 +121,23 @@ struct PrefillPlan {
 };
 PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
 
+// Plan of the packed-cache slab kernel (sdpa_qslab.hpp): ncb column blocks of
+// 16 virtual heads per workgroup (2 when the heads of a KV head fit 32
+// columns, else 4), nchunk head chunks of ncb * 16, and the rows of a KV head
+// split so that about one workgroup per CU runs; each split is a whole
+// number of steps (waves / ncb tiles of 32 rows).  Used for packed
+// caches at head_dim 128 when a KV head has more than 16 and at most
+// kQSlabMaxHeads virtual heads.
+constexpr int kQSlabMinHeads = 17;
+constexpr int kQSlabMaxHeads = 64;
+struct QSlabPlan {
+  int ncb, nchunk;
+  int waves;  // 8 (two per SIMD, one LDS stage) or 4 (tuning waves_per_wg 4)
+  int nsplit, rows_per_split;
+  size_t workspace_bytes;  // counters + partials
+};
+QSlabPlan plan_qslab(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
+
 // The matrix-core decode kernels deal 16-row tiles of a whole KV head to
 // their splits and address them with 32-bit byte offsets from the head's
 // first row: they take kv_len <= kMfmaMaxRows (the VALU kernels take the

@@ -91,6 +91,144 @@ __device__ inline bool prefill_block_coords(const SdpaArgs& a, int bid, int& qbl
   return true;
 }
 
+// One column's online-softmax state over 32-row fp16/bf16 K/V tiles held in
+// LDS with 16-byte chunk c of row r at byte r * 256 + (c ^ (r % 16)) * 16:
+// S^T = K Q^T (16x16x32 MFMA, two 16-row halves), scores in log2 units with
+// lazy rescaling, O^T = V^T P^T over the 32 rows.  Lane (col, blk) of a wave
+// owns column col; acc[j][r] ends as channel 32*blk + 4*j + r.
+template <typename T>
+struct SwizzledTileAcc {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
+  floatx4 acc1[8], acc2[8], accl;
+  float m_run;
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc1[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    accl = floatx4{0.f, 0.f, 0.f, 0.f};
+    m_run = kNegSentinel;
+  }
+
+  // Rows row0 + 16*h + 4*blk + r of the tile hold k index 8*blk + 4*h + r of
+  // the PV products (as in the decode kernel); rows at or past r_end or lim
+  // are masked.
+  __device__ __forceinline__ void tile(const uint8_t* Kt, const uint8_t* V1t, const uint8_t* V2t,
+                                       const V8 (&qb)[4], int row0, int r_end, int lim,
+                                       float qscale, int col, int blk) {
+    floatx4 sacc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sacc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kr = 16 * h + col;
+        const V8 ka = __builtin_bit_cast(
+            V8, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
+        sacc[h] = Op::mma(ka, qb[s], sacc[h]);
+      }
+    }
+    float sc[8];
+    float mx = kNegSentinel;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = row0 + 16 * h + 4 * blk + r;
+        const bool ok = row < r_end && row < lim;
+        sc[4 * h + r] = ok ? sacc[h][r] * qscale : kNegSentinel;
+        mx = fmaxf(mx, sc[4 * h + r]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float fac = fast_exp2(m_run - m_new);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc1[j] *= fac;
+        acc2[j] *= fac;
+      }
+      accl *= fac;
+      m_run = m_new;
+    }
+    V8 pb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+
+    // V^T fragments straight from LDS with transposing reads
+    // (ds_read_b64_tr_b16).  In the 16-lane group of lanes with one blk,
+    // lane 4*jj + q points at 4 channels of row 16*h + 4*blk + jj, and group
+    // lane i receives element i % 4 of the 4 channels lane 4*jj + i/4
+    // pointed at, for jj = 0..3: four rows of one channel, the A fragment.
+    // MFMA j takes channels 32*q + 4*j .. +3 from lane 4*jj + q, so A row m
+    // is channel 32*(m/4) + 4*j + m%4 and a lane's results cover 32
+    // consecutive channels.
+    const int jj = col >> 2;
+    const int qq = col & 3;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint2 f1[2], f2[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int vr = 16 * h + 4 * blk + jj;
+        const int o = vr * 256 + (((4 * qq + j / 2) ^ (vr % 16)) * 16) + (j % 2) * 8;
+        f1[h] = lds_read_tr16(&V1t[o]);
+        f2[h] = lds_read_tr16(&V2t[o]);
+      }
+      const V8 a1 = __builtin_bit_cast(V8, make_uint4(f1[0].x, f1[0].y, f1[1].x, f1[1].y));
+      const V8 a2 = __builtin_bit_cast(V8, make_uint4(f2[0].x, f2[0].y, f2[1].x, f2[1].y));
+      acc1[j] = Op::mma(a1, pb, acc1[j]);
+      acc2[j] = Op::mma(a2, pb, acc2[j]);
+    }
+    const typename Op::S one = Op::from_f32(1.f);
+    const V8 ones = {one, one, one, one, one, one, one, one};
+    accl = Op::mma(ones, pb, accl);
+  }
+
+  // Column vrow's result: y (normalised, nsplit == 1) or its split partial.
+  __device__ __forceinline__ void store(const SdpaArgs& a, long vrow, int split, int blk) const {
+    constexpr int D = 128;
+    const float l = accl[0];
+    if (a.nsplit == 1) {
+      const float inv = l == 0.f ? 1.f : 1.f / l;  // o stays 0 when no key is visible
+      uint16_t* yp = (uint16_t*)a.y + vrow * 2 * D + 32 * blk;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {  // channels 32*blk + 8*p .. +7
+        uint32_t w1[4], w2[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int j = 2 * p + t / 2;
+          const int r = 2 * (t % 2);
+          w1[t] = (uint32_t)Elem<T>::from_f32(acc1[j][r] * inv) |
+                  ((uint32_t)Elem<T>::from_f32(acc1[j][r + 1] * inv) << 16);
+          w2[t] = (uint32_t)Elem<T>::from_f32(acc2[j][r] * inv) |
+                  ((uint32_t)Elem<T>::from_f32(acc2[j][r + 1] * inv) << 16);
+        }
+        *reinterpret_cast<uint4*>(yp + 8 * p) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+      }
+    } else {
+      const int ns = a.nsplit;
+      float* po = a.part_o + (vrow * ns + split) * 2 * D + 32 * blk;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        *reinterpret_cast<float4*>(po + 4 * j) =
+            make_float4(acc1[j][0], acc1[j][1], acc1[j][2], acc1[j][3]);
+        *reinterpret_cast<float4*>(po + D + 4 * j) =
+            make_float4(acc2[j][0], acc2[j][1], acc2[j][2], acc2[j][3]);
+      }
+      if (blk == 0)
+        *reinterpret_cast<float2*>(a.part_ml + (vrow * ns + split) * 2) = make_float2(m_run, l);
+    }
+  }
+};
+
 // The ring's LDS holds one workgroup per CU: two waves per SIMD at 8 waves,
 // one at 4.
 // T: half_t (fp16 cache) or bf16_t (bf16 cache, bf16 matrix cores).
@@ -167,91 +305,11 @@ sdpa_prefill_kernel(SdpaArgs a) {
     }
   };
 
-  floatx4 acc1[8], acc2[8], accl;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    acc1[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  }
-  accl = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegSentinel;
-  const typename Op::S one = Op::from_f32(1.f);
-  const V8 ones = {one, one, one, one, one, one, one, one};
-
-  // One 32-row tile from ring stage st: rows t0 + 16*h + 4*blk + r hold
-  // k index 8*blk + 4*h + r of the PV products (as in the decode kernel).
+  SwizzledTileAcc<T> st_acc;
+  st_acc.init();
   auto compute = [&](int st, int t0) {
-    const uint8_t* Kt = ring[st][0];
-    const uint8_t* V1t = ring[st][1];
-    const uint8_t* V2t = ring[st][2];
-    floatx4 sacc[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      sacc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int kr = 16 * h + col;
-        const V8 ka = __builtin_bit_cast(
-            V8, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
-        sacc[h] = Op::mma(ka, qb[s], sacc[h]);
-      }
-    }
-    float sc[8];
-    float mx = kNegSentinel;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = r_begin + t0 + 16 * h + 4 * blk + r;
-        const bool ok = row < r_end && row < lim;
-        sc[4 * h + r] = ok ? sacc[h][r] * a.qscale : kNegSentinel;
-        mx = fmaxf(mx, sc[4 * h + r]);
-      }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float fac = fast_exp2(m_run - m_new);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        acc1[j] *= fac;
-        acc2[j] *= fac;
-      }
-      accl *= fac;
-      m_run = m_new;
-    }
-    V8 pb;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
-
-    // V^T fragments straight from the ring with transposing LDS reads
-    // (ds_read_b64_tr_b16).  In the 16-lane group of lanes with one blk,
-    // lane 4*jj + q points at 4 channels of row 16*h + 4*blk + jj, and group
-    // lane i receives element i % 4 of the 4 channels lane 4*jj + i/4
-    // pointed at, for jj = 0..3: four rows of one channel, the A fragment.
-    // MFMA j takes channels 32*q + 4*j .. +3 from lane 4*jj + q, so A row m
-    // is channel 32*(m/4) + 4*j + m%4 and a lane's results cover 32
-    // consecutive channels.
-    const int jj = col >> 2;
-    const int qq = col & 3;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      uint2 f1[2], f2[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int vr = 16 * h + 4 * blk + jj;
-        const int o = vr * 256 + (((4 * qq + j / 2) ^ (vr % 16)) * 16) + (j % 2) * 8;
-        f1[h] = lds_read_tr16(&V1t[o]);
-        f2[h] = lds_read_tr16(&V2t[o]);
-      }
-      const V8 a1 = __builtin_bit_cast(V8, make_uint4(f1[0].x, f1[0].y, f1[1].x, f1[1].y));
-      const V8 a2 = __builtin_bit_cast(V8, make_uint4(f2[0].x, f2[0].y, f2[1].x, f2[1].y));
-      acc1[j] = Op::mma(a1, pb, acc1[j]);
-      acc2[j] = Op::mma(a2, pb, acc2[j]);
-    }
-    accl = Op::mma(ones, pb, accl);
+    st_acc.tile(ring[st][0], ring[st][1], ring[st][2], qb, r_begin + t0, r_end, lim, a.qscale,
+                col, blk);
   };
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
@@ -283,37 +341,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
 
   // acc[j][r] of lane (col, blk) is channel 32*blk + 4*j + r of column col.
   if (!col_ok) return;
-  const long vrow = qrow0 + vh;
-  const float l = accl[0];
-  if (a.nsplit == 1) {
-    const float inv = l == 0.f ? 1.f : 1.f / l;  // o stays 0 when no key is visible
-    uint16_t* yp = (uint16_t*)a.y + vrow * 2 * D + 32 * blk;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {  // channels 32*blk + 8*p .. +7
-      uint32_t w1[4], w2[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int j = 2 * p + t / 2;
-        const int r = 2 * (t % 2);
-        w1[t] = (uint32_t)Elem<T>::from_f32(acc1[j][r] * inv) |
-                ((uint32_t)Elem<T>::from_f32(acc1[j][r + 1] * inv) << 16);
-        w2[t] = (uint32_t)Elem<T>::from_f32(acc2[j][r] * inv) |
-                ((uint32_t)Elem<T>::from_f32(acc2[j][r + 1] * inv) << 16);
-      }
-      *reinterpret_cast<uint4*>(yp + 8 * p) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-      *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-    }
-  } else {
-    const int ns = a.nsplit;
-    float* po = a.part_o + (vrow * ns + split) * 2 * D + 32 * blk;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      *reinterpret_cast<float4*>(po + 4 * j) = make_float4(acc1[j][0], acc1[j][1], acc1[j][2], acc1[j][3]);
-      *reinterpret_cast<float4*>(po + D + 4 * j) = make_float4(acc2[j][0], acc2[j][1], acc2[j][2], acc2[j][3]);
-    }
-    if (blk == 0)
-      *reinterpret_cast<float2*>(a.part_ml + (vrow * ns + split) * 2) = make_float2(m_run, l);
-  }
+  st_acc.store(a, qrow0 + vh, split, blk);
 }
 
 template <typename T>

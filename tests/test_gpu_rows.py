@@ -77,7 +77,8 @@ def test_rows_single_row_equals_decode(gpu, rng):
 @pytest.mark.parametrize("S,cap,kv_len", [(5, 512, 400), (3, 256, 3), (4, 512, 300)])
 def test_rows_packed(gpu, rng, bits, S, cap, kv_len):
     """S x GQA 4 virtual heads: 12 and 16 take the two-column-block kernel
-    (one workgroup per KV head and split), 20 three head chunks."""
+    (one workgroup per KV head and split), 20 the slab kernel for q8 (tiles
+    dequantised into LDS once per workgroup) and three head chunks for q4."""
     from mlx_motif.kernels import sdpa_dual_v_q4_rows
 
     q = randn(rng, (1, 32, S, 128), "f16")
