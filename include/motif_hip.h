@@ -202,6 +202,39 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
                       int origin_first, void* stream);
 
 /* ------------------------------------------------------------------------ *
+ * A GDA layer's prefill chunk from the projection outputs, in one attention
+ * launch (plus the split merge when its rows are split).  Replaces, for a
+ * chunk of S tokens at cache offset `offset`, the rope calls on q and k
+ * (src/mlx_motif/model.py:590-594), the 4-slot split with
+ * update_and_fetch_4 (model.py:620-629, cache.py:337) and the four
+ * mx.fast.scaled_dot_product_attention calls of the k_ratio-1 fallback with
+ * the causal mask (model.py:769-797), whose outputs feed gda_post_split.
+ *   q_proj (B, S, q_groups*(gr+1)*D): heads g*(gr+1)+j (origin j < gr,
+ *          noise j = gr), or with origin_first the q_groups*gr origin heads
+ *          first
+ *   k_proj (B, S, 2*k_groups*D): k1[g] = head 2g, k2[g] = head 2g+1
+ *   v_proj (B, S, 2*k_groups*D): v1[g] = head 2g, v2[g] = head 2g+1
+ *   k1, k2, v1, v2 (B, k_groups, kv_cap, D): the 4-slot fp cache; rows
+ *          offset .. offset + S - 1 are written (k roped)
+ *   y_origin (B, q_groups*gr, S, 2D) = [softmax(q1 k1^T) V1 || .. V2]
+ *   y_noise  (B, q_groups, S, 2D)    = the same for q2 over k2
+ * q and k are roped at positions offset + s exactly as motif_rope_split4
+ * rounds them, so the cache rows equal its output bit for bit.  Query row
+ * s sees cache rows [0, offset + s] (bottom-right causal).  fp32
+ * accumulation.  q_groups % k_groups == 0.  fp16/bf16 at D = 128 only;
+ * other shapes return MOTIF_ERR_UNSUPPORTED (compose motif_rope_split4 and
+ * motif_sdpa_dual_v_rows).  workspace: motif_gda_prefill_workspace_bytes
+ * (0 when the rows are not split).
+ * ------------------------------------------------------------------------ */
+size_t motif_gda_prefill_workspace_bytes(int B, int S, int q_groups, int gr, int k_groups, int D,
+                                         int kv_len);
+int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                           void* k2, void* v1, void* v2, void* y_origin, void* y_noise, int dtype,
+                           int B, int S, int q_groups, int gr, int k_groups, int D, int kv_cap,
+                           int offset, float scale, float theta, int origin_first,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ *
  * MLX affine quantisation (mx.quantize, mode "affine") of `rows` rows of D
  * values: data (rows, D*bits/32) uint32, scales/biases (rows, D/group_size)
  * in dtype.  The reference calls mx.quantize at cache.py:498 and

@@ -1,5 +1,6 @@
 // C-ABI plumbing shared by every entry point: thread-local error messages,
 // tuning knobs, device queries and the split-KV launch plan.
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -165,6 +166,42 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
     const size_t vrows = (size_t)B * Hq * S_q;
     p.workspace_bytes = round_up(vrows * sizeof(unsigned), 256) +
                         round_up(vrows * p.nsplit * 2 * D * sizeof(float), 256) +
+                        round_up(vrows * p.nsplit * 2 * sizeof(float), 256);
+  }
+  return p;
+}
+
+GdaPrefillPlan plan_gda_prefill(int B, int Hkv, int G_origin, int G_noise, int S, int kv_len) {
+  GdaPrefillPlan p{};
+  p.waves = G_origin * S >= 512 ? 8 : 4;  // as plan_prefill
+  if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
+  const int cols = p.waves * 16;
+  p.nqb_origin = (G_origin * S + cols - 1) / cols;
+  p.nqb_noise = (G_noise * S + cols - 1) / cols;
+  const long units = (long)B * Hkv * (p.nqb_origin + p.nqb_noise);
+  const int cus = device_cu_count();
+  const int rows = kv_len > 0 ? kv_len : 1;
+  int nsplit = 1;
+  if (tuning().rows_per_split > 0) {
+    const int rps = (int)round_up((size_t)tuning().rows_per_split, kPrefillTileRowsHost);
+    nsplit = (rows + rps - 1) / rps;
+  } else if (units < cus / 2) {
+    // Workgroups hold one CU each (the LDS ring).  Rows are split only when
+    // the query blocks leave most CUs idle: with 160 blocks on 256 CUs (a
+    // 512-row chunk of 32 + 8 heads over 8 KV heads, 3716 rows) one split
+    // measured 178 us, 2 / 3 / 4 / 8 splits 229 / 198 / 222 / 255 us (the
+    // partials, the merge launch and a second round of workgroups).
+    nsplit = (int)std::min<long>((cus + units - 1) / units, std::max(1, (rows + 127) / 128));
+  }
+  if (nsplit > kMaxSplits) nsplit = kMaxSplits;
+  int rps = (rows + nsplit - 1) / nsplit;
+  rps = (int)round_up((size_t)rps, kPrefillTileRowsHost);
+  p.rows_per_split = rps;
+  p.nsplit = (rows + rps - 1) / rps;
+  if (p.nsplit > 1) {
+    const size_t vrows = (size_t)B * Hkv * (G_origin + G_noise) * S;
+    p.workspace_bytes = round_up(vrows * sizeof(unsigned), 256) +
+                        round_up(vrows * p.nsplit * 2 * 128 * sizeof(float), 256) +
                         round_up(vrows * p.nsplit * 2 * sizeof(float), 256);
   }
   return p;

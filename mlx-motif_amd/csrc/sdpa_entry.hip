@@ -830,3 +830,99 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
 }
 
 }  // extern "C"
+
+// ------------------------------------------ GDA prefill chunk from projections ---
+extern "C" {
+
+size_t motif_gda_prefill_workspace_bytes(int B, int S, int q_groups, int gr, int k_groups,
+                                         int D, int kv_len) {
+  if (B < 1 || S < 1 || q_groups < 1 || gr < 1 || k_groups < 1 || q_groups % k_groups != 0 ||
+      D != 128 || kv_len < S)
+    return 0;
+  CallScope scope;
+  const int G_o = q_groups * gr / k_groups, G_n = q_groups / k_groups;
+  return plan_gda_prefill(B, k_groups, G_o, G_n, S, kv_len).workspace_bytes;
+}
+
+int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                           void* k2, void* v1, void* v2, void* y_origin, void* y_noise, int dtype,
+                           int B, int S, int q_groups, int gr, int k_groups, int D, int kv_cap,
+                           int offset, float scale, float theta, int origin_first,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  CallScope scope;
+  clear_error();
+  const char* name = "gda_prefill_proj";
+  MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
+                "%s: unknown dtype code %d", name, dtype);
+  MOTIF_REQUIRE(B >= 1 && S >= 1, "%s: B and S must be >= 1", name);
+  MOTIF_REQUIRE(q_groups >= 1 && gr >= 1 && k_groups >= 1,
+                "%s: q_groups, gr and k_groups must be >= 1", name);
+  MOTIF_REQUIRE(q_groups % k_groups == 0, "%s: q_groups=%d must be a multiple of k_groups=%d",
+                name, q_groups, k_groups);
+  MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
+  MOTIF_REQUIRE(offset >= 0 && (long)offset + S <= kv_cap,
+                "%s: rows [%d, %d) must fit the cache capacity %d", name, offset, offset + S,
+                kv_cap);
+  MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  MOTIF_REQUIRE((long)B * k_groups * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
+  MOTIF_REQUIRE(q_proj && k_proj && v_proj && k1 && k2 && v1 && v2 && y_origin && y_noise,
+                "%s: null pointer", name);
+  const bool ok = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
+                  (long)S * 2 * k_groups * D * 2 < (1L << 31) && aligned(q_proj, 16) &&
+                  aligned(k_proj, 16) && aligned(v_proj, 16) && aligned(k1, 16) &&
+                  aligned(k2, 16) && aligned(v1, 16) && aligned(v2, 16) && aligned(y_origin, 16) &&
+                  aligned(y_noise, 16);
+  if (!ok) {
+    set_error("%s: no fused variant for this shape (dtype %d, D=%d); use motif_rope_split4 and "
+              "motif_sdpa_dual_v_rows", name, dtype, D);
+    return MOTIF_ERR_UNSUPPORTED;
+  }
+  const int kv_len = offset + S;
+  const int Hq_o = q_groups * gr;
+  const int G_o = Hq_o / k_groups, G_n = q_groups / k_groups;
+  const GdaPrefillPlan pp = plan_gda_prefill(B, k_groups, G_o, G_n, S, kv_len);
+  SdpaArgs a{};
+  a.q = q_proj;
+  a.k = k1; a.k2 = k2; a.v1 = v1; a.v2 = v2;
+  a.new_k1 = k_proj; a.new_v1 = v_proj;
+  a.y = y_origin;
+  a.y2 = y_noise;
+  a.B = B; a.Hq = Hq_o; a.Hkv = k_groups; a.S_q = S;
+  a.G = G_o; a.G2 = G_n; a.GV = G_o * S;
+  a.nchunk = pp.nqb_origin + pp.nqb_noise;
+  a.nqb_origin = pp.nqb_origin;
+  a.kv_cap = kv_cap; a.kv_len = kv_len; a.causal = 1;
+  a.nsplit = pp.nsplit; a.rows_per_split = pp.rows_per_split;
+  a.fused_merge = 0;
+  a.qscale = scale * 1.4426950408889634f;
+  a.q_groups = q_groups; a.q_gr = gr; a.q_origin_first = origin_first != 0;
+  a.rope_log2_theta = log2f(theta);
+  a.rope_pos0 = offset;
+  a.y2_row0 = (long)B * Hq_o * S;
+  if (pp.nsplit > 1) {
+    if (workspace == nullptr || workspace_bytes < pp.workspace_bytes) {
+      set_error("%s: workspace of %zu bytes needed, %zu given", name, pp.workspace_bytes,
+                workspace == nullptr ? (size_t)0 : workspace_bytes);
+      return MOTIF_ERR_WORKSPACE;
+    }
+    MOTIF_REQUIRE(aligned(workspace, 256), "%s: workspace must be 256-byte aligned", name);
+    const size_t vrows = (size_t)B * (Hq_o + q_groups) * S;
+    char* w = (char*)workspace;
+    const size_t cbytes = (vrows * sizeof(unsigned) + 255) / 256 * 256;
+    const size_t obytes = (vrows * pp.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
+    a.counters = (unsigned*)w;
+    a.part_o = (float*)(w + cbytes);
+    a.part_ml = (float*)(w + cbytes + obytes);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  const int nblocks = sdpa_grid_blocks(B * k_groups, a.nchunk, pp.nsplit);
+  int rc = dtype == MOTIF_F16 ? launch_gda_prefill_proj_f16(a, pp.waves, nblocks, s)
+                              : launch_gda_prefill_proj_bf16(a, pp.waves, nblocks, s);
+  if (rc != MOTIF_OK || pp.nsplit == 1) return rc;
+  // One merge over both passes' partial rows (noise rows into y_noise).
+  SdpaArgs m = a;
+  m.Hq = Hq_o + q_groups;
+  return sdpa_merge(m, dtype, D, s);
+}
+
+}  // extern "C"

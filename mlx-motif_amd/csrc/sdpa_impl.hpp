@@ -233,7 +233,7 @@ constexpr int kLdsPad = 4;
 // y[off .. off+3] = v / L (v itself where L == 0: no visible key), one
 // 8-byte store for 2-byte types (off is a multiple of 4).
 template <typename T, int D>
-__device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) {
+__device__ inline void store_y4_to(void* y, long off, float4 v, float L) {
   const bool z = L == 0.f;
   const float o[4] = {z ? v.x : v.x / L, z ? v.y : v.y / L, z ? v.z : v.z / L,
                       z ? v.w : v.w / L};
@@ -241,10 +241,14 @@ __device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) 
     const uint2 w = make_uint2(
         (uint32_t)Elem<T>::from_f32(o[0]) | ((uint32_t)Elem<T>::from_f32(o[1]) << 16),
         (uint32_t)Elem<T>::from_f32(o[2]) | ((uint32_t)Elem<T>::from_f32(o[3]) << 16));
-    *reinterpret_cast<uint2*>((uint16_t*)a.y + off) = w;
+    *reinterpret_cast<uint2*>((uint16_t*)y + off) = w;
   } else {
-    *reinterpret_cast<float4*>((float*)a.y + off) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>((float*)y + off) = make_float4(o[0], o[1], o[2], o[3]);
   }
+}
+template <typename T, int D>
+__device__ inline void store_y4(const SdpaArgs& a, long off, float4 v, float L) {
+  store_y4_to<T, D>(a.y, off, v, L);
 }
 
 // ------------------------------------------------------- split merge ---
@@ -552,7 +556,12 @@ __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   const int col = slice * S::CW + lane % S::CW;
   float L;
   const float4 acc = merge_row_column<D>(a, vrow, col, lane, L);
-  if (lane < S::CW) store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
+  if (lane < S::CW) {
+    if (a.y2 != nullptr && vrow >= a.y2_row0)  // second output (fused prefill's noise pass)
+      store_y4_to<T, D>(a.y2, (vrow - a.y2_row0) * 2 * D + col * 4, acc, L);
+    else
+      store_y4<T, D>(a, vrow * 2 * D + col * 4, acc, L);
+  }
 }
 
 template <typename T, int D>

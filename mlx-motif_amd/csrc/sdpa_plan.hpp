@@ -74,6 +74,20 @@ struct SdpaArgs {
   int from_proj;
   int q_origin_first;
   float rope_log2_theta;
+  // Prefill chunk of a GDA layer from the projection outputs
+  // (gda_prefill_proj_kernel): q is q_proj (B, S_q, q_groups*(q_gr+1)*D),
+  // new_k1 k_proj and new_v1 v_proj (B, S_q, 2*Hkv*D; k1[g] = head 2g,
+  // k2[g] = 2g+1, likewise v1/v2).  Query blocks [0, nqb_origin) of a
+  // (b, KV head, split) run the origin pass (G heads per KV head: q1 x k1,
+  // output y), the others the noise pass (G2 heads: q2 x k2, output y2,
+  // whose split partials start at row y2_row0).  The chunk is cache rows
+  // kv_len - S_q .. kv_len - 1, roped at positions rope_pos0 + s.
+  void* y2;
+  long y2_row0;
+  int nqb_origin;
+  int G2;
+  int q_groups, q_gr;
+  int rope_pos0;
 };
 
 struct SdpaPlan {
@@ -120,6 +134,21 @@ struct PrefillPlan {
   size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1
 };
 PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
+
+// Plan of a GDA layer's prefill chunk from the projections
+// (gda_prefill_proj_kernel): per (b, KV head) nqb_origin query blocks of the
+// origin pass (G_origin heads x S rows) and nqb_noise of the noise pass
+// (G_noise heads x S rows) of waves x 16 virtual heads each; rows are split
+// (to about one workgroup per CU) only when the blocks fill fewer than half
+// the CUs.  Partial rows (nsplit > 1): the origin pass's B*Hkv*G_origin*S,
+// then the noise pass's.
+struct GdaPrefillPlan {
+  int waves;
+  int nqb_origin, nqb_noise;
+  int nsplit, rows_per_split;
+  size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1
+};
+GdaPrefillPlan plan_gda_prefill(int B, int Hkv, int G_origin, int G_noise, int S, int kv_len);
 
 // Plan of the packed-cache slab kernel (sdpa_qslab.hpp): ncb column blocks of
 // 16 virtual heads per workgroup (2 when the heads of a KV head fit 32

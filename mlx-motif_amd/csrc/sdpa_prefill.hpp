@@ -193,11 +193,16 @@ struct SwizzledTileAcc {
 
   // Column vrow's result: y (normalised, nsplit == 1) or its split partial.
   __device__ __forceinline__ void store(const SdpaArgs& a, long vrow, int split, int blk) const {
+    store_to(a.y, vrow, a.part_o, a.part_ml, vrow, a.nsplit, split, blk);
+  }
+  // The same into row yrow of y (nsplit == 1) or partial row prow.
+  __device__ __forceinline__ void store_to(void* y, long yrow, float* part_o, float* part_ml,
+                                           long prow, int nsplit, int split, int blk) const {
     constexpr int D = 128;
     const float l = accl[0];
-    if (a.nsplit == 1) {
+    if (nsplit == 1) {
       const float inv = l == 0.f ? 1.f : 1.f / l;  // o stays 0 when no key is visible
-      uint16_t* yp = (uint16_t*)a.y + vrow * 2 * D + 32 * blk;
+      uint16_t* yp = (uint16_t*)y + yrow * 2 * D + 32 * blk;
 #pragma unroll
       for (int p = 0; p < 4; ++p) {  // channels 32*blk + 8*p .. +7
         uint32_t w1[4], w2[4];
@@ -214,8 +219,8 @@ struct SwizzledTileAcc {
         *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
       }
     } else {
-      const int ns = a.nsplit;
-      float* po = a.part_o + (vrow * ns + split) * 2 * D + 32 * blk;
+      const int ns = nsplit;
+      float* po = part_o + (prow * ns + split) * 2 * D + 32 * blk;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         *reinterpret_cast<float4*>(po + 4 * j) =
@@ -224,7 +229,7 @@ struct SwizzledTileAcc {
             make_float4(acc2[j][0], acc2[j][1], acc2[j][2], acc2[j][3]);
       }
       if (blk == 0)
-        *reinterpret_cast<float2*>(a.part_ml + (vrow * ns + split) * 2) = make_float2(m_run, l);
+        *reinterpret_cast<float2*>(part_ml + (prow * ns + split) * 2) = make_float2(m_run, l);
     }
   }
 };
@@ -352,6 +357,282 @@ inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int nblocks, h
     hipLaunchKernelGGL((sdpa_prefill_kernel<T, 4>), dim3(nblocks), dim3(256), 0, st, a);
   }
   return check_launch("sdpa_dual_v_rows (prefill)");
+}
+
+
+// ------------------------------------------------- prefill chunk from the projections ---
+// One launch for a GDA layer's prefill chunk (src/mlx_motif/model.py:590-594
+// rope on q and k, :620-629 the 4-slot split and cache write, :769-807 the
+// two dual-V passes with the bottom-right causal mask): query blocks of the
+// origin pass (q1 x k1) and of the noise pass (q2 x k2) share the grid, each
+// over V1/V2.  What differs from sdpa_prefill_kernel:
+//   - q is read from q_proj and roped in registers: channel c of k-step s
+//     (s < 2) pairs with channel c + 64 of k-step s + 2 in the same lane;
+//   - a split's rows before the chunk (kv_len - S_q) come from the cache,
+//     its rows of the chunk from k_proj / v_proj, as separate tile runs (the
+//     chunk's tiles start at its first row); after a chunk tile has landed
+//     in LDS its K rows are roped in place, then the waves meet again;
+//   - before its tile loop each block writes its share of the chunk's rows
+//     into the cache (roped k1 / k2, v1, v2): the origin blocks of a (b, KV
+//     head, split) share the split's k1, v1 and v2 rows, the noise blocks its
+//     k2 rows.  No block reads those cache rows (every block takes the chunk
+//     from the projections), so no block waits for another.
+// RoPE is rope_impl.hpp's, rounded once to T, so q, the cache rows and the
+// K tiles carry the values motif_rope_split4 produces.
+
+// stream_rsrc from a wave-uniform base and size, made explicitly scalar
+// (readfirstlane) so that the resource always lands in SGPRs, as the
+// LDS-direct copies' inline asm requires.
+__device__ inline __amdgpu_buffer_rsrc_t uniform_stream_rsrc(const void* base, unsigned bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return stream_rsrc((const void*)(uintptr_t)(((uint64_t)hi << 32) | lo),
+                     __builtin_amdgcn_readfirstlane(bytes));
+}
+
+// Roped or copied pairs (c, c + 64) of 16-bit channels: 4 values from each
+// half as 8-byte words.
+template <typename T>
+__device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float log2_theta) {
+  uint32_t a[2] = {lo.x, lo.y}, b[2] = {hi.x, hi.y};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float y1[2], y2[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float x1 = Elem<T>::to_f32((uint16_t)(e ? a[h] >> 16 : a[h] & 0xFFFFu));
+      const float x2 = Elem<T>::to_f32((uint16_t)(e ? b[h] >> 16 : b[h] & 0xFFFFu));
+      float cs, sn;
+      rope_angle(p0 + 2 * h + e, 128, pos, log2_theta, cs, sn);
+      rope_rotate(x1, x2, cs, sn, y1[e], y2[e]);
+    }
+    a[h] = (uint32_t)Elem<T>::from_f32(y1[0]) | ((uint32_t)Elem<T>::from_f32(y1[1]) << 16);
+    b[h] = (uint32_t)Elem<T>::from_f32(y2[0]) | ((uint32_t)Elem<T>::from_f32(y2[1]) << 16);
+  }
+  lo = make_uint2(a[0], a[1]);
+  hi = make_uint2(b[0], b[1]);
+}
+
+template <typename T, int NW, int NS = kPrefillStages>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
+gda_prefill_proj_kernel(SdpaArgs a) {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
+  constexpr int D = 128;
+  constexpr int TR = kPrefillTileRows;
+  constexpr int NT = NW * 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;
+  const int blk = lane >> 4;
+
+  int qblk, unit, split;
+  if (!prefill_block_coords(a, blockIdx.x, qblk, unit, split)) return;  // grid padding
+  const bool noise = qblk >= a.nqb_origin;
+  const int qb = noise ? qblk - a.nqb_origin : qblk;
+  const int nqb = noise ? a.nchunk - a.nqb_origin : a.nqb_origin;
+  const int G = noise ? a.G2 : a.G;  // heads of this pass per KV head
+  const int S = a.S_q;
+  const int GV = G * S;
+  const int b = unit / a.Hkv;
+  const int kvh = unit % a.Hkv;
+  const int wg_vh0 = qb * NW * 16;
+  const int vh = wg_vh0 + wave * 16 + col;  // virtual head (pass head vh / S, query row vh % S)
+  const bool col_ok = vh < GV;
+  const int lim = col_ok ? vhead_limit(a, vh) : 0;
+  int max_lim = 0;
+  for (int g = wg_vh0; g < min(wg_vh0 + NW * 16, GV); ++g)
+    max_lim = max(max_lim, vhead_limit(a, g));
+
+  const int row0 = a.kv_len - S;  // the chunk's first cache row
+  const int split_begin = split * a.rows_per_split;
+  const int split_end = min(split_begin + a.rows_per_split, a.kv_len);
+  const int r_end = min(split_end, max_lim);
+  const int old_end = min(r_end, row0);
+  const int n_old = max(old_end - split_begin, 0);
+  const int new_begin = max(split_begin, row0);
+  const int n_new = max(r_end - new_begin, 0);
+  const int t_old = (n_old + TR - 1) / TR;
+  const int ntiles = t_old + (n_new + TR - 1) / TR;
+
+  const int HK = 2 * a.Hkv;  // heads of k_proj and of v_proj
+  const long pstride = (long)HK * D;
+  const uint16_t* kproj = (const uint16_t*)a.new_k1;
+  const uint16_t* vproj = (const uint16_t*)a.new_v1;
+  uint16_t* kc = (uint16_t*)(noise ? a.k2 : a.k);  // this pass's K slot
+  const long crow0 = (long)unit * a.kv_cap;       // cache row 0 of this KV head
+
+  // ---- this block's share of the chunk's cache rows (written, not read) ----
+  {
+    const int wb = max(split_begin, row0);
+    const int nrows = max(split_end - wb, 0);
+    const int per = (nrows + nqb - 1) / nqb;
+    const int r_lo = wb + qb * per;
+    const int r_hi = min(r_lo + per, wb + nrows);
+    const int hk = 2 * kvh + (noise ? 1 : 0);
+    // K: one (row, chunk pair, half) item per thread: 4 pairs (c, c + 64).
+    for (int it = threadIdx.x; it < (r_hi - r_lo) * 16; it += NT) {
+      const int r = r_lo + (it >> 4);
+      const int cp = (it >> 1) & 7;
+      const int p0 = 8 * cp + 4 * (it & 1);
+      const long src = ((long)b * S + (r - row0)) * pstride + (long)hk * D;
+      uint2 lo = *reinterpret_cast<const uint2*>(kproj + src + p0);
+      uint2 hi = *reinterpret_cast<const uint2*>(kproj + src + 64 + p0);
+      rope_words<T>(lo, hi, p0, a.rope_pos0 + (r - row0), a.rope_log2_theta);
+      *reinterpret_cast<uint2*>(kc + (crow0 + r) * D + p0) = lo;
+      *reinterpret_cast<uint2*>(kc + (crow0 + r) * D + 64 + p0) = hi;
+    }
+    if (!noise) {  // V1 and V2: 16-byte copies
+      for (int it = threadIdx.x; it < (r_hi - r_lo) * 32; it += NT) {
+        const int r = r_lo + (it >> 5);
+        const int t = (it >> 4) & 1;
+        const int c = it & 15;
+        const long src = ((long)b * S + (r - row0)) * pstride + (long)(2 * kvh + t) * D + 8 * c;
+        const uint4 w = *reinterpret_cast<const uint4*>(vproj + src);
+        *reinterpret_cast<uint4*>((uint16_t*)(t ? a.v2 : a.v1) + (crow0 + r) * D + 8 * c) = w;
+      }
+    }
+  }
+
+  // ---- Q^T from q_proj, roped: lane (col, blk) holds channels 32*s + 8*blk .. +7 ----
+  V8 qbv[4];
+  {
+    const int hp = kvh * G + (col_ok ? vh / S : 0);  // head within the pass
+    const int srow = col_ok ? vh % S : 0;
+    const int HQ = a.q_groups * (a.q_gr + 1);
+    int qh;
+    if (!noise)
+      qh = a.q_origin_first ? hp : (hp / a.q_gr) * (a.q_gr + 1) + hp % a.q_gr;
+    else
+      qh = a.q_origin_first ? a.q_groups * a.q_gr + hp : hp * (a.q_gr + 1) + a.q_gr;
+    const uint16_t* qp = (const uint16_t*)a.q + (((long)b * S + srow) * HQ + qh) * D + 8 * blk;
+    uint4 w[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      w[s] = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
+    const int pos = a.rope_pos0 + srow;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      uint2 l0 = make_uint2(w[s].x, w[s].y), h0 = make_uint2(w[s + 2].x, w[s + 2].y);
+      uint2 l1 = make_uint2(w[s].z, w[s].w), h1 = make_uint2(w[s + 2].z, w[s + 2].w);
+      rope_words<T>(l0, h0, 32 * s + 8 * blk, pos, a.rope_log2_theta);
+      rope_words<T>(l1, h1, 32 * s + 8 * blk + 4, pos, a.rope_log2_theta);
+      w[s] = make_uint4(l0.x, l0.y, l1.x, l1.y);
+      w[s + 2] = make_uint4(h0.x, h0.y, h1.x, h1.y);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qbv[s] = __builtin_bit_cast(V8, w[s]);
+    // q and this block's cache stores are waited for here, before the first
+    // tile copies are issued (vmcnt also counts stores; the tile waits below
+    // count only the copies).
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(qbv[0]), "v"(qbv[1]), "v"(qbv[2]), "v"(qbv[3])
+                 : "memory");
+  }
+
+  // Rows [split_begin, old_end) from the cache, [new_begin, r_end) from the
+  // projections, through range-checked resources (past the range: zeros).
+  const long hrow0 = crow0 + split_begin;
+  const unsigned obytes = (unsigned)(n_old * D * 2);
+  const __amdgpu_buffer_rsrc_t r_old[3] = {
+      uniform_stream_rsrc(kc + hrow0 * D, obytes),
+      uniform_stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, obytes),
+      uniform_stream_rsrc((const uint16_t*)a.v2 + hrow0 * D, obytes)};
+  const long prow0 = ((long)b * S + (new_begin - row0)) * pstride;
+  const unsigned nbytes = n_new > 0 ? (unsigned)(((long)(n_new - 1) * pstride + D) * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t r_new[3] = {
+      uniform_stream_rsrc(kproj + prow0 + (long)(2 * kvh + (noise ? 1 : 0)) * D, nbytes),
+      uniform_stream_rsrc(vproj + prow0 + (long)(2 * kvh) * D, nbytes),
+      uniform_stream_rsrc(vproj + prow0 + (long)(2 * kvh + 1) * D, nbytes)};
+  const unsigned pstride_b = (unsigned)(pstride * 2);
+
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NS][3][TR * D * 2];
+  constexpr int CPW = 3 * TR * D * 2 / 1024 / NW;
+  static_assert(3 * TR * D * 2 / 1024 % NW == 0, "whole copies per wave");
+  static_assert((NS - 1) * CPW <= 63, "vmcnt counts at most 63");
+  static_assert(NW == 4 || NW == 8, "copies are dealt over 4 or 8 waves");
+  auto issue = [&](int st, int tile) {
+    const bool is_new = tile >= t_old;  // wave-uniform
+    const int tr = is_new ? tile - t_old : tile;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      const int t = c * NW / 8;
+      const int g = (wave + c * NW) % 8;
+      const int r = 4 * g + lane / 16;
+      const int chunk = (lane % 16) ^ (r % 16);
+      const unsigned lds = lds_byte_addr(&ring[st][t][g * 1024]);
+      if (is_new)
+        lds_copy16_rsrc(r_new[t], (unsigned)(tr * TR + r) * pstride_b + chunk * 16, lds);
+      else
+        lds_copy16_rsrc(r_old[t], (unsigned)((tr * TR + r) * D * 2 + chunk * 16), lds);
+    }
+  };
+
+  // K rows of a chunk tile, roped in place: (row, chunk pair, half) items.
+  auto rope_tile = [&](int st, int first_row, int nrows) {
+    uint8_t* Kt = ring[st][0];
+    for (int it = threadIdx.x; it < nrows * 16; it += NT) {
+      const int r = it >> 4;
+      const int cp = (it >> 1) & 7;
+      const int h = it & 1;
+      uint2* plo = reinterpret_cast<uint2*>(&Kt[r * 256 + ((cp ^ (r % 16)) * 16) + 8 * h]);
+      uint2* phi = reinterpret_cast<uint2*>(&Kt[r * 256 + (((cp + 8) ^ (r % 16)) * 16) + 8 * h]);
+      uint2 lo = *plo, hi = *phi;
+      rope_words<T>(lo, hi, 8 * cp + 4 * h, a.rope_pos0 + (first_row + r - row0),
+                    a.rope_log2_theta);
+      *plo = lo;
+      *phi = hi;
+    }
+  };
+
+  SwizzledTileAcc<T> st_acc;
+  st_acc.init();
+  int inflight = 0;
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t) {
+    if (t < ntiles) {
+      issue(t, t);
+      ++inflight;
+    }
+  }
+  int st = 0;
+  for (int i = 0; i < ntiles; ++i) {
+    prefill_wait_vm_groups<CPW, NS - 2>(inflight - 1);  // this wave's copies of tile i landed
+    asm volatile("s_barrier" ::: "memory");             // every wave's copies landed
+    --inflight;
+    if (i + NS - 1 < ntiles) {
+      issue(st == 0 ? NS - 1 : st - 1, i + NS - 1);
+      ++inflight;
+    }
+    const bool is_new = i >= t_old;
+    const int first = is_new ? new_begin + (i - t_old) * TR : split_begin + i * TR;
+    const int tile_end = is_new ? r_end : old_end;
+    if (is_new) {
+      rope_tile(st, first, min(TR, tile_end - first));
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    st_acc.tile(ring[st][0], ring[st][1], ring[st][2], qbv, first, tile_end, lim, a.qscale, col,
+                blk);
+    st = st + 1 == NS ? 0 : st + 1;
+  }
+
+  if (!col_ok) return;
+  // Output rows: origin (b, head, s) of y, noise (b, head, s) of y2; split
+  // partials in one row space, the noise rows after y2_row0.
+  const int Hp = a.Hkv * G;
+  const long yrow = ((long)b * Hp + (long)kvh * G) * S + vh;
+  st_acc.store_to(noise ? a.y2 : a.y, yrow, a.part_o, a.part_ml, (noise ? a.y2_row0 : 0) + yrow,
+                  a.nsplit, split, blk);
+}
+
+template <typename T>
+inline int launch_gda_prefill_proj_16(const SdpaArgs& a, int waves, int nblocks, hipStream_t st) {
+  if (waves == 8) {
+    hipLaunchKernelGGL((gda_prefill_proj_kernel<T, 8>), dim3(nblocks), dim3(512), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((gda_prefill_proj_kernel<T, 4>), dim3(nblocks), dim3(256), 0, st, a);
+  }
+  return check_launch("gda_prefill_proj");
 }
 
 }  // namespace motif

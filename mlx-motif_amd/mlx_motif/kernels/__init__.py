@@ -13,6 +13,8 @@ import) routes every wrapper to its reference.
     quant.py     — quantize / dequantize (MLX affine format of the KV cache)
     rope.py      — rope_split4 (RoPE + q/k/v head split + 4-slot cache write
                    in one launch; the reference uses rope() and reshapes)
+    prefill.py   — gda_prefill_attention_from_proj (a layer's prefill chunk:
+                   RoPE, cache write and both dual-V passes in one launch)
 """
 
 from .attention import (
@@ -43,6 +45,7 @@ from .mlp import (
     polynorm_reference,
 )
 from .quant import dequantize, dequantize_reference, quantize, quantize_reference
+from .prefill import gda_prefill_attention_from_proj, gda_prefill_attention_from_proj_reference
 from .rope import rope_split4, rope_split4_reference
 
 __all__ = [
@@ -70,4 +73,6 @@ __all__ = [
     "dequantize_reference",
     "rope_split4",
     "rope_split4_reference",
+    "gda_prefill_attention_from_proj",
+    "gda_prefill_attention_from_proj_reference",
 ]

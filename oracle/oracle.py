@@ -47,6 +47,12 @@ How each function is pinned (tests/test_oracle.py):
   polynorm           the reference's only numeric golden vector
                      (tests/fixtures/motif_parity_cases.json,
                      component_checks[0]).
+  gda_prefill_from_proj
+                     a composition of rope_split4 and sdpa_dual_v (pinned as
+                     stated), in the order of model.py:590-629 and 769-797;
+                     checked against an explicit per-head loop over the
+                     reference's four causal SDPA calls (torch float64) on a
+                     tiny shape.
   rope / rope_split4 the rotation's closed form on D = 2 (angle = position),
                      position 0 is the identity, every channel pair keeps
                      its norm, and q(m).k(n) depends on m - n only; the split
@@ -365,3 +371,31 @@ def rope_split4(q, k, v, q_groups: int, gr: int, k_groups: int, kr: int, pos0: i
     k2 = k_[:, :, kr:].reshape(B, k_groups, S, D)
     v_ = vv.reshape(B, k_groups, 2, S, D)
     return q1, q2, k1, k2, v_[:, :, 0], v_[:, :, 1]
+
+
+def gda_prefill_from_proj(q, k, v, caches, offset: int, q_groups: int, gr: int, k_groups: int,
+                          scale: float, theta: float = 10000.0, origin_first: bool = False,
+                          dtype: str = "f16"):
+    """A GDA layer's prefill chunk on the k_ratio-1 fallback path: rope q and k
+    at positions offset + s (model.py:590-594), split and write the 4-slot
+    cache rows offset .. offset + S - 1 (model.py:620-629, update_and_fetch_4),
+    split q1/q2 (model.py:669-679), then the four causal SDPA calls, concatenated
+    per pass (model.py:769-797): origin = [q1 over (k1, V1) || q1 over (k1, V2)],
+    noise = the same for q2 over k2.  The roped q/k are rounded to ``dtype``
+    (the reference's rope output has the activation dtype).  ``caches`` is
+    (k1, k2, v1, v2), each (B, k_groups, cap, D).  Returns float64 (y_origin,
+    y_noise, the four written cache slots)."""
+    q1, q2, k1n, k2n, v1n, v2n = rope_split4(q, k, v, q_groups, gr, k_groups, 1, offset, theta,
+                                             origin_first)
+
+    def rnd(x):
+        return round_to(x, dtype).astype(np.float64)
+
+    S = q1.shape[2]
+    slots = [np.array(c, dtype=np.float64, copy=True) for c in caches]
+    for c, new in zip(slots, (k1n, k2n, v1n, v2n)):
+        c[:, :, offset:offset + S] = rnd(new)
+    kv_len = offset + S
+    y_o = sdpa_dual_v(rnd(q1), slots[0], slots[2], slots[3], scale, kv_len, causal=True)
+    y_n = sdpa_dual_v(rnd(q2), slots[1], slots[2], slots[3], scale, kv_len, causal=True)
+    return y_o, y_n, slots

@@ -357,3 +357,56 @@ def test_rope_split4_head_mapping_explicit_loop(rng):
     o1, o2, *_ = O.rope_split4(q, k, v, qg, gr, kg, kr, 5, origin_first=True)
     np.testing.assert_array_equal(o1, qr.transpose(0, 2, 1, 3)[:, : qg * gr])
     np.testing.assert_array_equal(o2, qr.transpose(0, 2, 1, 3)[:, qg * gr:])
+
+
+def test_gda_prefill_from_proj_per_head_loop(rng):
+    """The prefill-chunk composition against an explicit loop over the
+    reference's steps (model.py:590-629 rope + 4-slot write, 769-797 four
+    causal SDPA calls): for each origin head h (KV head of q1 head h under
+    the GQA broadcast) and noise head, torch's float64 SDPA over the cache
+    with the chunk written, query row s seeing rows [0, offset + s]."""
+    import torch
+
+    B, S, qg, gr, kg, D, offset, cap = 2, 3, 4, 2, 2, 32, 5, 12
+    f16 = lambda x: O.round_to(x, "f16").astype(np.float64)  # noqa: E731
+    q = f16(rng.standard_normal((B, S, qg * (gr + 1) * D)))
+    k = f16(rng.standard_normal((B, S, 2 * kg * D)))
+    v = f16(rng.standard_normal((B, S, 2 * kg * D)))
+    caches = [f16(rng.standard_normal((B, kg, cap, D))) for _ in range(4)]
+    scale = 0.17
+    y_o, y_n, slots = O.gda_prefill_from_proj(q, k, v, caches, offset, qg, gr, kg, scale)
+    qr = f16(O.rope(q.reshape(B, S, -1, D), offset))
+    kr_ = f16(O.rope(k.reshape(B, S, -1, D), offset))
+    vv = v.reshape(B, S, -1, D)
+    cache = [c.copy() for c in caches]
+    for b in range(B):
+        for s in range(S):
+            for g in range(kg):
+                cache[0][b, g, offset + s] = kr_[b, s, 2 * g]
+                cache[1][b, g, offset + s] = kr_[b, s, 2 * g + 1]
+                cache[2][b, g, offset + s] = vv[b, s, 2 * g]
+                cache[3][b, g, offset + s] = vv[b, s, 2 * g + 1]
+    for a, c in zip(slots, cache):
+        np.testing.assert_array_equal(a, c)
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    t = torch.from_numpy
+    kv = offset + S
+    mask = t(np.arange(kv)[None, :] <= offset + np.arange(S)[:, None])
+
+    def att(qrows, kslot, j, b):
+        qs = t(qrows)[None, None]
+        ks = t(cache[kslot][b, j, :kv])[None, None]
+        a1 = sdpa(qs, ks, t(cache[2][b, j, :kv])[None, None], attn_mask=mask, scale=scale)
+        a2 = sdpa(qs, ks, t(cache[3][b, j, :kv])[None, None], attn_mask=mask, scale=scale)
+        return torch.cat([a1, a2], -1).numpy()[0, 0]
+
+    G_o, G_n = qg * gr // kg, qg // kg
+    for b in range(B):
+        for h in range(qg * gr):  # q1 head h = group h // gr, slot h % gr
+            qrows = qr[b, :, (h // gr) * (gr + 1) + h % gr]
+            np.testing.assert_allclose(y_o[b, h], att(qrows, 0, h // G_o, b), rtol=1e-12,
+                                       atol=1e-12)
+        for h in range(qg):
+            qrows = qr[b, :, h * (gr + 1) + gr]
+            np.testing.assert_allclose(y_n[b, h], att(qrows, 1, h // G_n, b), rtol=1e-12,
+                                       atol=1e-12)
