@@ -651,6 +651,45 @@ def run_extra(torch, lib, dev, args):
                                "pct_peak_f16_mfma": round(100 * flops / us / 1e6 / PEAK_F16_TFLOPS, 1)}))
     del calls, keep
     torch.cuda.empty_cache()
+    # a 12.7B layer's prefill chunk from the projections: 512 rows at offset
+    # 3204 (and a first chunk at offset 0), RoPE + cache write + origin
+    # (32 heads) and noise (8 heads) passes in one launch, against
+    # rope_split4 + two multi-row calls
+    from mlx_motif.kernels import gda_prefill_attention_from_proj, rope_split4, sdpa_dual_v_rows
+    g3 = torch.Generator(device=dev)
+    g3.manual_seed(9)
+    for off in (3204, 0):
+        S = 512
+        cap = (off + S + 255) // 256 * 256
+        sets = []
+        for _ in range(4):
+            sets.append((torch.randn((B, S, 40 * D), generator=g3, device=dev).half(),
+                         torch.randn((B, S, 16 * D), generator=g3, device=dev).half(),
+                         torch.randn((B, S, 16 * D), generator=g3, device=dev).half(),
+                         [torch.randn((B, HKV, cap, D), generator=g3, device=dev).half()
+                          for _ in range(4)]))
+        flops = 2 * (HQ + HKV) * D * 3 * sum(off + s + 1 for s in range(S))
+
+        def fused(st):
+            return lambda: gda_prefill_attention_from_proj(st[0], st[1], st[2], st[3], off, 8, 4,
+                                                           8, D ** -0.5)
+
+        def unfused(st):
+            def call():
+                q1, q2, k1, k2, v1, v2 = rope_split4(st[0], st[1], st[2], 8, 4, 8, 1, off,
+                                                     caches=st[3])
+                sdpa_dual_v_rows(q1, k1, v1, v2, D ** -0.5, kv_len=off + S, causal=True)
+                sdpa_dual_v_rows(q2, k2, v1, v2, D ** -0.5, kv_len=off + S, causal=True)
+            return call
+
+        for name, mk in (("one launch", fused), ("rope_split4 + 2 calls", unfused)):
+            us = time_calls(torch, [mk(st) for st in sets], steps, warm)
+            log("EXTRA " + json.dumps({
+                "workload": f"prefill layer chunk f16 512 rows at offset {off}, 32+8 heads ({name})",
+                "us_per_call": round(us, 3), "tflops": round(flops / us / 1e6, 1),
+                "pct_peak_f16_mfma": round(100 * flops / us / 1e6 / PEAK_F16_TFLOPS, 1)}))
+        del sets
+        torch.cuda.empty_cache()
     # gda_post_split prefill [1,16,3204,128]
     g = torch.Generator(device=dev)
     g.manual_seed(7)

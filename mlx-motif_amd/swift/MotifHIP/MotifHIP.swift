@@ -255,6 +255,41 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// Workspace bytes of gdaPrefillFromProjections (0 when its rows are not
+    /// split).
+    public static func gdaPrefillWorkspaceBytes(batch: Int, seqLen: Int, qGroups: Int, gr: Int,
+                                                kGroups: Int, headDim: Int, kvLen: Int) -> Int {
+        return Int(motif_gda_prefill_workspace_bytes(Int32(batch), Int32(seqLen), Int32(qGroups),
+                                                     Int32(gr), Int32(kGroups), Int32(headDim),
+                                                     Int32(kvLen)))
+    }
+
+    /// A layer's prefill chunk from the projection outputs in one attention
+    /// launch: q and k roped at positions offset + s, the chunk's rows
+    /// written into the 4-slot fp cache, the origin (q1 over k1) and noise
+    /// (q2 over k2) dual-V passes with the bottom-right causal mask
+    /// (fp16/bf16 cache, head_dim 128; other shapes return .unsupported:
+    /// compose ropeSplit4 and the multi-row sdpa calls).  Only unscaled
+    /// RoPE: check the model's rope_scaling is nil first.
+    public static func gdaPrefillFromProjections(
+        qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
+        keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
+        value1: UnsafeMutableRawPointer, value2: UnsafeMutableRawPointer,
+        outputOrigin: UnsafeMutableRawPointer, outputNoise: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, seqLen: Int, qGroups: Int, gr: Int, kGroups: Int,
+        headDim: Int, kvCapacity: Int, offset: Int, scale: Float, theta: Float,
+        originFirst: Bool, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_prefill_proj(qProj, kProj, vProj, keys1, keys2, value1, value2,
+                                        outputOrigin, outputNoise, dtype.rawValue, Int32(batch),
+                                        Int32(seqLen), Int32(qGroups), Int32(gr), Int32(kGroups),
+                                        Int32(headDim), Int32(kvCapacity), Int32(offset), scale,
+                                        theta, originFirst ? 1 : 0, workspace, workspaceBytes,
+                                        stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// A layer's decode attention from the projection outputs: RoPE at
     /// position kvLen - 1, the head split and the token's cache rows inside
     /// the attention launch (fp16/bf16 cache, head_dim 128; other shapes
