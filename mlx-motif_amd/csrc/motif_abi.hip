@@ -187,11 +187,12 @@ GdaPrefillPlan plan_gda_prefill(int B, int Hkv, int G_origin, int G_noise, int S
     nsplit = (rows + rps - 1) / rps;
   } else if (units < cus / 2) {
     // Workgroups hold one CU each (the LDS ring).  Rows are split only when
-    // the query blocks leave most CUs idle: with 160 blocks on 256 CUs (a
+    // the query blocks leave most CUs idle, into as many splits as keep the
+    // workgroups within one round: with 160 blocks on 256 CUs (a
     // 512-row chunk of 32 + 8 heads over 8 KV heads, 3716 rows) one split
     // measured 178 us, 2 / 3 / 4 / 8 splits 229 / 198 / 222 / 255 us (the
     // partials, the merge launch and a second round of workgroups).
-    nsplit = (int)std::min<long>((cus + units - 1) / units, std::max(1, (rows + 127) / 128));
+    nsplit = (int)std::min<long>(std::max<long>(cus / units, 1), std::max(1, (rows + 127) / 128));
   }
   if (nsplit > kMaxSplits) nsplit = kMaxSplits;
   int rps = (rows + nsplit - 1) / nsplit;

@@ -6,9 +6,14 @@
 
 namespace motif {
 
-__device__ inline void rope_angle(int p, int D, int pos, float log2_theta, float& cs, float& sn) {
-  const float inv_freq = exp2f(-(2.f * (float)p / (float)D) * log2_theta);
+__device__ inline float rope_inv_freq(int p, int D, float log2_theta) {
+  return exp2f(-(2.f * (float)p / (float)D) * log2_theta);
+}
+__device__ inline void rope_angle_inv(float inv_freq, int pos, float& cs, float& sn) {
   sincosf((float)pos * inv_freq, &sn, &cs);
+}
+__device__ inline void rope_angle(int p, int D, int pos, float log2_theta, float& cs, float& sn) {
+  rope_angle_inv(rope_inv_freq(p, D, log2_theta), pos, cs, sn);
 }
 
 __device__ inline void rope_rotate(float x1, float x2, float cs, float sn, float& y1, float& y2) {

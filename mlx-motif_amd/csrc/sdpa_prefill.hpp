@@ -113,13 +113,11 @@ struct SwizzledTileAcc {
     m_run = kNegSentinel;
   }
 
-  // Rows row0 + 16*h + 4*blk + r of the tile hold k index 8*blk + 4*h + r of
-  // the PV products (as in the decode kernel); rows at or past r_end or lim
-  // are masked.
-  __device__ __forceinline__ void tile(const uint8_t* Kt, const uint8_t* V1t, const uint8_t* V2t,
-                                       const V8 (&qb)[4], int row0, int r_end, int lim,
-                                       float qscale, int col, int blk) {
-    floatx4 sacc[2];
+  // S^T = K Q^T of a tile (unscaled): sacc[h][r] is the score of row
+  // 16*h + 4*blk + r for column col.  Issued on its own so that a loop can
+  // start the next tile's products before this tile's softmax.
+  __device__ __forceinline__ static void scores(const uint8_t* Kt, const V8 (&qb)[4],
+                                                floatx4 (&sacc)[2], int col, int blk) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       sacc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -131,6 +129,15 @@ struct SwizzledTileAcc {
         sacc[h] = Op::mma(ka, qb[s], sacc[h]);
       }
     }
+  }
+
+  // Mask, online softmax and both PV products of a tile with scores sacc.
+  // Rows row0 + 16*h + 4*blk + r of the tile hold k index 8*blk + 4*h + r of
+  // the PV products (as in the decode kernel); rows at or past r_end or lim
+  // are masked.
+  __device__ __forceinline__ void update(const floatx4 (&sacc)[2], const uint8_t* V1t,
+                                         const uint8_t* V2t, int row0, int r_end, int lim,
+                                         float qscale, int col, int blk) {
     float sc[8];
     float mx = kNegSentinel;
 #pragma unroll
@@ -143,8 +150,7 @@ struct SwizzledTileAcc {
         mx = fmaxf(mx, sc[4 * h + r]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = rows4_max(mx);
     if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float fac = fast_exp2(m_run - m_new);
@@ -189,6 +195,15 @@ struct SwizzledTileAcc {
     const typename Op::S one = Op::from_f32(1.f);
     const V8 ones = {one, one, one, one, one, one, one, one};
     accl = Op::mma(ones, pb, accl);
+  }
+
+  // One tile: scores() then update().
+  __device__ __forceinline__ void tile(const uint8_t* Kt, const uint8_t* V1t, const uint8_t* V2t,
+                                       const V8 (&qb)[4], int row0, int r_end, int lim,
+                                       float qscale, int col, int blk) {
+    floatx4 sacc[2];
+    scores(Kt, qb, sacc, col, blk);
+    update(sacc, V1t, V2t, row0, r_end, lim, qscale, col, blk);
   }
 
   // Column vrow's result: y (normalised, nsplit == 1) or its split partial.
@@ -312,15 +327,15 @@ sdpa_prefill_kernel(SdpaArgs a) {
 
   SwizzledTileAcc<T> st_acc;
   st_acc.init();
-  auto compute = [&](int st, int t0) {
-    st_acc.tile(ring[st][0], ring[st][1], ring[st][2], qb, r_begin + t0, r_end, lim, a.qscale,
-                col, blk);
-  };
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
-  // all of its threads.  Tile i sits in stage i % NS.  At the barrier of
-  // tile i every wave has computed tile i - 1, so stage (i - 1) % NS is
-  // refilled (with tile i + NS - 1) right after it.
+  // all of its threads.  Software-pipelined over tiles: the S^T products of
+  // tile i + 1 are issued before the softmax and PV products of tile i.
+  // Tile i sits in stage i % NS.  Barrier i publishes tile i; at it every
+  // wave has finished the PV products of tile i - 2, so stage (i - 2) % NS
+  // is refilled with tile i + NS - 2 right after it (barrier 0 fills stage
+  // NS - 1, unused until then): NS - 2 tiles in flight ahead of the two
+  // being worked on.
   const int nrows = max(r_end - r_begin, 0);
   const int ntiles = (nrows + TR - 1) / TR;
   int inflight = 0;
@@ -331,17 +346,30 @@ sdpa_prefill_kernel(SdpaArgs a) {
       ++inflight;
     }
   }
-  int st = 0;
-  for (int i = 0; i < ntiles; ++i) {
+  auto publish = [&](int i) {
     prefill_wait_vm_groups<CPW, NS - 2>(inflight - 1);  // this wave's copies of tile i landed
     asm volatile("s_barrier" ::: "memory");             // every wave's copies landed
     --inflight;
-    if (i + NS - 1 < ntiles) {
-      issue(st == 0 ? NS - 1 : st - 1, i + NS - 1);
+    const int t = i == 0 ? NS - 1 : i + NS - 2;
+    if (i != 1 && t < ntiles) {
+      issue(t % NS, t);
       ++inflight;
     }
-    compute(st, i * TR);
-    st = st + 1 == NS ? 0 : st + 1;
+  };
+  floatx4 s_cur[2], s_nxt[2];
+  if (ntiles > 0) {
+    publish(0);
+    SwizzledTileAcc<T>::scores(ring[0][0], qb, s_cur, col, blk);
+  }
+  for (int i = 0; i < ntiles; ++i) {
+    if (i + 1 < ntiles) {
+      publish(i + 1);
+      SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb, s_nxt, col, blk);
+    }
+    st_acc.update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end, lim,
+                  a.qscale, col, blk);
+    s_cur[0] = s_nxt[0];
+    s_cur[1] = s_nxt[1];
   }
 
   // acc[j][r] of lane (col, blk) is channel 32*blk + 4*j + r of column col.
@@ -370,8 +398,9 @@ inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int nblocks, h
 //     (s < 2) pairs with channel c + 64 of k-step s + 2 in the same lane;
 //   - a split's rows before the chunk (kv_len - S_q) come from the cache,
 //     its rows of the chunk from k_proj / v_proj, as separate tile runs (the
-//     chunk's tiles start at its first row); after a chunk tile has landed
-//     in LDS its K rows are roped in place, then the waves meet again;
+//     chunk's tiles start at its first row); each wave ropes in place the
+//     K rows of a chunk tile it copied, once its own copies have landed and
+//     before the tile's barrier;
 //   - before its tile loop each block writes its share of the chunk's rows
 //     into the cache (roped k1 / k2, v1, v2): the origin blocks of a (b, KV
 //     head, split) share the split's k1, v1 and v2 rows, the noise blocks its
@@ -393,8 +422,9 @@ __device__ inline __amdgpu_buffer_rsrc_t uniform_stream_rsrc(const void* base, u
 
 // Roped or copied pairs (c, c + 64) of 16-bit channels: 4 values from each
 // half as 8-byte words.
+// (inv: the pairs' inverse frequencies, rope_inv_freq.)
 template <typename T>
-__device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float log2_theta) {
+__device__ inline void rope_words_inv(uint2& lo, uint2& hi, const float (&inv)[4], int pos) {
   uint32_t a[2] = {lo.x, lo.y}, b[2] = {hi.x, hi.y};
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -404,7 +434,7 @@ __device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float l
       const float x1 = Elem<T>::to_f32((uint16_t)(e ? a[h] >> 16 : a[h] & 0xFFFFu));
       const float x2 = Elem<T>::to_f32((uint16_t)(e ? b[h] >> 16 : b[h] & 0xFFFFu));
       float cs, sn;
-      rope_angle(p0 + 2 * h + e, 128, pos, log2_theta, cs, sn);
+      rope_angle_inv(inv[2 * h + e], pos, cs, sn);
       rope_rotate(x1, x2, cs, sn, y1[e], y2[e]);
     }
     a[h] = (uint32_t)Elem<T>::from_f32(y1[0]) | ((uint32_t)Elem<T>::from_f32(y1[1]) << 16);
@@ -412,6 +442,13 @@ __device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float l
   }
   lo = make_uint2(a[0], a[1]);
   hi = make_uint2(b[0], b[1]);
+}
+template <typename T>
+__device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float log2_theta) {
+  const float inv[4] = {rope_inv_freq(p0, 128, log2_theta), rope_inv_freq(p0 + 1, 128, log2_theta),
+                        rope_inv_freq(p0 + 2, 128, log2_theta),
+                        rope_inv_freq(p0 + 3, 128, log2_theta)};
+  rope_words_inv<T>(lo, hi, inv, pos);
 }
 
 template <typename T, int NW, int NS = kPrefillStages>
@@ -568,25 +605,39 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     }
   };
 
-  // K rows of a chunk tile, roped in place: (row, chunk pair, half) items.
-  auto rope_tile = [&](int st, int first_row, int nrows) {
+  // K rows of a chunk tile, roped in place by the wave that copied them
+  // (copy `wave` of a tile holds K rows 4*wave .. 4*wave + 3, and with 4
+  // waves copy `wave + 4` rows 4*wave + 16 .. + 19): lane (row rr = lane/16
+  // of those four, channel pair block cp = lane/2 % 8, half h = lane % 2)
+  // ropes channels 8*cp + 4*h .. +3 with their partners 64 on.
+  const int rr = lane >> 4;
+  const int rcp = (lane >> 1) & 7;
+  const int rh = lane & 1;
+  float rinv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) rinv[e] = rope_inv_freq(8 * rcp + 4 * rh + e, D, a.rope_log2_theta);
+  auto rope_own_rows = [&](int st, int first_row, int nrows) {
     uint8_t* Kt = ring[st][0];
-    for (int it = threadIdx.x; it < nrows * 16; it += NT) {
-      const int r = it >> 4;
-      const int cp = (it >> 1) & 7;
-      const int h = it & 1;
-      uint2* plo = reinterpret_cast<uint2*>(&Kt[r * 256 + ((cp ^ (r % 16)) * 16) + 8 * h]);
-      uint2* phi = reinterpret_cast<uint2*>(&Kt[r * 256 + (((cp + 8) ^ (r % 16)) * 16) + 8 * h]);
-      uint2 lo = *plo, hi = *phi;
-      rope_words<T>(lo, hi, 8 * cp + 4 * h, a.rope_pos0 + (first_row + r - row0),
-                    a.rope_log2_theta);
-      *plo = lo;
-      *phi = hi;
+#pragma unroll
+    for (int c = 0; c < 8 / NW; ++c) {
+      const int r = 4 * (wave + c * NW) + rr;
+      if (r < nrows) {
+        uint2* plo = reinterpret_cast<uint2*>(&Kt[r * 256 + ((rcp ^ (r % 16)) * 16) + 8 * rh]);
+        uint2* phi =
+            reinterpret_cast<uint2*>(&Kt[r * 256 + (((rcp + 8) ^ (r % 16)) * 16) + 8 * rh]);
+        uint2 lo = *plo, hi = *phi;
+        rope_words_inv<T>(lo, hi, rinv, a.rope_pos0 + (first_row + r - row0));
+        *plo = lo;
+        *phi = hi;
+      }
     }
   };
 
   SwizzledTileAcc<T> st_acc;
   st_acc.init();
+  // Pipelined as sdpa_prefill_kernel: barrier i publishes tile i (a chunk
+  // tile's K rows roped first by the waves that copied them); the scores of
+  // tile i + 1 are issued before the softmax and PV products of tile i.
   int inflight = 0;
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t) {
@@ -595,25 +646,38 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       ++inflight;
     }
   }
-  int st = 0;
-  for (int i = 0; i < ntiles; ++i) {
+  auto first_row = [&](int i) {
+    return i >= t_old ? new_begin + (i - t_old) * TR : split_begin + i * TR;
+  };
+  auto publish = [&](int i) {
     prefill_wait_vm_groups<CPW, NS - 2>(inflight - 1);  // this wave's copies of tile i landed
-    asm volatile("s_barrier" ::: "memory");             // every wave's copies landed
+    if (i >= t_old) {  // rope the K rows this wave copied, before the waves meet
+      const int first = first_row(i);
+      rope_own_rows(i % NS, first, min(TR, r_end - first));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    asm volatile("s_barrier" ::: "memory");  // every wave's copies (and ropes) landed
     --inflight;
-    if (i + NS - 1 < ntiles) {
-      issue(st == 0 ? NS - 1 : st - 1, i + NS - 1);
+    const int t = i == 0 ? NS - 1 : i + NS - 2;
+    if (i != 1 && t < ntiles) {
+      issue(t % NS, t);
       ++inflight;
     }
-    const bool is_new = i >= t_old;
-    const int first = is_new ? new_begin + (i - t_old) * TR : split_begin + i * TR;
-    const int tile_end = is_new ? r_end : old_end;
-    if (is_new) {
-      rope_tile(st, first, min(TR, tile_end - first));
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  floatx4 s_cur[2], s_nxt[2];
+  if (ntiles > 0) {
+    publish(0);
+    SwizzledTileAcc<T>::scores(ring[0][0], qbv, s_cur, col, blk);
+  }
+  for (int i = 0; i < ntiles; ++i) {
+    if (i + 1 < ntiles) {
+      publish(i + 1);
+      SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qbv, s_nxt, col, blk);
     }
-    st_acc.tile(ring[st][0], ring[st][1], ring[st][2], qbv, first, tile_end, lim, a.qscale, col,
-                blk);
-    st = st + 1 == NS ? 0 : st + 1;
+    st_acc.update(s_cur, ring[i % NS][1], ring[i % NS][2], first_row(i),
+                  i >= t_old ? r_end : old_end, lim, a.qscale, col, blk);
+    s_cur[0] = s_nxt[0];
+    s_cur[1] = s_nxt[1];
   }
 
   if (!col_ok) return;

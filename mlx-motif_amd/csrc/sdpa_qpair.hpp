@@ -36,41 +36,6 @@
 
 namespace motif {
 
-// Lane l receives its own value and lane l ^ 16's (in row order: rows 0/1
-// hold (row 0, row 1) of the pair, rows 2/3 (row 2, row 3)); likewise l ^ 32
-// for the 32-lane swap.  Issued as asm: at -O3 the compiler folds the second
-// result of __builtin_amdgcn_permlane16_swap into the first, which breaks a
-// swap of one value against itself.  The s_nops cover the VALU-write ->
-// permlane-read and permlane-write -> VALU-read hazards.
-__device__ inline void swap16(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-__device__ inline void swap32(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-
-// Max over the four 16-lane rows (lanes l, l^16, l^32, l^48): every lane
-// receives the same value.
-__device__ inline float rows4_max(float x) {
-  float a, b;
-  swap16(x, a, b);
-  swap32(fmaxf(a, b), a, b);
-  return fmaxf(a, b);
-}
-// Sum over the four 16-lane rows; every lane receives the same bits (the
-// operands of each add are the same pair, in the same order, on both
-// partners).
-__device__ inline float rows4_sum(float x) {
-  float a, b;
-  swap16(x, a, b);
-  swap32(a + b, a, b);
-  return a + b;
-}
-
 // Sum over the NG adjacent group columns of a head (quad permutes); both
 // partners add the same two operands, so every column gets the same bits.
 template <int NG>
