@@ -329,6 +329,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.qslab = value; });
+  } else if (!strcmp(key, "qslab_ws")) {
+    if (value > 1) {
+      set_error("motif_set_tuning: qslab_ws must be 0 or 1");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.qslab_ws = value; });
   } else if (!strcmp(key, "poly_rows")) {
     update_tuning([&](Tuning& t) { t.poly_rows = value; });
   } else {

@@ -39,7 +39,8 @@ struct Tuning {
   int fused_merge = 0;     // 1 = last-arriving workgroup merges splits, 0 = merge kernel
   int poly_rows = 0;       // persistent PolyNorm workgroups per CU (0 = by register use)
   int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 q4, 2 q4+q8
-  int qslab = 1;           // slabs of 17..64 virtual heads, tiles dequantised into LDS: 0 off, 1 q8, 2 q4+q8
+  int qslab = 2;           // slabs of 17..64 virtual heads, tiles dequantised into LDS: 0 off, 1 q8, 2 q4+q8
+  int qslab_ws = 1;        // slab kernel with producer / consumer waves (8 waves): 1 on, 0 off
 };
 // The calling thread's snapshot of the process-wide knobs.  Inside a
 // CallScope it is the copy taken when the outermost scope opened, so every

@@ -205,9 +205,9 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   a.group_size = gs;
   hipStream_t s = (hipStream_t)stream;
   // A verify slab of 17..64 virtual heads per KV head: packed tiles
-  // dequantised once per workgroup into LDS and shared by its waves.
-  // On by default for q8 (46.3 vs 48.6 us on a 5-row slab over 32768 rows);
-  // for q4 the head chunks of the decode kernel stay faster (41.6 vs 48.7 us).
+  // dequantised once per workgroup into LDS and shared by its waves (with
+  // producer and consumer waves: 5-row slab over 32768 rows, q8 33.0 against
+  // 49.0 us in head chunks, q4 35.3 against 43.6 us).
   if (dtype == MOTIF_F16 && D == 128 && tuning().mfma && tuning().qslab >= (bits == 8 ? 1 : 2) &&
       a.GV >= kQSlabMinHeads && a.GV <= kQSlabMaxHeads && kv_len <= kMfmaMaxRows &&
       aligned(q, 16) && aligned(y, 16) && aligned(kd, bits == 8 ? 16 : 8) &&

@@ -7,6 +7,14 @@ namespace motif {
 
 template <int BITS, int GS>
 static int launch_qslab_gs(const SdpaArgs& a, int ncb, int waves, int nblocks, hipStream_t st) {
+  // 8 waves: producer / consumer roles (dequantisation beside the attention)
+  if (waves == 8 && tuning().qslab_ws) {
+    if (ncb == 2)
+      hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, 2>), dim3(nblocks), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, 4>), dim3(nblocks), dim3(512), 0, st, a);
+    return check_launch("sdpa_dual_v_q (slab, producer/consumer)");
+  }
   if (ncb == 2 && waves == 8)
     hipLaunchKernelGGL((sdpa_qslab_kernel<BITS, GS, 2, 8>), dim3(nblocks), dim3(512), 0, st, a);
   else if (ncb == 4 && waves == 8)

@@ -289,4 +289,251 @@ sdpa_qslab_kernel(SdpaArgs a) {
   acc.store(a, qrow0 + vh, split, blk);
 }
 
+
+// ---------------------------------------------------- producer / consumer ---
+// The same slab with the waves split by role, so that dequantisation (VALU)
+// and attention (matrix cores) run at the same time on every SIMD: waves
+// 0..3 are consumers (column block w % NCB, tile w / NCB of a step of
+// NP = 4 / NCB tiles), waves 4..7 producers, one of each per SIMD.  Two LDS
+// stages: in step j the consumers attend stage j % 2 while the producers
+// dequantise step j + 1 into the other stage from the registers its loads
+// landed in (issued two steps ahead, two register sets) and issue step
+// j + 3's loads; one barrier ends the step.  Dequantisation is packed fp16:
+// two codes become 1024 + u in the halves of one word (their byte or nibble
+// under an fp16 exponent), a packed subtract leaves u exactly, and a packed
+// fma gives s * u + b rounded once to fp16 -- the value mx.dequantize feeds
+// the reference path's attention (src/mlx_motif/kernels/attention.py:497-499).
+template <int BITS, int GS, int NCB>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+sdpa_qslab_ws_kernel(SdpaArgs a) {
+  using Acc = SwizzledTileAcc<half_t>;
+  using V8 = Acc::V8;
+  constexpr int D = 128;
+  constexpr int TR = kPrefillTileRows;  // 32
+  constexpr int NC = 4;                 // consumer waves
+  constexpr int NP = NC / NCB;          // tiles per step
+  constexpr int NG = D / GS;
+  constexpr int RB = D * BITS / 8;   // packed bytes per row
+  constexpr int CB = 16 * BITS / 8;  // packed bytes per 16-code chunk
+  constexpr int CPT = 3 * NP;        // chunks per producer thread per step
+  static_assert(NCB == 2 || NCB == 4, "2 or 4 column blocks");
+  static_assert(GS % 16 == 0, "a chunk sits in one scale group");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool producer = wave >= NC;
+  const int col = lane & 15;
+  const int blk = lane >> 4;
+  const int cb = wave % NCB;  // consumers: column block
+  const int tp = wave / NCB;  // consumers: tile of the step
+
+  int qblk, unit, split;
+  if (!prefill_block_coords(a, blockIdx.x, qblk, unit, split)) return;  // grid padding
+  const int b = unit / a.Hkv;
+  const int kvh = unit % a.Hkv;
+  const int wg_vh0 = qblk * NCB * 16;
+  const int vh = wg_vh0 + cb * 16 + col;
+  const bool col_ok = !producer && vh < a.GV;
+  const int lim = col_ok ? vhead_limit(a, vh) : 0;
+  int max_lim = 0;
+  for (int g = wg_vh0; g < min(wg_vh0 + NCB * 16, a.GV); ++g)
+    max_lim = max(max_lim, vhead_limit(a, g));
+  const int r_begin = split * a.rows_per_split;
+  const int r_end = min(r_begin + a.rows_per_split, max_lim);
+  const int nrows = max(r_end - r_begin, 0);
+  const int nsteps = (nrows + NP * TR - 1) / (NP * TR);
+  const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q;
+
+  // Ring stage st, tile p, tensor t: 32 rows x 256 bytes of fp16, 16-byte
+  // chunk c of row r at byte r * 256 + (c ^ (r % 16)) * 16.  Reused by the
+  // consumers' merge at the end.
+  constexpr int STAGE_BYTES = NP * 3 * TR * D * 2;
+  constexpr int MERGE_BYTES = NCB * (NP / 2) * 64 * 66 * 4;
+  static_assert(2 * STAGE_BYTES >= MERGE_BYTES, "merge fits the stages");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2][NP][3][TR * D * 2];
+
+  // Producers: thread p = tid - 256 handles row p / 8, 16-code chunk p % 8 of
+  // every (tile, tensor) block k = 0 .. CPT - 1 of a step (tile k / 3,
+  // tensor k % 3); eight lanes cover a row, so one load reads a tensor's
+  // 32 rows contiguously.
+  const int ptid = tid - NC * 64;
+  const int crow = (ptid & 255) >> 3;
+  const int cchunk = ptid & 7;
+  const int cgroup = 16 * cchunk / GS;
+  const long hrow0 = (long)unit * a.kv_cap + r_begin;
+  const unsigned dbytes = (unsigned)(nrows * RB);
+  const unsigned sbytes = (unsigned)(nrows * NG * 2);
+  const __amdgpu_buffer_rsrc_t rd[3] = {
+      stream_rsrc((const uint8_t*)a.kd + hrow0 * RB, dbytes),
+      stream_rsrc((const uint8_t*)a.v1d + hrow0 * RB, dbytes),
+      stream_rsrc((const uint8_t*)a.v2d + hrow0 * RB, dbytes)};
+  const __amdgpu_buffer_rsrc_t rsc[3] = {
+      stream_rsrc((const uint16_t*)a.ks + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v1s + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v2s + hrow0 * NG, sbytes)};
+  const __amdgpu_buffer_rsrc_t rbi[3] = {
+      stream_rsrc((const uint16_t*)a.kb + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v1b + hrow0 * NG, sbytes),
+      stream_rsrc((const uint16_t*)a.v2b + hrow0 * NG, sbytes)};
+  struct Packed {
+    uint32_t w[CPT][CB / 4];
+    uint32_t s[CPT], b[CPT];
+  };
+  auto load = [&](Packed& P, int step) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int t = k % 3;
+      const unsigned row = (unsigned)((step * NP + k / 3) * TR + crow);
+      const unsigned off = row * RB + (unsigned)(cchunk * CB);
+      if constexpr (CB == 16) {
+        const uint4 x = bload4(rd[t], off);
+        P.w[k][0] = x.x; P.w[k][1] = x.y; P.w[k][2] = x.z; P.w[k][3] = x.w;
+      } else {
+        const uint2 x = bload2(rd[t], off);
+        P.w[k][0] = x.x; P.w[k][1] = x.y;
+      }
+      const unsigned soff = (row * NG + (unsigned)cgroup) * 2u;
+      P.s[k] = __builtin_amdgcn_raw_buffer_load_b16(rsc[t], soff, 0, kCachePolicyStream);
+      P.b[k] = __builtin_amdgcn_raw_buffer_load_b16(rbi[t], soff, 0, kCachePolicyStream);
+    }
+  };
+  auto dequant_store = [&](const Packed& P, int st) {
+    const half2_t k1024 = half2_t{(_Float16)1024.f, (_Float16)1024.f};
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const uint32_t s16 = P.s[k] & 0xFFFFu, b16 = P.b[k] & 0xFFFFu;
+      const half2_t s2 = as_h2(s16 | (s16 << 16));
+      const half2_t b2 = as_h2(b16 | (b16 << 16));
+      const uint32_t* cw = P.w[k];
+      uint32_t h[8];  // codes (2i, 2i + 1) of the chunk
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t x;  // 1024 + u for both codes, as fp16 halves
+        if constexpr (BITS == 8) {
+          // bytes 2i%4, 2i%4 + 1 of word i / 2 under the exponent byte 0x64
+          x = __builtin_amdgcn_perm(0x64646464u, cw[i / 2], (i & 1) ? 0x04030402u : 0x04010400u);
+        } else {
+          // the two nibbles of byte i % 4 of word i / 4
+          const uint32_t by = (cw[i / 4] >> (8 * (i % 4))) & 0xFFu;
+          x = (by & 0xFu) | ((by >> 4) << 16) | 0x64006400u;
+        }
+        const half2_t u = as_h2(x) - k1024;
+        h[i] = h2_bits(__builtin_elementwise_fma(u, s2, b2));
+      }
+      uint8_t* base = ring[st][k / 3][k % 3] + crow * 256;
+      const int c0 = (2 * cchunk) ^ (crow % 16);
+      const int c1 = (2 * cchunk + 1) ^ (crow % 16);
+      *reinterpret_cast<uint4*>(base + c0 * 16) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(base + c1 * 16) = make_uint4(h[4], h[5], h[6], h[7]);
+    }
+  };
+
+  // Producers: step j's data in set A for even j, set B for odd j (loaded
+  // two steps ahead; steps past the last read past the resources' ends:
+  // zeros, no memory access).  The two roles run separate loops with the
+  // same barriers (one per step, then the merge's), so their registers do
+  // not add up; the step count is uniform over the workgroup, so every
+  // barrier is reached by all of its threads.
+  constexpr int kMergeBarriers = NP == 4 ? 4 : NP == 2 ? 2 : 0;
+  if (producer) {
+    Packed PA, PB;
+    // Step 0 alone first (it lands sooner with nothing queued behind it),
+    // then the next two.
+    load(PA, 0);
+    dequant_store(PA, 0);
+    load(PB, 1);
+    load(PA, 2);
+    qslab_barrier();
+    // Unrolled by two, so that the compiler's wait before each set's
+    // dequantisation counts the other set's loads as still in flight.
+    // (The scheduling barriers keep the dequantisation of the set due after
+    // a barrier from being hoisted above it, where its wait would also
+    // drain the loads of the other set.)
+    int j = 0;
+    for (; j + 1 < nsteps; j += 2) {
+      dequant_store(PB, 1);  // step j + 1
+      load(PB, j + 3);
+      qslab_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      dequant_store(PA, 0);  // step j + 2
+      load(PA, j + 4);
+      qslab_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (j < nsteps) {
+      dequant_store(PB, 1);
+      qslab_barrier();
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeBarriers; ++i) __syncthreads();
+    return;
+  }
+
+  Acc acc;
+  acc.init();
+  V8 qb[4];
+  {
+    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? vh : 0)) * D + 8 * blk;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
+      qb[s] = __builtin_bit_cast(V8, w);
+    }
+  }
+  qslab_barrier();
+  for (int j = 0; j < nsteps; ++j) {
+    acc.tile(ring[j & 1][tp][0], ring[j & 1][tp][1], ring[j & 1][tp][2], qb,
+             r_begin + (j * NP + tp) * TR, r_end, lim, a.qscale, col, blk);
+    qslab_barrier();
+  }
+
+  // The NP consumer waves of a column block merge their (m, l, o) through
+  // LDS (the ring is free after the last barrier); every wave takes part in
+  // the barriers.
+  if constexpr (NP > 1) {
+    float* xo = reinterpret_cast<float*>(&ring[0][0][0][0]);  // [NCB][NP / 2][64 lanes][66]
+#pragma unroll
+    for (int half = NP / 2; half >= 1; half /= 2) {
+      if (tp >= half && tp < 2 * half) {
+        float* p = xo + ((cb * (NP / 2) + tp - half) * 64 + lane) * 66;
+#pragma unroll
+        for (int jx = 0; jx < 8; ++jx) {
+          *reinterpret_cast<float4*>(p + 4 * jx) =
+              make_float4(acc.acc1[jx][0], acc.acc1[jx][1], acc.acc1[jx][2], acc.acc1[jx][3]);
+          *reinterpret_cast<float4*>(p + 32 + 4 * jx) =
+              make_float4(acc.acc2[jx][0], acc.acc2[jx][1], acc.acc2[jx][2], acc.acc2[jx][3]);
+        }
+        p[64] = acc.m_run;
+        p[65] = acc.accl[0];
+      }
+      __syncthreads();
+      if (tp < half) {
+        const float* p = xo + ((cb * (NP / 2) + tp) * 64 + lane) * 66;
+        const float m2 = p[64];
+        const float m = fmaxf(acc.m_run, m2);
+        const float f1 = fast_exp2(acc.m_run - m);
+        const float f2 = fast_exp2(m2 - m);
+#pragma unroll
+        for (int jx = 0; jx < 8; ++jx) {
+          const float4 o1 = *reinterpret_cast<const float4*>(p + 4 * jx);
+          const float4 o2 = *reinterpret_cast<const float4*>(p + 32 + 4 * jx);
+          acc.acc1[jx][0] = fmaf(acc.acc1[jx][0], f1, o1.x * f2);
+          acc.acc1[jx][1] = fmaf(acc.acc1[jx][1], f1, o1.y * f2);
+          acc.acc1[jx][2] = fmaf(acc.acc1[jx][2], f1, o1.z * f2);
+          acc.acc1[jx][3] = fmaf(acc.acc1[jx][3], f1, o1.w * f2);
+          acc.acc2[jx][0] = fmaf(acc.acc2[jx][0], f1, o2.x * f2);
+          acc.acc2[jx][1] = fmaf(acc.acc2[jx][1], f1, o2.y * f2);
+          acc.acc2[jx][2] = fmaf(acc.acc2[jx][2], f1, o2.z * f2);
+          acc.acc2[jx][3] = fmaf(acc.acc2[jx][3], f1, o2.w * f2);
+        }
+        acc.accl[0] = fmaf(acc.accl[0], f1, p[65] * f2);
+        acc.m_run = m;
+      }
+      __syncthreads();
+    }
+  }
+  if (tp > 0 || !col_ok) return;
+  acc.store(a, qrow0 + vh, split, blk);
+}
+
 }  // namespace motif

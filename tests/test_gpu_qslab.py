@@ -6,8 +6,10 @@ matrix cores with fp32 accumulation.
 
 Bars: max |gpu - oracle| <= 2e-3 against the oracle at that rounding point
 (``dequant_dtype="f16"``) and against exact dequant; the same bar against the
-head-chunk / column-block kernels (tuning ``qslab`` 0); both the 8-wave and
-the 4-wave variant.
+head-chunk / column-block kernels (tuning ``qslab`` 0); the 8-wave kernel
+with producer and consumer waves (dequantisation in packed fp16 beside the
+attention), the 8-wave kernel whose waves share each step, and the 4-wave
+variant.
 Shapes: 20 (the 5-row x GQA 4 slab), 17, 32, 36 and 64 virtual heads, group
 sizes 32/64/128, q4 and q8, causal and not, batch 2, short and odd kv_len,
 poisoned padding rows.
@@ -24,17 +26,21 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=[0, 4], ids=["w8", "w4"])
+@pytest.fixture(autouse=True, params=[(0, 1), (0, 0), (4, 1)], ids=["w8_roles", "w8", "w4"])
 def slab_kernel(request):
-    """Every slab on the slab kernel (qslab 2: 4-bit slabs too), in its
-    8-wave (default) and 4-wave variants."""
+    """Every slab on the slab kernel (qslab 2: 4-bit slabs too): 8 waves as
+    producers and consumers (default), 8 waves sharing every step's work,
+    and 4 waves."""
     from mlx_motif import _native
 
+    waves, roles = request.param
     _native.set_tuning("qslab", 2)
-    _native.set_tuning("waves_per_wg", request.param)
+    _native.set_tuning("waves_per_wg", waves)
+    _native.set_tuning("qslab_ws", roles)
     yield
-    _native.set_tuning("qslab", 1)
+    _native.set_tuning("qslab", 2)
     _native.set_tuning("waves_per_wg", 0)
+    _native.set_tuning("qslab_ws", 1)
 
 _CASES = [
     # B, Hq, Hkv, S, cap, kv_len, causal, bits, gs
