@@ -421,10 +421,13 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * "qpair" (packed caches at head_dim 128, group size 64/128: 1, the
  * default, decodes 4-bit caches with the paired-tile kernel; 2 also 8-bit
  * caches; 0 keeps the per-tile kernel for both), "qslab" (packed-cache
- * verify slabs of 17..64 virtual heads per KV head: 1, the default, runs 8-bit
- * slabs on the kernel that dequantises each tile once into LDS; 2 also
- * 4-bit slabs; 0 neither), "waves_per_wg" 4 also selects that kernel's
- * 4-wave variant,
+ * verify slabs of 17..64 virtual heads per KV head: 2, the default, runs 8-
+ * and 4-bit slabs on the kernel that dequantises each tile once into LDS;
+ * 1 only 8-bit slabs; 0 neither), "waves_per_wg" 4 also selects that
+ * kernel's 4-wave variant, "qslab_ws" (1, the default: its 8-wave variant
+ * runs four producer waves beside four consumer waves; 0: every wave does
+ * both), "merge_rows" (1, the default: a merge launch of at least 2048
+ * partial rows runs one wave per row; 0: one wave per row slice),
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
  * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.

@@ -158,6 +158,8 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   if (nsplit > kMaxSplits) nsplit = kMaxSplits;
   if (nsplit < 1) nsplit = 1;
   int rps = (rows + nsplit - 1) / nsplit;
+  if (tuning().rows_per_split > 0)  // forced split size, at most kMaxSplits splits
+    rps = std::max(tuning().rows_per_split, (rows + kMaxSplits - 1) / kMaxSplits);
   rps = (rps + kPrefillTileRowsHost - 1) / kPrefillTileRowsHost * kPrefillTileRowsHost;
   p.rows_per_split = rps;
   p.nsplit = (rows + rps - 1) / rps;
@@ -330,11 +332,17 @@ int motif_set_tuning(const char* key, int value) {
     }
     update_tuning([&](Tuning& t) { t.qslab = value; });
   } else if (!strcmp(key, "qslab_ws")) {
-    if (value > 1) {
+    if (value < 0 || value > 1) {
       set_error("motif_set_tuning: qslab_ws must be 0 or 1");
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.qslab_ws = value; });
+  } else if (!strcmp(key, "merge_rows")) {
+    if (value < 0 || value > 1) {
+      set_error("motif_set_tuning: merge_rows must be 0 or 1");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.merge_rows = value; });
   } else if (!strcmp(key, "poly_rows")) {
     update_tuning([&](Tuning& t) { t.poly_rows = value; });
   } else {

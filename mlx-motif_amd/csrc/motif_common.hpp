@@ -41,6 +41,7 @@ struct Tuning {
   int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 q4, 2 q4+q8
   int qslab = 2;           // slabs of 17..64 virtual heads, tiles dequantised into LDS: 0 off, 1 q8, 2 q4+q8
   int qslab_ws = 1;        // slab kernel with producer / consumer waves (8 waves): 1 on, 0 off
+  int merge_rows = 1;      // row-per-wave merge launch from 2048 partial rows: 1 on, 0 off
 };
 // The calling thread's snapshot of the process-wide knobs.  Inside a
 // CallScope it is the copy taken when the outermost scope opened, so every

@@ -564,11 +564,93 @@ __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
   }
 }
 
+// Merge launch for many partial rows (prefill chunks, long slabs split over
+// few workgroups each): one wave per row, lane c holding float4 columns c,
+// c + 64, .. of the row's 2D channels, four rows per workgroup.  The
+// one-wave workgroups of sdpa_merge_kernel are capped by how many
+// workgroups a CU holds at once (16384 rows x 4 slices of a 512-row chunk
+// took ~24 us for 34 MB); here the splits are taken in batches of 8 with
+// every load of a batch issued before any is consumed, and the running
+// maximum rescales earlier batches.  With at most 8 splits the result is
+// sum_s o_s * exp2(m_s - M) in split order, M the largest m_s.
+constexpr int kMergeRowsMin = 2048;  // rows from which the row-per-wave merge runs
+template <typename T, int D>
+__global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long rows) {
+  constexpr int C4 = 2 * D / 4;
+  constexpr int CPL = (C4 + 63) / 64;  // float4 columns per lane
+  constexpr int NB = 8;                // splits per batch
+  const int lane = threadIdx.x & 63;
+  const long vrow = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (vrow >= rows) return;
+  const int ns = a.nsplit;
+  const float4* po = reinterpret_cast<const float4*>(a.part_o + vrow * ns * 2 * D);
+  const float2* pml = reinterpret_cast<const float2*>(a.part_ml + vrow * ns * 2);
+  float4 acc[CPL];
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  float M = kNegSentinel, L = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += NB) {
+    float2 ml[NB];
+    float4 v[NB][CPL];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int s = s0 + j;
+      ml[j] = s < ns ? pml[s] : make_float2(kNegSentinel, 0.f);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const int c = lane + 64 * k;
+        v[j][k] = s < ns && c < C4 ? po[(long)s * C4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float Mb = M;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) Mb = fmaxf(Mb, ml[j].x);
+    if (s0 > 0) {
+      const float r = fast_exp2(M - Mb);
+      L *= r;
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        acc[k].x *= r;
+        acc[k].y *= r;
+        acc[k].z *= r;
+        acc[k].w *= r;
+      }
+    }
+    M = Mb;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const float f = fast_exp2(ml[j].x - M);  // 0 for splits past ns (sentinel m)
+      L = fmaf(ml[j].y, f, L);
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        acc[k].x = fmaf(v[j][k].x, f, acc[k].x);
+        acc[k].y = fmaf(v[j][k].y, f, acc[k].y);
+        acc[k].z = fmaf(v[j][k].z, f, acc[k].z);
+        acc[k].w = fmaf(v[j][k].w, f, acc[k].w);
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int c = lane + 64 * k;
+    if (c >= C4) continue;
+    if (a.y2 != nullptr && vrow >= a.y2_row0)  // second output (fused prefill's noise pass)
+      store_y4_to<T, D>(a.y2, (vrow - a.y2_row0) * 2 * D + c * 4, acc[k], L);
+    else
+      store_y4<T, D>(a, vrow * 2 * D + c * 4, acc[k], L);
+  }
+}
+
 template <typename T, int D>
 int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
   constexpr int C4 = 2 * D / 4;
   constexpr int NSL = C4 / (C4 < 16 ? C4 : 16);
   const long rows = (long)a.B * a.Hq * a.S_q;
+  if (rows >= kMergeRowsMin && tuning().merge_rows) {
+    hipLaunchKernelGGL((sdpa_merge_rows_kernel<T, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256),
+                       0, s, a, rows);
+    return check_launch("sdpa split merge (rows)");
+  }
   hipLaunchKernelGGL((sdpa_merge_kernel<T, D>), dim3(merge_grid_blocks(a, NSL, rows, a.G * a.S_q)),
                      dim3(64), 0, s, a);
   return check_launch("sdpa split merge");

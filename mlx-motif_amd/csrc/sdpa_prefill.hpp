@@ -131,13 +131,13 @@ struct SwizzledTileAcc {
     }
   }
 
-  // Mask, online softmax and both PV products of a tile with scores sacc.
-  // Rows row0 + 16*h + 4*blk + r of the tile hold k index 8*blk + 4*h + r of
-  // the PV products (as in the decode kernel); rows at or past r_end or lim
-  // are masked.
-  __device__ __forceinline__ void update(const floatx4 (&sacc)[2], const uint8_t* V1t,
-                                         const uint8_t* V2t, int row0, int r_end, int lim,
-                                         float qscale, int col, int blk) {
+  // Mask and online softmax of a tile with scores sacc: returns P^T, the B
+  // operand of the PV products, after rescaling the accumulators when the
+  // running maximum moved past the lazy-rescale slack.  Rows row0 + 16*h +
+  // 4*blk + r of the tile hold k index 8*blk + 4*h + r of the PV products (as
+  // in the decode kernel); rows at or past r_end or lim are masked.
+  __device__ __forceinline__ V8 softmax(const floatx4 (&sacc)[2], int row0, int r_end, int lim,
+                                        float qscale, int blk) {
     float sc[8];
     float mx = kNegSentinel;
 #pragma unroll
@@ -166,7 +166,12 @@ struct SwizzledTileAcc {
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+    return pb;
+  }
 
+  // Both PV products and l of a tile with softmax weights pb.
+  __device__ __forceinline__ void pv(const V8& pb, const uint8_t* V1t, const uint8_t* V2t, int col,
+                                     int blk) {
     // V^T fragments straight from LDS with transposing reads
     // (ds_read_b64_tr_b16).  In the 16-lane group of lanes with one blk,
     // lane 4*jj + q points at 4 channels of row 16*h + 4*blk + jj, and group
@@ -195,6 +200,14 @@ struct SwizzledTileAcc {
     const typename Op::S one = Op::from_f32(1.f);
     const V8 ones = {one, one, one, one, one, one, one, one};
     accl = Op::mma(ones, pb, accl);
+  }
+
+  // Mask, online softmax and both PV products of a tile with scores sacc.
+  __device__ __forceinline__ void update(const floatx4 (&sacc)[2], const uint8_t* V1t,
+                                         const uint8_t* V2t, int row0, int r_end, int lim,
+                                         float qscale, int col, int blk) {
+    const V8 pb = softmax(sacc, row0, r_end, lim, qscale, blk);
+    pv(pb, V1t, V2t, col, blk);
   }
 
   // One tile: scores() then update().
@@ -327,6 +340,8 @@ sdpa_prefill_kernel(SdpaArgs a) {
 
   SwizzledTileAcc<T> st_acc;
   st_acc.init();
+  const int nrows = max(r_end - r_begin, 0);
+  const int ntiles = (nrows + TR - 1) / TR;
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
   // all of its threads.  Software-pipelined over tiles: the S^T products of
@@ -336,8 +351,6 @@ sdpa_prefill_kernel(SdpaArgs a) {
   // is refilled with tile i + NS - 2 right after it (barrier 0 fills stage
   // NS - 1, unused until then): NS - 2 tiles in flight ahead of the two
   // being worked on.
-  const int nrows = max(r_end - r_begin, 0);
-  const int ntiles = (nrows + TR - 1) / TR;
   int inflight = 0;
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t) {

@@ -105,6 +105,11 @@ def test_workspace_sizing_and_tuning():
     assert big <= counters + 32 * 256 * (2 * 128 + 2) * 4 + 512
     with pytest.raises(_native.MotifNativeError):
         _native.set_tuning("no_such_knob", 1)
+    for key in ("qslab_ws", "merge_rows"):  # switches take 0 or 1 only
+        for bad in (-1, 2):
+            with pytest.raises(_native.MotifNativeError):
+                _native.set_tuning(key, bad)
+        _native.set_tuning(key, 1)
     _native.set_tuning("rows_per_split", 64)
     forced = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128)
     _native.set_tuning("rows_per_split", 0)

@@ -100,3 +100,31 @@ def test_prefill_agrees_with_valu_kernels(gpu, rng):
     finally:
         _native.set_tuning("mfma", 1)
     assert float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2)))) <= 2e-3
+
+
+@pytest.mark.parametrize("S,cap,kv_len,tag", [
+    (64, 3328, 3204, "f16"),     # 2048 partial rows over 16 splits: two batches of 8
+    (512, 3840, 3716, "f16"),    # the 512-row chunk: 16384 rows, 2 splits
+    (64, 3328, 3204, "bf16"),
+])
+def test_merge_launch_row_per_wave(gpu, rng, S, cap, kv_len, tag):
+    """From 2048 partial rows the merge launch runs one wave per row (splits
+    in batches of 8, the running maximum rescaling earlier batches); it
+    matches the oracle and the one-wave-per-slice merge it replaces."""
+    import torch
+
+    from conftest import torch_dtype
+    from mlx_motif import _native
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    err, y, (q, k, v1, v2) = _run(gpu, rng, 1, 32, 8, S, cap, kv_len, True, tag=tag)
+    assert err <= (2e-3 if tag == "f16" else 1e-2), f"{err:.3e}"
+    T = lambda a: np_to_torch(a, torch_dtype(tag), gpu)  # noqa: E731
+    _native.set_tuning("merge_rows", 0)
+    try:
+        y2 = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=kv_len, causal=True)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning("merge_rows", 1)
+    d = float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2))))
+    assert d <= (1e-3 if tag == "f16" else 8e-3), f"{d:.3e}"
