@@ -71,11 +71,33 @@ struct MfmaOp<bf16_t> {
 // the matrix cores take as fp16 or bf16: 2^8 leaves p a wide margin.
 constexpr float kRescaleSlackF16 = 8.f;
 
-// Causal row limit of virtual head vh (see sdpa_dual_v_kernel).
-__device__ inline int vhead_limit(const SdpaArgs& a, int vh) {
-  const int s = vh % a.S_q;
+// Causal row limit of query row s (see sdpa_dual_v_kernel).
+__device__ inline int row_limit(const SdpaArgs& a, int s) {
   int L = a.causal ? a.kv_len - a.S_q + s + 1 : a.kv_len;
   return L < 0 ? 0 : (L > a.kv_len ? a.kv_len : L);
+}
+// Causal row limit of virtual head vh (query row vh % S_q).
+__device__ inline int vhead_limit(const SdpaArgs& a, int vh) { return row_limit(a, vh % a.S_q); }
+// Largest (hi) and smallest (lo) vhead_limit over the virtual heads v0 ..
+// v0 + n - 1 without a division per head: the limit grows with the query
+// row, so the extremes sit at the range's first and last rows, or at rows
+// S_q - 1 and 0 once the range crosses into the next head.  n <= 0: hi 0, lo
+// kv_len (the empty maximum and minimum).
+__device__ inline void vhead_limit_range(const SdpaArgs& a, int v0, int n, int& lo, int& hi) {
+  if (n <= 0) {
+    lo = a.kv_len;
+    hi = 0;
+    return;
+  }
+  const int s0 = v0 % a.S_q;
+  const bool wraps = s0 + n > a.S_q;
+  lo = row_limit(a, wraps ? 0 : s0);
+  hi = row_limit(a, wraps ? a.S_q - 1 : s0 + n - 1);
+}
+__device__ inline int vhead_limit_max(const SdpaArgs& a, int v0, int n) {
+  int lo, hi;
+  vhead_limit_range(a, v0, n, lo, hi);
+  return hi;
 }
 
 // Append (fused decode step): the wave whose tiles include row kv_len - 1
@@ -175,8 +197,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
   const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
                           : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
-  int max_lim = 0;
-  for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
+  const int max_lim = vhead_limit_max(a, vh0, nvh);
   const bool col_ok = col < nvh;
   const int lim = col_ok ? vhead_limit(a, vh0 + col) : 0;  // <= max_lim
 

@@ -349,8 +349,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int gsel = grp < NG ? grp : 0;  // group whose scales this lane reads
   // v_perm selector keeping half (gsel & 1) of two words: low word = row r.
   const uint32_t sel = (gsel & 1) ? 0x07060302u : 0x05040100u;
-  int max_lim = 0;
-  for (int g = 0; g < nvh; ++g) max_lim = max(max_lim, vhead_limit(a, vh0 + g));
+  const int max_lim = vhead_limit_max(a, vh0, nvh);
   // Rows are dealt to the splits in blocks of NW 16-row tiles, round robin,
   // as in sdpa_mfma_kernel: tile k of wave w in split s is tile
   // (k * nsplit + s) * NW + w of the KV head.  The resources cover rows

@@ -285,9 +285,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + wave * 16 + col;  // this lane's virtual head (column)
   const bool col_ok = vh < a.GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  int max_lim = 0;
-  for (int g = wg_vh0; g < min(wg_vh0 + NW * 16, a.GV); ++g)
-    max_lim = max(max_lim, vhead_limit(a, g));
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q;  // row of virtual head 0
@@ -491,9 +489,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + wave * 16 + col;  // virtual head (pass head vh / S, query row vh % S)
   const bool col_ok = vh < GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  int max_lim = 0;
-  for (int g = wg_vh0; g < min(wg_vh0 + NW * 16, GV); ++g)
-    max_lim = max(max_lim, vhead_limit(a, g));
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16, GV - wg_vh0));
 
   const int row0 = a.kv_len - S;  // the chunk's first cache row
   const int split_begin = split * a.rows_per_split;

@@ -120,12 +120,8 @@ sdpa_qpair_kernel(SdpaArgs a) {
   const int g = col % NG;   // scale group of this column
   const bool used = col < GC * NG && hh < nvh;
   const int lim = used ? vhead_limit(a, vh0 + hh) : 0;
-  int max_lim = 0, min_lim = a.kv_len;
-  for (int v = 0; v < nvh; ++v) {
-    const int L = vhead_limit(a, vh0 + v);
-    max_lim = max(max_lim, L);
-    min_lim = min(min_lim, L);
-  }
+  int max_lim, min_lim;
+  vhead_limit_range(a, vh0, nvh, min_lim, max_lim);
   // v_perm selector keeping half g of two (row, group) words: NG = 2.
   const uint32_t sel = g ? 0x07060302u : 0x05040100u;
 

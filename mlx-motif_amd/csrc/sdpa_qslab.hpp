@@ -70,9 +70,7 @@ sdpa_qslab_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + cb * 16 + col;  // this lane's virtual head (column)
   const bool col_ok = vh < a.GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  int max_lim = 0;
-  for (int g = wg_vh0; g < min(wg_vh0 + NCB * 16, a.GV); ++g)
-    max_lim = max(max_lim, vhead_limit(a, g));
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NCB * 16, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const int nrows = max(r_end - r_begin, 0);
@@ -335,9 +333,7 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + cb * 16 + col;
   const bool col_ok = !producer && vh < a.GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  int max_lim = 0;
-  for (int g = wg_vh0; g < min(wg_vh0 + NCB * 16, a.GV); ++g)
-    max_lim = max(max_lim, vhead_limit(a, g));
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NCB * 16, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const int nrows = max(r_end - r_begin, 0);
