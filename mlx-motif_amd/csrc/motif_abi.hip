@@ -149,7 +149,16 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   // rows 4 waves are faster, 41 vs 47 us).
   p.waves = GV >= 512 ? 8 : 4;
   if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
-  p.nqb = (GV + p.waves * 16 - 1) / (p.waves * 16);
+  // Two column blocks per wave (256 virtual heads per 8-wave block: each
+  // K/V fragment read from LDS feeds twice the MFMAs) from 2048 virtual heads
+  // per KV head.  Measured, 32 q-heads over 8 KV heads, one / two blocks:
+  // 256 rows over 3204 55.4 / 61.9 us, 512 over 3716 90.3 / 87.3, 1024 over
+  // 4228 145.6 / 138.8, 2048 over 4228 283.5 / 210.0, 4096 over 8192
+  // 1005.9 / 781.1 (1.06 PFLOP/s).
+  const int ncb_t = tuning().prefill_ncb;
+  p.ncb = p.waves == 8 && (ncb_t == 2 || (ncb_t == 0 && GV >= 2048)) ? 2 : 1;
+  const int cols = p.waves * 16 * p.ncb;
+  p.nqb = (GV + cols - 1) / cols;
   const long units = (long)bh * p.nqb;
   const int rows = kv_len > 0 ? kv_len : 1;
   int nsplit = units >= cus ? 1 : (int)((cus + units - 1) / units);
@@ -343,6 +352,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.merge_rows = value; });
+  } else if (!strcmp(key, "prefill_ncb")) {
+    if (value < 0 || value > 2) {
+      set_error("motif_set_tuning: prefill_ncb must be 0, 1 or 2");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.prefill_ncb = value; });
   } else if (!strcmp(key, "poly_rows")) {
     update_tuning([&](Tuning& t) { t.poly_rows = value; });
   } else {

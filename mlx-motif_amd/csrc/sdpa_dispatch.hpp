@@ -49,9 +49,9 @@ int launch_gda_decode_q_f32(const SdpaArgs& a, int bits, int gc, int nblocks, hi
 
 // Multi-row attention with LDS-shared K/V tiles; the f16 and bf16 instances
 // have a kernel (head_dim 128).
-int launch_sdpa_prefill_f16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
-int launch_sdpa_prefill_bf16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
-int launch_sdpa_prefill_f32(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
+int launch_sdpa_prefill_f16(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
+int launch_sdpa_prefill_bf16(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
+int launch_sdpa_prefill_f32(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
 
 // A GDA layer's prefill chunk from the projection outputs (RoPE, the
 // chunk's cache rows and both dual-V passes in one launch); f16 and bf16

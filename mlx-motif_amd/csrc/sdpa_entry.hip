@@ -134,8 +134,8 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
       a.part_ml = (float*)(w + cbytes + obytes);
     }
     const int nblocks = sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit);
-    rc = dtype == MOTIF_F16 ? launch_sdpa_prefill_f16(a, pp.waves, nblocks, s)
-                            : launch_sdpa_prefill_bf16(a, pp.waves, nblocks, s);
+    rc = dtype == MOTIF_F16 ? launch_sdpa_prefill_f16(a, pp.waves, pp.ncb, nblocks, s)
+                            : launch_sdpa_prefill_bf16(a, pp.waves, pp.ncb, nblocks, s);
     return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
   }
   switch (dtype) {

@@ -113,11 +113,11 @@ int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int n
 
 // Multi-row attention with LDS-shared K/V tiles (fp16 or bf16 cache,
 // head_dim 128).
-int MOTIF_CAT(launch_sdpa_prefill_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, int nblocks,
+int MOTIF_CAT(launch_sdpa_prefill_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, int ncb, int nblocks,
                                                  hipStream_t s) {
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
                 std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    return launch_prefill_kernel_16<MOTIF_ELEM>(a, waves, nblocks, s);
+    return launch_prefill_kernel_16<MOTIF_ELEM>(a, waves, ncb, nblocks, s);
   }
   set_error("sdpa_dual_v_rows: no shared-tile variant for this element type");
   return MOTIF_ERR_UNSUPPORTED;

@@ -129,6 +129,7 @@ constexpr int kPrefillMinHeads = 64;
 constexpr int kPrefillTileRowsHost = 32;  // KV rows per tile (kPrefillTileRows)
 struct PrefillPlan {
   int waves;  // 4 or 8
+  int ncb;    // column blocks of 16 virtual heads per wave (1 or 2)
   int nqb;    // query blocks per (b, KV head)
   int nsplit, rows_per_split;
   size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1

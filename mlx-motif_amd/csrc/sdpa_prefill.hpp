@@ -262,10 +262,70 @@ struct SwizzledTileAcc {
   }
 };
 
+// S^T = K Q^T of a tile for NCB column blocks (16 columns each) of one
+// wave: each K fragment is read from LDS once and used by every block.
+template <typename T, int NCB>
+__device__ __forceinline__ void tile_scores_n(const uint8_t* Kt,
+                                              const typename MfmaOp<T>::V8 (&qb)[NCB][4],
+                                              floatx4 (&sacc)[NCB][2], int col, int blk) {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) sacc[cb][h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int kr = 16 * h + col;
+      const V8 ka = __builtin_bit_cast(
+          V8, *reinterpret_cast<const uint4*>(&Kt[kr * 256 + (((4 * s + blk) ^ (kr % 16)) * 16)]));
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) sacc[cb][h] = Op::mma(ka, qb[cb][s], sacc[cb][h]);
+    }
+  }
+}
+
+// Both PV products and l of a tile for NCB column blocks: each V^T fragment
+// (SwizzledTileAcc::pv's transposing reads) is read once for every block.
+template <typename T, int NCB>
+__device__ __forceinline__ void tile_pv_n(SwizzledTileAcc<T> (&acc)[NCB],
+                                          const typename MfmaOp<T>::V8 (&pb)[NCB],
+                                          const uint8_t* V1t, const uint8_t* V2t, int col,
+                                          int blk) {
+  using Op = MfmaOp<T>;
+  using V8 = typename Op::V8;
+  const int jj = col >> 2;
+  const int qq = col & 3;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint2 f1[2], f2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int vr = 16 * h + 4 * blk + jj;
+      const int o = vr * 256 + (((4 * qq + j / 2) ^ (vr % 16)) * 16) + (j % 2) * 8;
+      f1[h] = lds_read_tr16(&V1t[o]);
+      f2[h] = lds_read_tr16(&V2t[o]);
+    }
+    const V8 a1 = __builtin_bit_cast(V8, make_uint4(f1[0].x, f1[0].y, f1[1].x, f1[1].y));
+    const V8 a2 = __builtin_bit_cast(V8, make_uint4(f2[0].x, f2[0].y, f2[1].x, f2[1].y));
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      acc[cb].acc1[j] = Op::mma(a1, pb[cb], acc[cb].acc1[j]);
+      acc[cb].acc2[j] = Op::mma(a2, pb[cb], acc[cb].acc2[j]);
+    }
+  }
+  const typename Op::S one = Op::from_f32(1.f);
+  const V8 ones = {one, one, one, one, one, one, one, one};
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) acc[cb].accl = Op::mma(ones, pb[cb], acc[cb].accl);
+}
+
 // The ring's LDS holds one workgroup per CU: two waves per SIMD at 8 waves,
 // one at 4.
 // T: half_t (fp16 cache) or bf16_t (bf16 cache, bf16 matrix cores).
-template <typename T, int NW, int NS = kPrefillStages>
+// NCB: column blocks of 16 virtual heads per wave (2: every K/V fragment
+// read from LDS feeds two blocks' MFMAs, half the LDS reads per head).
+template <typename T, int NW, int NS = kPrefillStages, int NCB = 1>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 sdpa_prefill_kernel(SdpaArgs a) {
   using Op = MfmaOp<T>;
@@ -281,29 +341,37 @@ sdpa_prefill_kernel(SdpaArgs a) {
   if (!prefill_block_coords(a, blockIdx.x, qblk, unit, split)) return;  // grid padding
   const int b = unit / a.Hkv;
   const int kvh = unit % a.Hkv;
-  const int wg_vh0 = qblk * NW * 16;
-  const int vh = wg_vh0 + wave * 16 + col;  // this lane's virtual head (column)
-  const bool col_ok = vh < a.GV;
-  const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16, a.GV - wg_vh0));
+  const int wg_vh0 = qblk * NW * 16 * NCB;
+  int vh[NCB], lim[NCB];
+  bool col_ok[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    vh[cb] = wg_vh0 + (wave * NCB + cb) * 16 + col;  // this lane's virtual heads (columns)
+    col_ok[cb] = vh[cb] < a.GV;
+    lim[cb] = col_ok[cb] ? vhead_limit(a, vh[cb]) : 0;
+  }
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16 * NCB, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
   const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q;  // row of virtual head 0
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds its column's
   // channels 32*s + 8*blk .. +7 for k-step s.
-  V8 qb[4];
-  {
-    const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? vh : 0)) * D + 8 * blk;
+  V8 qb[NCB][4];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const uint16_t* qp =
+        (const uint16_t*)a.q + (qrow0 + (col_ok[cb] ? vh[cb] : 0)) * D + 8 * blk;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
-      qb[s] = __builtin_bit_cast(V8, w);
+      const uint4 w =
+          col_ok[cb] ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
+      qb[cb][s] = __builtin_bit_cast(V8, w);
     }
     // q is waited for here, before the first tile copies are issued: the
     // compiler's own wait would otherwise sit inside the tile loop and, as
     // vmcnt(0), drain the copies in flight on every iteration.
-    asm volatile("" ::"v"(qb[0]), "v"(qb[1]), "v"(qb[2]), "v"(qb[3]));
+    asm volatile("" ::"v"(qb[cb][0]), "v"(qb[cb][1]), "v"(qb[cb][2]), "v"(qb[cb][3]));
   }
 
   // Rows [r_begin, r_end) of this KV head through range-checked resources.
@@ -336,8 +404,9 @@ sdpa_prefill_kernel(SdpaArgs a) {
     }
   };
 
-  SwizzledTileAcc<T> st_acc;
-  st_acc.init();
+  SwizzledTileAcc<T> st_acc[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) st_acc[cb].init();
   const int nrows = max(r_end - r_begin, 0);
   const int ntiles = (nrows + TR - 1) / TR;
 
@@ -367,30 +436,49 @@ sdpa_prefill_kernel(SdpaArgs a) {
       ++inflight;
     }
   };
-  floatx4 s_cur[2], s_nxt[2];
-  if (ntiles > 0) {
-    publish(0);
-    SwizzledTileAcc<T>::scores(ring[0][0], qb, s_cur, col, blk);
-  }
-  for (int i = 0; i < ntiles; ++i) {
-    if (i + 1 < ntiles) {
-      publish(i + 1);
-      SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb, s_nxt, col, blk);
+  if constexpr (NCB == 1) {
+    floatx4 s_cur[2], s_nxt[2];
+    if (ntiles > 0) {
+      publish(0);
+      SwizzledTileAcc<T>::scores(ring[0][0], qb[0], s_cur, col, blk);
     }
-    st_acc.update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end, lim,
-                  a.qscale, col, blk);
-    s_cur[0] = s_nxt[0];
-    s_cur[1] = s_nxt[1];
+    for (int i = 0; i < ntiles; ++i) {
+      if (i + 1 < ntiles) {
+        publish(i + 1);
+        SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb[0], s_nxt, col, blk);
+      }
+      st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end, lim[0],
+                       a.qscale, col, blk);
+      s_cur[0] = s_nxt[0];
+      s_cur[1] = s_nxt[1];
+    }
+  } else {
+    // One tile per barrier (publish(i) frees the stage of tile i - 2 as above).
+    for (int i = 0; i < ntiles; ++i) {
+      publish(i);
+      floatx4 sacc[NCB][2];
+      tile_scores_n<T, NCB>(ring[i % NS][0], qb, sacc, col, blk);
+      V8 pb[NCB];
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb)
+        pb[cb] = st_acc[cb].softmax(sacc[cb], r_begin + i * TR, r_end, lim[cb], a.qscale, blk);
+      tile_pv_n<T, NCB>(st_acc, pb, ring[i % NS][1], ring[i % NS][2], col, blk);
+    }
   }
 
   // acc[j][r] of lane (col, blk) is channel 32*blk + 4*j + r of column col.
-  if (!col_ok) return;
-  st_acc.store(a, qrow0 + vh, split, blk);
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+    if (col_ok[cb]) st_acc[cb].store(a, qrow0 + vh[cb], split, blk);
 }
 
 template <typename T>
-inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int nblocks, hipStream_t st) {
-  if (waves == 8) {
+inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int ncb, int nblocks,
+                                   hipStream_t st) {
+  if (waves == 8 && ncb == 2) {
+    hipLaunchKernelGGL((sdpa_prefill_kernel<T, 8, kPrefillStages, 2>), dim3(nblocks), dim3(512),
+                       0, st, a);
+  } else if (waves == 8) {
     hipLaunchKernelGGL((sdpa_prefill_kernel<T, 8>), dim3(nblocks), dim3(512), 0, st, a);
   } else {
     hipLaunchKernelGGL((sdpa_prefill_kernel<T, 4>), dim3(nblocks), dim3(256), 0, st, a);

@@ -110,6 +110,10 @@ def test_workspace_sizing_and_tuning():
             with pytest.raises(_native.MotifNativeError):
                 _native.set_tuning(key, bad)
         _native.set_tuning(key, 1)
+    for bad in (-1, 3):
+        with pytest.raises(_native.MotifNativeError):
+            _native.set_tuning("prefill_ncb", bad)
+    _native.set_tuning("prefill_ncb", 0)
     _native.set_tuning("rows_per_split", 64)
     forced = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128)
     _native.set_tuning("rows_per_split", 0)

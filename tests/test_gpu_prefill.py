@@ -128,3 +128,24 @@ def test_merge_launch_row_per_wave(gpu, rng, S, cap, kv_len, tag):
         _native.set_tuning("merge_rows", 1)
     d = float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2))))
     assert d <= (1e-3 if tag == "f16" else 8e-3), f"{d:.3e}"
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,S,cap,kv_len,tag", [
+    (1, 32, 8, 200, 1024, 1000, "f16"),   # 800 heads per KV head: a ragged 256-head block
+    (2, 40, 8, 130, 512, 400, "f16"),     # batch 2, GQA 5
+    (1, 32, 8, 512, 3840, 3716, "f16"),   # the 512-row chunk (2 blocks per wave by default)
+    (1, 32, 8, 512, 3840, 3716, "bf16"),
+])
+@pytest.mark.parametrize("ncb", [1, 2])
+def test_prefill_column_blocks_per_wave(gpu, rng, B, Hq, Hkv, S, cap, kv_len, tag, ncb):
+    """The 8-wave kernel with one or two 16-head column blocks per wave (two:
+    each K/V fragment read from LDS feeds both blocks' MFMAs) against the
+    oracle."""
+    from mlx_motif import _native
+
+    _native.set_tuning("prefill_ncb", ncb)
+    try:
+        err, *_ = _run(gpu, rng, B, Hq, Hkv, S, cap, kv_len, True, poison=True, tag=tag)
+    finally:
+        _native.set_tuning("prefill_ncb", 0)
+    assert err <= (2e-3 if tag == "f16" else 1e-2), f"ncb={ncb} S={S} {tag}: {err:.3e}"
