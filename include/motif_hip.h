@@ -429,8 +429,8 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * both), "merge_rows" (1, the default: a merge launch of at least 2048
  * partial rows runs one wave per row; 0: one wave per row slice),
  * "prefill_ncb" (column blocks of 16 virtual heads per wave of the 8-wave
- * shared-tile kernel: 0, the default, takes 2 from 2048 virtual heads per
- * KV head, else 1; 1 or 2 forces it),
+ * shared-tile kernels: 0, the default, takes 2 from 2048 virtual heads per
+ * KV head over at least 2048 rows, else 1; 1 or 2 forces it),
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
  * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.

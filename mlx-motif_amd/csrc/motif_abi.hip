@@ -151,12 +151,14 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
   // Two column blocks per wave (256 virtual heads per 8-wave block: each
   // K/V fragment read from LDS feeds twice the MFMAs) from 2048 virtual heads
-  // per KV head.  Measured, 32 q-heads over 8 KV heads, one / two blocks:
+  // per KV head over at least 2048 rows (on fewer rows the halved block
+  // count costs more than the LDS reads save: a first 512-row layer chunk
+  // 42.8 vs 55.5 us).  Measured, 32 q-heads over 8 KV heads, one / two blocks:
   // 256 rows over 3204 55.4 / 61.9 us, 512 over 3716 90.3 / 87.3, 1024 over
   // 4228 145.6 / 138.8, 2048 over 4228 283.5 / 210.0, 4096 over 8192
   // 1005.9 / 781.1 (1.06 PFLOP/s).
   const int ncb_t = tuning().prefill_ncb;
-  p.ncb = p.waves == 8 && (ncb_t == 2 || (ncb_t == 0 && GV >= 2048)) ? 2 : 1;
+  p.ncb = p.waves == 8 && (ncb_t == 2 || (ncb_t == 0 && GV >= 2048 && kv_len >= 2048)) ? 2 : 1;
   const int cols = p.waves * 16 * p.ncb;
   p.nqb = (GV + cols - 1) / cols;
   const long units = (long)bh * p.nqb;
@@ -186,24 +188,34 @@ GdaPrefillPlan plan_gda_prefill(int B, int Hkv, int G_origin, int G_noise, int S
   GdaPrefillPlan p{};
   p.waves = G_origin * S >= 512 ? 8 : 4;  // as plan_prefill
   if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
-  const int cols = p.waves * 16;
+  const int ncb_t = tuning().prefill_ncb;  // as plan_prefill
+  p.ncb = p.waves == 8 && (ncb_t == 2 || (ncb_t == 0 && G_origin * S >= 2048 && kv_len >= 2048))
+              ? 2
+              : 1;
+  const int cols = p.waves * 16 * p.ncb;
   p.nqb_origin = (G_origin * S + cols - 1) / cols;
   p.nqb_noise = (G_noise * S + cols - 1) / cols;
   const long units = (long)B * Hkv * (p.nqb_origin + p.nqb_noise);
   const int cus = device_cu_count();
   const int rows = kv_len > 0 ? kv_len : 1;
+  const int tiles = (rows + kPrefillTileRowsHost - 1) / kPrefillTileRowsHost;
   int nsplit = 1;
   if (tuning().rows_per_split > 0) {
     const int rps = (int)round_up((size_t)tuning().rows_per_split, kPrefillTileRowsHost);
     nsplit = (rows + rps - 1) / rps;
   } else if (units < cus / 2) {
-    // Workgroups hold one CU each (the LDS ring).  Rows are split only when
-    // the query blocks leave most CUs idle, into as many splits as keep the
-    // workgroups within one round: with 160 blocks on 256 CUs (a
-    // 512-row chunk of 32 + 8 heads over 8 KV heads, 3716 rows) one split
-    // measured 178 us, 2 / 3 / 4 / 8 splits 229 / 198 / 222 / 255 us (the
-    // partials, the merge launch and a second round of workgroups).
-    nsplit = (int)std::min<long>(std::max<long>(cus / units, 1), std::max(1, (rows + 127) / 128));
+    // Workgroups hold one CU each (the LDS ring).  Few query blocks: as many
+    // splits (tiles dealt round robin) as keep the workgroups within one
+    // round, at least 4 tiles each.
+    nsplit = (int)std::min<long>(std::max<long>(cus / units, 1), std::max(1, tiles / 4));
+  } else {
+    // Enough blocks for most CUs: split only while the workgroups fit two
+    // rounds and every split keeps at least 32 tiles (each workgroup's
+    // prologue, partials and the merge launch cost more than a round's idle
+    // CUs on short ranges).  A 512-row chunk of 32 + 8 heads over 8 KV heads
+    // at offset 3204 (160 blocks): 1 / 2 / 3 / 4 splits 158 / 180 / 141 /
+    // 165 us; at offset 0: 1 / 2 splits 42 / 67 us.
+    for (int k = 2; units * k <= 2L * cus && tiles / k >= 32; ++k) nsplit = k;
   }
   if (nsplit > kMaxSplits) nsplit = kMaxSplits;
   int rps = (rows + nsplit - 1) / nsplit;

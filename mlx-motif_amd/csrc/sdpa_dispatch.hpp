@@ -56,9 +56,9 @@ int launch_sdpa_prefill_f32(const SdpaArgs& a, int waves, int ncb, int nblocks, 
 // A GDA layer's prefill chunk from the projection outputs (RoPE, the
 // chunk's cache rows and both dual-V passes in one launch); f16 and bf16
 // instances have a kernel (head_dim 128).
-int launch_gda_prefill_proj_f16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
-int launch_gda_prefill_proj_bf16(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
-int launch_gda_prefill_proj_f32(const SdpaArgs& a, int waves, int nblocks, hipStream_t s);
+int launch_gda_prefill_proj_f16(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
+int launch_gda_prefill_proj_bf16(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
+int launch_gda_prefill_proj_f32(const SdpaArgs& a, int waves, int ncb, int nblocks, hipStream_t s);
 
 // Pointer alignment (bytes) the kernels need for head dim D.
 int sdpa_fp_align(int dtype, int D);

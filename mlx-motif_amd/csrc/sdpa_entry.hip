@@ -916,8 +916,8 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
   }
   hipStream_t s = (hipStream_t)stream;
   const int nblocks = sdpa_grid_blocks(B * k_groups, a.nchunk, pp.nsplit);
-  int rc = dtype == MOTIF_F16 ? launch_gda_prefill_proj_f16(a, pp.waves, nblocks, s)
-                              : launch_gda_prefill_proj_bf16(a, pp.waves, nblocks, s);
+  int rc = dtype == MOTIF_F16 ? launch_gda_prefill_proj_f16(a, pp.waves, pp.ncb, nblocks, s)
+                              : launch_gda_prefill_proj_bf16(a, pp.waves, pp.ncb, nblocks, s);
   if (rc != MOTIF_OK || pp.nsplit == 1) return rc;
   // One merge over both passes' partial rows (noise rows into y_noise).
   SdpaArgs m = a;

@@ -125,11 +125,11 @@ int MOTIF_CAT(launch_sdpa_prefill_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, 
 
 // Prefill chunk of a GDA layer from the projections (fp16 or bf16, head_dim
 // 128).
-int MOTIF_CAT(launch_gda_prefill_proj_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, int nblocks,
-                                                     hipStream_t s) {
+int MOTIF_CAT(launch_gda_prefill_proj_, MOTIF_SUFFIX)(const SdpaArgs& a, int waves, int ncb,
+                                                     int nblocks, hipStream_t s) {
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
                 std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    return launch_gda_prefill_proj_16<MOTIF_ELEM>(a, waves, nblocks, s);
+    return launch_gda_prefill_proj_16<MOTIF_ELEM>(a, waves, ncb, nblocks, s);
   }
   set_error("gda_prefill_proj: no variant for this element type");
   return MOTIF_ERR_UNSUPPORTED;

@@ -145,6 +145,7 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
 // then the noise pass's.
 struct GdaPrefillPlan {
   int waves;
+  int ncb;  // column blocks of 16 virtual heads per wave (1 or 2)
   int nqb_origin, nqb_noise;
   int nsplit, rows_per_split;
   size_t workspace_bytes;  // counters + partials, 0 when nsplit == 1

@@ -550,7 +550,8 @@ __device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float l
   rope_words_inv<T>(lo, hi, inv, pos);
 }
 
-template <typename T, int NW, int NS = kPrefillStages>
+// NCB: column blocks of 16 virtual heads per wave, as in sdpa_prefill_kernel.
+template <typename T, int NW, int NS = kPrefillStages, int NCB = 1>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 2 : 1)))
 gda_prefill_proj_kernel(SdpaArgs a) {
   using Op = MfmaOp<T>;
@@ -573,22 +574,37 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   const int GV = G * S;
   const int b = unit / a.Hkv;
   const int kvh = unit % a.Hkv;
-  const int wg_vh0 = qb * NW * 16;
-  const int vh = wg_vh0 + wave * 16 + col;  // virtual head (pass head vh / S, query row vh % S)
-  const bool col_ok = vh < GV;
-  const int lim = col_ok ? vhead_limit(a, vh) : 0;
-  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16, GV - wg_vh0));
+  const int wg_vh0 = qb * NW * 16 * NCB;
+  int vh[NCB], lim[NCB];  // virtual heads (pass head vh / S, query row vh % S)
+  bool col_ok[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    vh[cb] = wg_vh0 + (wave * NCB + cb) * 16 + col;
+    col_ok[cb] = vh[cb] < GV;
+    lim[cb] = col_ok[cb] ? vhead_limit(a, vh[cb]) : 0;
+  }
+  const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16 * NCB, GV - wg_vh0));
 
+  // The KV head's tiles: T_OLD over cache rows [0, row0) (the last one may
+  // stop short of 32 rows), then T_NEW over the chunk's rows [row0, kv_len)
+  // from the projections, tile n at row0 + 32 n.  They are dealt to the
+  // splits round robin (global tile g to split g % nsplit), so every split
+  // gets its share of the old rows, of the chunk tiles to rope and of the
+  // rows the causal limit cuts off.  Tiles starting at or past max_lim are
+  // not visited.
   const int row0 = a.kv_len - S;  // the chunk's first cache row
-  const int split_begin = split * a.rows_per_split;
-  const int split_end = min(split_begin + a.rows_per_split, a.kv_len);
-  const int r_end = min(split_end, max_lim);
-  const int old_end = min(r_end, row0);
-  const int n_old = max(old_end - split_begin, 0);
-  const int new_begin = max(split_begin, row0);
-  const int n_new = max(r_end - new_begin, 0);
-  const int t_old = (n_old + TR - 1) / TR;
-  const int ntiles = t_old + (n_new + TR - 1) / TR;
+  const int ns = a.nsplit;
+  const int T_OLD = (row0 + TR - 1) / TR;
+  const int T_NEW = (S + TR - 1) / TR;
+  const int n_vis = max_lim <= row0 ? (max_lim + TR - 1) / TR
+                                    : T_OLD + (max_lim - row0 + TR - 1) / TR;
+  const int ntiles = n_vis > split ? (n_vis - split + ns - 1) / ns : 0;
+  auto gtile = [&](int i) { return split + i * ns; };
+  auto is_new_tile = [&](int i) { return gtile(i) >= T_OLD; };
+  auto first_row = [&](int i) {
+    const int g = gtile(i);
+    return g >= T_OLD ? row0 + (g - T_OLD) * TR : g * TR;
+  };
 
   const int HK = 2 * a.Hkv;  // heads of k_proj and of v_proj
   const long pstride = (long)HK * D;
@@ -598,16 +614,22 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   const long crow0 = (long)unit * a.kv_cap;       // cache row 0 of this KV head
 
   // ---- this block's share of the chunk's cache rows (written, not read) ----
+  // The split's chunk tiles n = n_first, n_first + ns, ..; local row lr of
+  // them is chunk row 32 (n_first + (lr / 32) ns) + lr % 32.  The split's
+  // origin blocks share k1, v1, v2 of those rows, its noise blocks k2.
   {
-    const int wb = max(split_begin, row0);
-    const int nrows = max(split_end - wb, 0);
+    const int n_first = ((split - T_OLD) % ns + ns) % ns;
+    const int nnew = T_NEW > n_first ? (T_NEW - n_first + ns - 1) / ns : 0;
+    const int nrows = nnew * TR;
     const int per = (nrows + nqb - 1) / nqb;
-    const int r_lo = wb + qb * per;
-    const int r_hi = min(r_lo + per, wb + nrows);
+    const int r_lo = qb * per;
+    const int r_hi = min(r_lo + per, nrows);
+    auto chunk_row = [&](int lr) { return row0 + (n_first + (lr / TR) * ns) * TR + lr % TR; };
     const int hk = 2 * kvh + (noise ? 1 : 0);
     // K: one (row, chunk pair, half) item per thread: 4 pairs (c, c + 64).
-    for (int it = threadIdx.x; it < (r_hi - r_lo) * 16; it += NT) {
-      const int r = r_lo + (it >> 4);
+    for (int it = threadIdx.x; it < max(r_hi - r_lo, 0) * 16; it += NT) {
+      const int r = chunk_row(r_lo + (it >> 4));
+      if (r >= a.kv_len) continue;
       const int cp = (it >> 1) & 7;
       const int p0 = 8 * cp + 4 * (it & 1);
       const long src = ((long)b * S + (r - row0)) * pstride + (long)hk * D;
@@ -618,8 +640,9 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       *reinterpret_cast<uint2*>(kc + (crow0 + r) * D + 64 + p0) = hi;
     }
     if (!noise) {  // V1 and V2: 16-byte copies
-      for (int it = threadIdx.x; it < (r_hi - r_lo) * 32; it += NT) {
-        const int r = r_lo + (it >> 5);
+      for (int it = threadIdx.x; it < max(r_hi - r_lo, 0) * 32; it += NT) {
+        const int r = chunk_row(r_lo + (it >> 5));
+        if (r >= a.kv_len) continue;
         const int t = (it >> 4) & 1;
         const int c = it & 15;
         const long src = ((long)b * S + (r - row0)) * pstride + (long)(2 * kvh + t) * D + 8 * c;
@@ -630,10 +653,11 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   }
 
   // ---- Q^T from q_proj, roped: lane (col, blk) holds channels 32*s + 8*blk .. +7 ----
-  V8 qbv[4];
-  {
-    const int hp = kvh * G + (col_ok ? vh / S : 0);  // head within the pass
-    const int srow = col_ok ? vh % S : 0;
+  V8 qbv[NCB][4];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int hp = kvh * G + (col_ok[cb] ? vh[cb] / S : 0);  // head within the pass
+    const int srow = col_ok[cb] ? vh[cb] % S : 0;
     const int HQ = a.q_groups * (a.q_gr + 1);
     int qh;
     if (!noise)
@@ -644,7 +668,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     uint4 w[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      w[s] = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
+      w[s] = col_ok[cb] ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
     const int pos = a.rope_pos0 + srow;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
@@ -656,24 +680,26 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       w[s + 2] = make_uint4(h0.x, h0.y, h1.x, h1.y);
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qbv[s] = __builtin_bit_cast(V8, w[s]);
-    // q and this block's cache stores are waited for here, before the first
-    // tile copies are issued (vmcnt also counts stores; the tile waits below
-    // count only the copies).
-    asm volatile("s_waitcnt vmcnt(0)" ::"v"(qbv[0]), "v"(qbv[1]), "v"(qbv[2]), "v"(qbv[3])
-                 : "memory");
+    for (int s = 0; s < 4; ++s) qbv[cb][s] = __builtin_bit_cast(V8, w[s]);
   }
+  // q and this block's cache stores are waited for here, before the first
+  // tile copies are issued (vmcnt also counts stores; the tile waits below
+  // count only the copies).
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb)
+    asm volatile("s_waitcnt vmcnt(0)" ::"v"(qbv[cb][0]), "v"(qbv[cb][1]), "v"(qbv[cb][2]),
+                 "v"(qbv[cb][3])
+                 : "memory");
 
-  // Rows [split_begin, old_end) from the cache, [new_begin, r_end) from the
-  // projections, through range-checked resources (past the range: zeros).
-  const long hrow0 = crow0 + split_begin;
-  const unsigned obytes = (unsigned)(n_old * D * 2);
+  // Rows [0, row0) from the cache, the chunk's rows from the projections,
+  // through range-checked resources (past the range: zeros).
+  const unsigned obytes = (unsigned)(row0 * D * 2);
   const __amdgpu_buffer_rsrc_t r_old[3] = {
-      uniform_stream_rsrc(kc + hrow0 * D, obytes),
-      uniform_stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, obytes),
-      uniform_stream_rsrc((const uint16_t*)a.v2 + hrow0 * D, obytes)};
-  const long prow0 = ((long)b * S + (new_begin - row0)) * pstride;
-  const unsigned nbytes = n_new > 0 ? (unsigned)(((long)(n_new - 1) * pstride + D) * 2) : 0u;
+      uniform_stream_rsrc(kc + crow0 * D, obytes),
+      uniform_stream_rsrc((const uint16_t*)a.v1 + crow0 * D, obytes),
+      uniform_stream_rsrc((const uint16_t*)a.v2 + crow0 * D, obytes)};
+  const long prow0 = (long)b * S * pstride;
+  const unsigned nbytes = S > 0 ? (unsigned)(((long)(S - 1) * pstride + D) * 2) : 0u;
   const __amdgpu_buffer_rsrc_t r_new[3] = {
       uniform_stream_rsrc(kproj + prow0 + (long)(2 * kvh + (noise ? 1 : 0)) * D, nbytes),
       uniform_stream_rsrc(vproj + prow0 + (long)(2 * kvh) * D, nbytes),
@@ -686,8 +712,8 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   static_assert((NS - 1) * CPW <= 63, "vmcnt counts at most 63");
   static_assert(NW == 4 || NW == 8, "copies are dealt over 4 or 8 waves");
   auto issue = [&](int st, int tile) {
-    const bool is_new = tile >= t_old;  // wave-uniform
-    const int tr = is_new ? tile - t_old : tile;
+    const bool is_new = is_new_tile(tile);  // wave-uniform
+    const int tr = is_new ? gtile(tile) - T_OLD : gtile(tile);
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
       const int t = c * NW / 8;
@@ -730,8 +756,9 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     }
   };
 
-  SwizzledTileAcc<T> st_acc;
-  st_acc.init();
+  SwizzledTileAcc<T> st_acc[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) st_acc[cb].init();
   // Pipelined as sdpa_prefill_kernel: barrier i publishes tile i (a chunk
   // tile's K rows roped first by the waves that copied them); the scores of
   // tile i + 1 are issued before the softmax and PV products of tile i.
@@ -743,14 +770,11 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       ++inflight;
     }
   }
-  auto first_row = [&](int i) {
-    return i >= t_old ? new_begin + (i - t_old) * TR : split_begin + i * TR;
-  };
   auto publish = [&](int i) {
     prefill_wait_vm_groups<CPW, NS - 2>(inflight - 1);  // this wave's copies of tile i landed
-    if (i >= t_old) {  // rope the K rows this wave copied, before the waves meet
+    if (is_new_tile(i)) {  // rope the K rows this wave copied, before the waves meet
       const int first = first_row(i);
-      rope_own_rows(i % NS, first, min(TR, r_end - first));
+      rope_own_rows(i % NS, first, min(TR, max_lim - first));
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     asm volatile("s_barrier" ::: "memory");  // every wave's copies (and ropes) landed
@@ -761,34 +785,55 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       ++inflight;
     }
   };
-  floatx4 s_cur[2], s_nxt[2];
-  if (ntiles > 0) {
-    publish(0);
-    SwizzledTileAcc<T>::scores(ring[0][0], qbv, s_cur, col, blk);
-  }
-  for (int i = 0; i < ntiles; ++i) {
-    if (i + 1 < ntiles) {
-      publish(i + 1);
-      SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qbv, s_nxt, col, blk);
+  if constexpr (NCB == 1) {
+    floatx4 s_cur[2], s_nxt[2];
+    if (ntiles > 0) {
+      publish(0);
+      SwizzledTileAcc<T>::scores(ring[0][0], qbv[0], s_cur, col, blk);
     }
-    st_acc.update(s_cur, ring[i % NS][1], ring[i % NS][2], first_row(i),
-                  i >= t_old ? r_end : old_end, lim, a.qscale, col, blk);
-    s_cur[0] = s_nxt[0];
-    s_cur[1] = s_nxt[1];
+    for (int i = 0; i < ntiles; ++i) {
+      if (i + 1 < ntiles) {
+        publish(i + 1);
+        SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qbv[0], s_nxt, col, blk);
+      }
+      st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], first_row(i),
+                       is_new_tile(i) ? max_lim : min(row0, max_lim), lim[0], a.qscale, col, blk);
+      s_cur[0] = s_nxt[0];
+      s_cur[1] = s_nxt[1];
+    }
+  } else {
+    for (int i = 0; i < ntiles; ++i) {  // one tile per barrier
+      publish(i);
+      floatx4 sacc[NCB][2];
+      tile_scores_n<T, NCB>(ring[i % NS][0], qbv, sacc, col, blk);
+      V8 pb[NCB];
+      const int rl = is_new_tile(i) ? max_lim : min(row0, max_lim);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb)
+        pb[cb] = st_acc[cb].softmax(sacc[cb], first_row(i), rl, lim[cb], a.qscale, blk);
+      tile_pv_n<T, NCB>(st_acc, pb, ring[i % NS][1], ring[i % NS][2], col, blk);
+    }
   }
 
-  if (!col_ok) return;
   // Output rows: origin (b, head, s) of y, noise (b, head, s) of y2; split
   // partials in one row space, the noise rows after y2_row0.
   const int Hp = a.Hkv * G;
-  const long yrow = ((long)b * Hp + (long)kvh * G) * S + vh;
-  st_acc.store_to(noise ? a.y2 : a.y, yrow, a.part_o, a.part_ml, (noise ? a.y2_row0 : 0) + yrow,
-                  a.nsplit, split, blk);
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    if (!col_ok[cb]) continue;
+    const long yrow = ((long)b * Hp + (long)kvh * G) * S + vh[cb];
+    st_acc[cb].store_to(noise ? a.y2 : a.y, yrow, a.part_o, a.part_ml,
+                        (noise ? a.y2_row0 : 0) + yrow, a.nsplit, split, blk);
+  }
 }
 
 template <typename T>
-inline int launch_gda_prefill_proj_16(const SdpaArgs& a, int waves, int nblocks, hipStream_t st) {
-  if (waves == 8) {
+inline int launch_gda_prefill_proj_16(const SdpaArgs& a, int waves, int ncb, int nblocks,
+                                      hipStream_t st) {
+  if (waves == 8 && ncb == 2) {
+    hipLaunchKernelGGL((gda_prefill_proj_kernel<T, 8, kPrefillStages, 2>), dim3(nblocks),
+                       dim3(512), 0, st, a);
+  } else if (waves == 8) {
     hipLaunchKernelGGL((gda_prefill_proj_kernel<T, 8>), dim3(nblocks), dim3(512), 0, st, a);
   } else {
     hipLaunchKernelGGL((gda_prefill_proj_kernel<T, 4>), dim3(nblocks), dim3(256), 0, st, a);

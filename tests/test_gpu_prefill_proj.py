@@ -152,3 +152,22 @@ def test_prefill_four_and_eight_wave_blocks(gpu, rng):
             _check(gpu, rng, 1, 160, 8, 4, 8, 300, 512)
         finally:
             _native.set_tuning("waves_per_wg", 0)
+
+
+@pytest.mark.parametrize("ncb", [1, 2])
+@pytest.mark.parametrize("S,offset,cap,rps,tag", [
+    (160, 300, 512, 0, "f16"),      # 640 origin heads per KV head: one ragged 256-head block
+    (130, 70, 256, 64, "f16"),      # many splits, tiles dealt round robin, the chunk's tiles among them
+    (200, 1000, 1280, 0, "bf16"),
+])
+def test_prefill_column_blocks_per_wave(gpu, rng, ncb, S, offset, cap, rps, tag):
+    """8-wave blocks with one or two 16-head column blocks per wave."""
+    from mlx_motif import _native
+
+    _native.set_tuning("prefill_ncb", ncb)
+    _native.set_tuning("rows_per_split", rps)
+    try:
+        _check(gpu, rng, 1, S, 8, 4, 8, offset, cap, tag=tag)
+    finally:
+        _native.set_tuning("prefill_ncb", 0)
+        _native.set_tuning("rows_per_split", 0)
