@@ -495,16 +495,16 @@ inline int launch_prefill_kernel_16(const SdpaArgs& a, int waves, int ncb, int n
 // over V1/V2.  What differs from sdpa_prefill_kernel:
 //   - q is read from q_proj and roped in registers: channel c of k-step s
 //     (s < 2) pairs with channel c + 64 of k-step s + 2 in the same lane;
-//   - a split's rows before the chunk (kv_len - S_q) come from the cache,
-//     its rows of the chunk from k_proj / v_proj, as separate tile runs (the
-//     chunk's tiles start at its first row); each wave ropes in place the
-//     K rows of a chunk tile it copied, once its own copies have landed and
-//     before the tile's barrier;
-//   - before its tile loop each block writes its share of the chunk's rows
-//     into the cache (roped k1 / k2, v1, v2): the origin blocks of a (b, KV
-//     head, split) share the split's k1, v1 and v2 rows, the noise blocks its
-//     k2 rows.  No block reads those cache rows (every block takes the chunk
-//     from the projections), so no block waits for another.
+//   - the rows before the chunk (kv_len - S_q) come from the cache in
+//     32-row tiles, the chunk's rows from k_proj / v_proj in 32-row tiles
+//     from its first row; the tiles are dealt to the row splits round robin;
+//     each wave ropes in place the K rows of a chunk tile it copied, once
+//     its own copies have landed and before the tile's barrier;
+//   - before its tile loop each block writes its share of its split's chunk
+//     rows into the cache (roped k1 / k2, v1, v2): the origin blocks of a
+//     (b, KV head, split) share the split's k1, v1 and v2 rows, the noise
+//     blocks its k2 rows.  No block reads those cache rows (every block
+//     takes the chunk from the projections), so no block waits for another.
 // RoPE is rope_impl.hpp's, rounded once to T, so q, the cache rows and the
 // K tiles carry the values motif_rope_split4 produces.
 
