@@ -97,3 +97,36 @@ def test_rope_split4_plain_outputs_equal_cache_writes(gpu, rng):
     for a, b in zip(plain, ref):
         diff = np.abs(torch_to_np(a) - torch_to_np(b))
         assert float((diff - 2 * _ulp(torch_to_np(b), "f16") - 1e-6).max()) <= 0
+
+
+@pytest.mark.parametrize("tag", ["f16", "bf16"])
+def test_rope_split4_unaligned_rows_take_the_scalar_path(gpu, rng, tag):
+    """Inputs 2 bytes off an 8-byte boundary (a view at element offset 1)
+    take the element-wise path; its outputs and cache rows are bit-identical
+    to the 8-byte vector path's on the same values."""
+    import torch
+
+    from mlx_motif.kernels import rope_split4
+
+    dt = torch_dtype(tag)
+    B, S, qg, gr, kg, D, offset, cap = 1, 6, 8, 4, 8, 128, 40, 64
+    shapes = [(B, S, qg * (gr + 1) * D), (B, S, 2 * kg * D), (B, S, 2 * kg * D)]
+    arrays = [np_to_torch(randn(rng, sh, tag), dt, gpu) for sh in shapes]
+
+    def unaligned(t):
+        buf = torch.empty(t.numel() + 1, dtype=dt, device=gpu)
+        u = buf[1:].view(t.shape)
+        u.copy_(t)
+        assert u.data_ptr() % 8 == 2 and u.is_contiguous()
+        return u
+
+    outs = []
+    for make in (lambda t: t, unaligned):
+        caches = [torch.full((B, kg, cap, D), 3.0, dtype=dt, device=gpu) for _ in range(4)]
+        print(f"rope_split4 {tag} {'unaligned' if make is unaligned else 'aligned'}", flush=True)
+        res = rope_split4(*(make(t) for t in arrays), qg, gr, kg, 1, offset, caches=caches)
+        torch.cuda.synchronize()
+        outs.append([r.contiguous().view(torch.int16).cpu() for r in res[:2]] +
+                    [c.view(torch.int16).cpu() for c in caches])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
