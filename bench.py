@@ -642,15 +642,17 @@ def run_extra(torch, lib, dev, args):
     # prefill chunk: 512 query rows of 32 heads over a 3716-row fp16 cache
     # (bottom-right causal), the multi-row kernel with LDS-shared K/V tiles;
     # matrix-core bound, so reported as TFLOP/s of QK^T and both PV products
-    calls, keep = make_fp16_calls(torch, lib, dev, 4, kv_len=3716, cap=3840, s_q=512)
-    us = time_calls(torch, calls, steps, warm)
-    flops = 2 * HQ * 512 * 3716 * D * 3
-    log("EXTRA " + json.dumps({"workload": "prefill chunk f16 512 rows kv3716 (causal)",
-                               "us_per_call": round(us, 3),
-                               "tflops": round(flops / us / 1e6, 1),
-                               "pct_peak_f16_mfma": round(100 * flops / us / 1e6 / PEAK_F16_TFLOPS, 1)}))
-    del calls, keep
-    torch.cuda.empty_cache()
+    # (and a 2048-row chunk over 4228 rows: blocks of 256 heads, no row split)
+    for s_q, kvl, cap in ((512, 3716, 3840), (2048, 4228, 4352)):
+        calls, keep = make_fp16_calls(torch, lib, dev, 4, kv_len=kvl, cap=cap, s_q=s_q)
+        us = time_calls(torch, calls, steps if s_q == 512 else max(steps // 4, 1), warm)
+        flops = 2 * HQ * s_q * kvl * D * 3
+        log("EXTRA " + json.dumps({
+            "workload": f"prefill chunk f16 {s_q} rows kv{kvl} (causal)",
+            "us_per_call": round(us, 3), "tflops": round(flops / us / 1e6, 1),
+            "pct_peak_f16_mfma": round(100 * flops / us / 1e6 / PEAK_F16_TFLOPS, 1)}))
+        del calls, keep
+        torch.cuda.empty_cache()
     # a 12.7B layer's prefill chunk from the projections: 512 rows at offset
     # 3204 (and a first chunk at offset 0), RoPE + cache write + origin
     # (32 heads) and noise (8 heads) passes in one launch, against
