@@ -262,6 +262,45 @@ struct SwizzledTileAcc {
   }
 };
 
+// Split partials of a wave's 16 columns staged through LDS: lane (col, blk)
+// holds channels 32*blk + 4*j .. +3 of its column, so direct stores write
+// 16-byte pieces of 16 rows per instruction; staged, each store instruction
+// writes two whole 512-byte halves of partial rows.  lds: this wave's 16
+// rows of 132 floats (16 bytes of padding per row put the 16 columns' writes
+// in distinct bank groups).  Column c's partial row is prow0 + c, stored for
+// c < ncols.
+constexpr int kStageRowFloats = 132;
+constexpr int kStageWaveBytes = 16 * kStageRowFloats * 4;
+template <typename T>
+__device__ __forceinline__ void store_partials_staged(const SwizzledTileAcc<T>& acc, float* lds,
+                                                      float* part_o, float* part_ml, long prow0,
+                                                      int ncols, int nsplit, int split, int col,
+                                                      int blk) {
+  constexpr int D = 128;
+  const int lane = col + 16 * blk;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const floatx4* src = half ? acc.acc2 : acc.acc1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<float4*>(lds + col * kStageRowFloats + 32 * blk + 4 * j) =
+          make_float4(src[j][0], src[j][1], src[j][2], src[j][3]);
+    // (a wave's LDS accesses complete in order: the reads below see these writes)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = 2 * i + (lane >> 5);
+      const int q = lane & 31;
+      const float4 v = *reinterpret_cast<const float4*>(lds + row * kStageRowFloats + 4 * q);
+      if (row < ncols)
+        *reinterpret_cast<float4*>(part_o + ((prow0 + row) * nsplit + split) * 2 * D + half * D +
+                                   4 * q) = v;
+    }
+  }
+  if (blk == 0 && col < ncols)
+    *reinterpret_cast<float2*>(part_ml + ((prow0 + col) * nsplit + split) * 2) =
+        make_float2(acc.m_run, acc.accl[0]);
+}
+
 // S^T = K Q^T of a tile for NCB column blocks (16 columns each) of one
 // wave: each K fragment is read from LDS once and used by every block.
 template <typename T, int NCB>
@@ -467,6 +506,19 @@ sdpa_prefill_kernel(SdpaArgs a) {
   }
 
   // acc[j][r] of lane (col, blk) is channel 32*blk + 4*j + r of column col.
+  if (a.nsplit > 1) {
+    // Partials through the ring, once every wave is done with it.
+    static_assert(NW * kStageWaveBytes <= (int)sizeof(ring), "staging fits the ring");
+    __syncthreads();
+    float* lds = reinterpret_cast<float*>(&ring[0][0][0]) + wave * (kStageWaveBytes / 4);
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int c0 = vh[cb] - col;  // the block's first virtual head
+      store_partials_staged<T>(st_acc[cb], lds, a.part_o, a.part_ml, qrow0 + c0,
+                               min(16, a.GV - c0), a.nsplit, split, col, blk);
+    }
+    return;
+  }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb)
     if (col_ok[cb]) st_acc[cb].store(a, qrow0 + vh[cb], split, blk);
@@ -818,10 +870,25 @@ gda_prefill_proj_kernel(SdpaArgs a) {
   // Output rows: origin (b, head, s) of y, noise (b, head, s) of y2; split
   // partials in one row space, the noise rows after y2_row0.
   const int Hp = a.Hkv * G;
+  const long yrow0 = ((long)b * Hp + (long)kvh * G) * S;
+  if (a.nsplit > 1) {
+    // Partials through the ring, once every wave is done with it.
+    static_assert(NW * kStageWaveBytes <= (int)sizeof(ring), "staging fits the ring");
+    __syncthreads();
+    float* lds = reinterpret_cast<float*>(&ring[0][0][0]) + wave * (kStageWaveBytes / 4);
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int c0 = vh[cb] - col;
+      store_partials_staged<T>(st_acc[cb], lds, a.part_o, a.part_ml,
+                               (noise ? a.y2_row0 : 0) + yrow0 + c0, min(16, GV - c0), a.nsplit,
+                               split, col, blk);
+    }
+    return;
+  }
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     if (!col_ok[cb]) continue;
-    const long yrow = ((long)b * Hp + (long)kvh * G) * S + vh[cb];
+    const long yrow = yrow0 + vh[cb];
     st_acc[cb].store_to(noise ? a.y2 : a.y, yrow, a.part_o, a.part_ml,
                         (noise ? a.y2_row0 : 0) + yrow, a.nsplit, split, blk);
   }
