@@ -282,6 +282,18 @@ sdpa_qslab_kernel(SdpaArgs a) {
       __syncthreads();  // before the next round's writes
     }
     if (tp > 0) return;
+    if constexpr (NW * kStageWaveBytes <= (int)sizeof(ring)) {
+      // Partials (split rows only: one split writes y) through the ring,
+      // free after the merge's last barrier.
+      if (a.nsplit > 1) {
+        const int c0 = vh - col;
+        store_partials_staged<half_t>(acc, reinterpret_cast<float*>(&ring[0][0][0][0]) +
+                                               wave * (kStageWaveBytes / 4),
+                                      a.part_o, a.part_ml, qrow0 + c0, min(16, a.GV - c0),
+                                      a.nsplit, split, col, blk);
+        return;
+      }
+    }
   }
   if (!col_ok) return;
   acc.store(a, qrow0 + vh, split, blk);
@@ -528,7 +540,20 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
       __syncthreads();
     }
   }
-  if (tp > 0 || !col_ok) return;
+  if (tp > 0) return;
+  if constexpr (NP > 1 && 8 * kStageWaveBytes <= (int)sizeof(ring)) {
+    // Partials (split rows only: one split writes y) through the ring, free
+    // after the merge's last barrier.
+    if (a.nsplit > 1) {
+      const int c0 = vh - col;
+      store_partials_staged<half_t>(acc, reinterpret_cast<float*>(&ring[0][0][0][0]) +
+                                             wave * (kStageWaveBytes / 4),
+                                    a.part_o, a.part_ml, qrow0 + c0, min(16, a.GV - c0),
+                                    a.nsplit, split, col, blk);
+      return;
+    }
+  }
+  if (!col_ok) return;
   acc.store(a, qrow0 + vh, split, blk);
 }
 
