@@ -431,6 +431,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * "prefill_ncb" (column blocks of 16 virtual heads per wave of the 8-wave
  * shared-tile kernels: 0, the default, takes 2 from 2048 virtual heads per
  * KV head over at least 2048 rows, else 1; 1 or 2 forces it),
+ * "prefill_min_heads" (0, the default: multi-row fp16/bf16 calls take the
+ * shared-tile kernel from 64 virtual heads per KV head, or from 17 over 2048
+ * or more rows; n > 0: from n heads),
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
  * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.

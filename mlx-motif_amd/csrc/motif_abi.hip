@@ -136,6 +136,12 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
   return p;
 }
 
+bool use_shared_tiles(int GV, int kv_len) {
+  const int t = tuning().prefill_min_heads;
+  if (t > 0) return GV >= t;
+  return GV >= kPrefillMinHeads || (GV > 16 && kv_len >= 2048);
+}
+
 PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   PrefillPlan p{};
   const int G = Hkv > 0 ? Hq / Hkv : 1;
@@ -295,7 +301,7 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
                                    nb > 1 ? nb * sdpa_gc_max_q(D, gs) : 0);
       if (p.workspace_bytes > ws) ws = p.workspace_bytes;
     }
-    if ((Hq / Hkv) * S_q >= kPrefillMinHeads) {
+    if (use_shared_tiles((Hq / Hkv) * S_q, kv_len)) {
       const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
       if (pp.workspace_bytes > ws) ws = pp.workspace_bytes;
     }
@@ -364,6 +370,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.merge_rows = value; });
+  } else if (!strcmp(key, "prefill_min_heads")) {
+    if (value < 0) {
+      set_error("motif_set_tuning: prefill_min_heads must be >= 0");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.prefill_min_heads = value; });
   } else if (!strcmp(key, "prefill_ncb")) {
     if (value < 0 || value > 2) {
       set_error("motif_set_tuning: prefill_ncb must be 0, 1 or 2");

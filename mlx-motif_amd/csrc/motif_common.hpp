@@ -43,6 +43,7 @@ struct Tuning {
   int qslab_ws = 1;        // slab kernel with producer / consumer waves (8 waves): 1 on, 0 off
   int merge_rows = 1;      // row-per-wave merge launch from 2048 partial rows: 1 on, 0 off
   int prefill_ncb = 0;     // column blocks per wave of the 8-wave prefill kernel (0 = automatic)
+  int prefill_min_heads = 0;  // virtual heads per KV head from which multi-row fp16/bf16 calls take the shared-tile kernel (0: automatic)
 };
 // The calling thread's snapshot of the process-wide knobs.  Inside a
 // CallScope it is the copy taken when the outermost scope opened, so every

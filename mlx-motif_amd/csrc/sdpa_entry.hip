@@ -111,7 +111,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // the kernel with LDS-shared K/V tiles reads the cache once per block of
   // up to 128 heads instead of once per 8.
   if ((dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
-      a.GV >= kPrefillMinHeads &&
+      use_shared_tiles(a.GV, kv_len) &&
       aligned(q, 16) && aligned(y, 16) && aligned(k, 16) && aligned(v1, 16) &&
       aligned(v2, 16)) {
     const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);

@@ -126,6 +126,14 @@ SdpaPlan plan_sdpa(int B, int Hq, int Hkv, int S_q, int kv_len, int D, int gc_ma
 // workgroups only when the query blocks do not fill the GPU.  Used when a KV
 // head has at least kPrefillMinHeads virtual heads.
 constexpr int kPrefillMinHeads = 64;
+// Whether a multi-row fp16/bf16 call of GV virtual heads per KV head over
+// kv_len rows takes the shared-tile kernel: from kPrefillMinHeads heads (or
+// the "prefill_min_heads" tuning), and from 17 heads (two decode head
+// chunks, each reading the cache) over 2048+ rows.  Measured, 32 q-heads
+// over 8 KV heads, decode chunks / shared tiles: 5 rows over 1024 9.6 /
+// 10.2 us, over 3204 17.6 / 12.3, over 16000 34.5 / 26.3, over 32768 59.2 /
+// 45.5; 8 rows over 16000 38.3 / 28.2.
+bool use_shared_tiles(int GV, int kv_len);
 constexpr int kPrefillTileRowsHost = 32;  // KV rows per tile (kPrefillTileRows)
 struct PrefillPlan {
   int waves;  // 4 or 8
