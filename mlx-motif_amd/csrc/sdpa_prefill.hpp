@@ -136,17 +136,19 @@ struct SwizzledTileAcc {
   // running maximum moved past the lazy-rescale slack.  Rows row0 + 16*h +
   // 4*blk + r of the tile hold k index 8*blk + 4*h + r of the PV products (as
   // in the decode kernel); rows at or past r_end or lim are masked.
+  // Masked rows score -inf, so their weight exp2(-inf - m) is 0 with no
+  // select (m_run starts at the finite sentinel and only grows).
   __device__ __forceinline__ V8 softmax(const floatx4 (&sacc)[2], int row0, int r_end, int lim,
                                         float qscale, int blk) {
     float sc[8];
     float mx = kNegSentinel;
+    // row 16*h + 4*blk + r of the tile is visible while 16*h + r < vis
+    const int vis = min(r_end, lim) - row0 - 4 * blk;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = row0 + 16 * h + 4 * blk + r;
-        const bool ok = row < r_end && row < lim;
-        sc[4 * h + r] = ok ? sacc[h][r] * qscale : kNegSentinel;
+        sc[4 * h + r] = 16 * h + r < vis ? sacc[h][r] * qscale : -__builtin_inff();
         mx = fmaxf(mx, sc[4 * h + r]);
       }
     }
@@ -164,8 +166,7 @@ struct SwizzledTileAcc {
     }
     V8 pb;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+    for (int j = 0; j < 8; ++j) pb[j] = Op::from_f32(fast_exp2(sc[j] - m_run));
     return pb;
   }
 
