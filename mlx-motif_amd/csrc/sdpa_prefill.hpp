@@ -137,22 +137,25 @@ struct SwizzledTileAcc {
   // 4*blk + r of the tile hold k index 8*blk + 4*h + r of the PV products (as
   // in the decode kernel); rows at or past r_end or lim are masked.
   // Masked rows score -inf, so their weight exp2(-inf - m) is 0 with no
-  // select (m_run starts at the finite sentinel and only grows).
+  // select (m_run starts at the finite sentinel and only grows).  The
+  // maximum is taken over the unscaled scores (qscale > 0, so scaling it
+  // gives the maximum of the scaled ones bit for bit) and each weight is
+  // exp2(fma(s, qscale, -m)).
   __device__ __forceinline__ V8 softmax(const floatx4 (&sacc)[2], int row0, int r_end, int lim,
                                         float qscale, int blk) {
     float sc[8];
-    float mx = kNegSentinel;
+    float mx = -__builtin_inff();
     // row 16*h + 4*blk + r of the tile is visible while 16*h + r < vis
     const int vis = min(r_end, lim) - row0 - 4 * blk;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[4 * h + r] = 16 * h + r < vis ? sacc[h][r] * qscale : -__builtin_inff();
+        sc[4 * h + r] = 16 * h + r < vis ? sacc[h][r] : -__builtin_inff();
         mx = fmaxf(mx, sc[4 * h + r]);
       }
     }
-    mx = rows4_max(mx);
+    mx = fmaxf(rows4_max(mx) * qscale, kNegSentinel);
     if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float fac = fast_exp2(m_run - m_new);
@@ -166,7 +169,7 @@ struct SwizzledTileAcc {
     }
     V8 pb;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) pb[j] = Op::from_f32(fast_exp2(sc[j] - m_run));
+    for (int j = 0; j < 8; ++j) pb[j] = Op::from_f32(fast_exp2(fmaf(sc[j], qscale, -m_run)));
     return pb;
   }
 
