@@ -114,6 +114,11 @@ def test_workspace_sizing_and_tuning():
         with pytest.raises(_native.MotifNativeError):
             _native.set_tuning("prefill_ncb", bad)
     _native.set_tuning("prefill_ncb", 0)
+    with pytest.raises(_native.MotifNativeError):
+        _native.set_tuning("prefill_min_heads", -1)
+    # the shared-tile kernel's workspace is covered from 17 heads over 2048+ rows
+    lib = _native.lib()
+    assert lib.motif_sdpa_workspace_bytes(1, 32, 8, 5, 32768, 128) > 0
     _native.set_tuning("rows_per_split", 64)
     forced = lib.motif_sdpa_workspace_bytes(1, 32, 8, 1, 16000, 128)
     _native.set_tuning("rows_per_split", 0)

@@ -40,24 +40,34 @@ def test_rows_fp16(gpu, rng, B, Hq, Hkv, S, cap, kv_len, d, causal):
     assert np.max(np.abs(torch_to_np(y) - ref)) <= 2e-3
 
 
-@pytest.mark.parametrize("tag,S,Hq,cap,kv_len", [
-    ("f16", 4, 32, 1024, 1000),    # 16 virtual heads per KV head: one 16-column chunk
-    ("f16", 5, 32, 32768, 32768),  # the 5-row verify slab at 32k rows: chunks of 16 + 4
-    ("bf16", 5, 32, 512, 300),     # bf16 matrix cores, 16 + 4
-    ("bf16", 3, 40, 640, 600),     # GQA 5 x 3 rows = 15 columns
+@pytest.mark.parametrize("tag,S,Hq,cap,kv_len,min_heads", [
+    ("f16", 4, 32, 1024, 1000, 0),      # 16 virtual heads per KV head: one 16-column chunk
+    ("f16", 5, 32, 32768, 32768, 64),   # the 5-row verify slab at 32k rows: chunks of 16 + 4
+    ("f16", 5, 32, 32768, 32768, 0),    # the same on the shared-tile kernel (the default)
+    ("bf16", 5, 32, 512, 300, 0),       # bf16 matrix cores, 16 + 4
+    ("bf16", 5, 32, 4096, 4001, 0),     # bf16, shared tiles (20 heads over 2048+ rows)
+    ("bf16", 3, 40, 640, 600, 0),       # GQA 5 x 3 rows = 15 columns
 ])
-def test_rows_sixteen_column_chunks(gpu, rng, tag, S, Hq, cap, kv_len):
-    """fp16/bf16 slabs at head_dim 128 run the matrix-core kernel with up to
-    16 virtual heads per workgroup."""
+def test_rows_sixteen_column_chunks(gpu, rng, tag, S, Hq, cap, kv_len, min_heads):
+    """fp16/bf16 slabs at head_dim 128: the matrix-core decode kernel with up
+    to 16 virtual heads per workgroup, or, from 17 heads over 2048+ rows,
+    the shared-tile kernel (min_heads 64 keeps the decode kernel)."""
+    from mlx_motif import _native
     from mlx_motif.kernels import sdpa_dual_v_rows
 
     q = randn(rng, (1, Hq, S, 128), tag)
     k, v1, v2 = (randn(rng, (1, 8, cap, 128), tag) for _ in range(3))
     T = lambda a: np_to_torch(a, torch_dtype(tag), gpu)  # noqa: E731
-    print(f"rows {tag} S={S} Hq={Hq} kv_len={kv_len}", flush=True)
-    y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=kv_len, causal=True)
+    print(f"rows {tag} S={S} Hq={Hq} kv_len={kv_len} min_heads={min_heads}", flush=True)
+    _native.set_tuning("prefill_min_heads", min_heads)
+    try:
+        y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=kv_len,
+                             causal=True)
+        torch_y = torch_to_np(y)
+    finally:
+        _native.set_tuning("prefill_min_heads", 0)
     ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128), kv_len, causal=True)
-    err = float(np.max(np.abs(torch_to_np(y) - ref)))
+    err = float(np.max(np.abs(torch_y - ref)))
     assert err <= (2e-3 if tag == "f16" else 1e-2), f"{tag} S={S}: {err:.3e}"
 
 
