@@ -391,6 +391,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other rows' shapes (decode step, verify slabs, prefill chunks)")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches")
     ap.add_argument("--extra", action="store_true", help="also time the other workloads")
     ap.add_argument("--valu", action="store_true",
@@ -442,6 +444,7 @@ def main() -> int:
 
     if args.extra:
         run_extra(torch, lib, dev, args)
+    sec = None if args.no_secondary else secondary(torch, lib, dev)
 
     f16 = res["f16"]
     basis = ("algorithmic bytes / us per call; a call is the attention launch plus the "
@@ -474,6 +477,7 @@ def main() -> int:
         "q8": dict(res["q8"], roofline=roofline("q8", res["q8"], basis)),
         "roofline": roofline("f16", f16, basis),
         "sources_digest": sources_digest(),
+        "secondary": sec,
         "cpu_baseline": None if args.no_cpu_baseline else cpu_baseline(),
     }
     print(json.dumps(out), flush=True)
@@ -578,6 +582,63 @@ def summarize_traffic(kind: str, fetch_dir: str, write_dir: str) -> int:
     dst.write_text(json.dumps(out, indent=1) + "\n")
     log(f"{dst.name}: {rd + wr} B per call, {out['traffic_over_algorithmic']}x algorithmic")
     return 0
+
+
+def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
+    """The other rows' headline shapes, timed as the decode calls are (graph
+    replay, HIP events): the fused GDA decode step at 16k, the 5-row verify
+    slabs over 32768 rows (fp16 and q8), the 512-row prefill chunk over 3716
+    rows and a 12.7B layer's 512-row chunk at offset 3204 from the
+    projections (RoPE + 4-slot write + both passes in one launch)."""
+    from mlx_motif.kernels import gda_prefill_attention_from_proj
+
+    out = {}
+
+    def hbm(name, us, nbytes):
+        gbps = nbytes / us / 1e3
+        out[name] = {"us_per_call": round(us, 3), "gbps": round(gbps, 1),
+                     "pct_peak_hbm": round(100 * gbps / PEAK_HBM_GBPS, 1)}
+
+    def mfma(name, us, flops):
+        tf = flops / us / 1e6
+        out[name] = {"us_per_call": round(us, 3), "tflops": round(tf, 1),
+                     "pct_peak_f16_mfma": round(100 * tf / PEAK_F16_TFLOPS, 1)}
+
+    calls, keep = make_decode_calls(torch, lib, dev, 6, fused=True)
+    hbm("gda_decode_step_f16_kv16000", time_calls(torch, calls, steps, warm),
+        decode_bytes(KV_LEN, True))
+    del calls, keep
+    calls, keep = make_fp16_calls(torch, lib, dev, 6, kv_len=32768, cap=32768, s_q=5)
+    hbm("verify_slab_f16_5x32768", time_calls(torch, calls, steps, warm),
+        alg_bytes("f16", 32768, s_q=5))
+    del calls, keep
+    torch.cuda.empty_cache()
+    calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
+    hbm("verify_slab_q8_5x32768", time_calls(torch, calls, steps, warm),
+        alg_bytes("q8", 32768, s_q=5))
+    del calls, keep
+    torch.cuda.empty_cache()
+    calls, keep = make_fp16_calls(torch, lib, dev, 4, kv_len=3716, cap=3840, s_q=512)
+    mfma("prefill_f16_512x3716_causal", time_calls(torch, calls, steps, warm),
+         2 * HQ * 512 * 3716 * D * 3)
+    del calls, keep
+    torch.cuda.empty_cache()
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    off, S = 3204, 512
+    cap = (off + S + 255) // 256 * 256
+    sets = [(torch.randn((B, S, 40 * D), generator=g, device=dev).half(),
+             torch.randn((B, S, 16 * D), generator=g, device=dev).half(),
+             torch.randn((B, S, 16 * D), generator=g, device=dev).half(),
+             [torch.randn((B, HKV, cap, D), generator=g, device=dev).half() for _ in range(4)])
+            for _ in range(4)]
+    calls = [lambda st=st: gda_prefill_attention_from_proj(st[0], st[1], st[2], st[3], off, 8, 4,
+                                                           8, D ** -0.5) for st in sets]
+    mfma("prefill_layer_chunk_f16_512_at_3204", time_calls(torch, calls, steps, warm),
+         2 * (HQ + HKV) * D * 3 * sum(off + s + 1 for s in range(S)))
+    del calls, sets
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_extra(torch, lib, dev, args):
