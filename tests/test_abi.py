@@ -197,3 +197,26 @@ def test_noalloc_refuses_calls_past_its_scratch_before_the_gpu():
     # more B*Hq rows than counters the scratch clears
     st = lib.motif_sdpa_dual_v_noalloc(1, 1, 1, 1, 1, 0, 1024, 32, 8, 128, 64, 64, 0.1, None)
     assert st == _native.MOTIF_ERR_WORKSPACE and "counters" in _err()
+
+
+def test_prefill_planner_choices_through_workspace_sizes():
+    """The prefill planners' choices, read back through the workspace sizes
+    (256 CUs without a device): a 12.7B layer's 512-row chunk at offset 3204
+    takes two column blocks per wave (8 + 2 blocks of 256 heads per KV head)
+    and 3 row splits; at offset 0 (512 rows) one block per wave and no split;
+    a 512-row multi-row call over 3716 rows 4 splits of 256-head blocks."""
+    lib = _native.lib()
+
+    def parts(vrows, ns):
+        r = lambda n: (n + 255) // 256 * 256  # noqa: E731
+        return r(vrows * 4) + r(vrows * ns * 256 * 4) + r(vrows * ns * 2 * 4)
+
+    vrows = 1 * 8 * (4 + 1) * 512
+    assert lib.motif_gda_prefill_workspace_bytes(1, 512, 8, 4, 8, 128, 3716) == parts(vrows, 3)
+    assert lib.motif_gda_prefill_workspace_bytes(1, 512, 8, 4, 8, 128, 512) == 0
+    _native.set_tuning("prefill_ncb", 1)
+    try:  # one block per wave: 160 blocks fit two rounds at 3 splits of 38 tiles
+        assert lib.motif_gda_prefill_workspace_bytes(1, 512, 8, 4, 8, 128, 3716) == parts(vrows, 3)
+    finally:
+        _native.set_tuning("prefill_ncb", 0)
+    assert lib.motif_sdpa_workspace_bytes(1, 32, 8, 512, 3716, 128) >= parts(32 * 512, 4)
