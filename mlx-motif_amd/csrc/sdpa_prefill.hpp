@@ -479,21 +479,27 @@ sdpa_prefill_kernel(SdpaArgs a) {
       ++inflight;
     }
   };
+  // A wave whose columns all lie past the last virtual head (a slab's
+  // 20 heads in a 4-wave block) only copies its share of the tiles and
+  // meets the others at the barriers.
+  const bool wave_busy = __builtin_amdgcn_readfirstlane(wg_vh0 + wave * NCB * 16 < a.GV);
   if constexpr (NCB == 1) {
     floatx4 s_cur[2], s_nxt[2];
     if (ntiles > 0) {
       publish(0);
-      SwizzledTileAcc<T>::scores(ring[0][0], qb[0], s_cur, col, blk);
+      if (wave_busy) SwizzledTileAcc<T>::scores(ring[0][0], qb[0], s_cur, col, blk);
     }
     for (int i = 0; i < ntiles; ++i) {
       if (i + 1 < ntiles) {
         publish(i + 1);
-        SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb[0], s_nxt, col, blk);
+        if (wave_busy) SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb[0], s_nxt, col, blk);
       }
-      st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end, lim[0],
-                       a.qscale, col, blk);
-      s_cur[0] = s_nxt[0];
-      s_cur[1] = s_nxt[1];
+      if (wave_busy) {
+        st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end,
+                         lim[0], a.qscale, col, blk);
+        s_cur[0] = s_nxt[0];
+        s_cur[1] = s_nxt[1];
+      }
     }
   } else {
     // One tile per barrier (publish(i) frees the stage of tile i - 2 as above).
