@@ -152,8 +152,12 @@ PrefillPlan plan_prefill(int B, int Hq, int Hkv, int S_q, int kv_len, int D) {
   // virtual heads per KV head on, even if the row splits that fill the GPU
   // then need the merge launch; 4 below (measured, 32 q-heads over 8 KV
   // heads: 512 rows over 3716 157 -> 127 us, 256 rows 93 -> 76 us; at 64
-  // rows 4 waves are faster, 41 vs 47 us).
-  p.waves = GV >= 512 ? 8 : 4;
+  // rows 4 waves were faster, 41 vs 47 us, now even).  Slabs of fewer than
+  // 64 heads (17..63 over 2048+ rows) take 8 waves too: the waves past the
+  // heads only copy tiles, and the extra copy issuers help a read-bound
+  // block (5 rows over 32768: 38.0 vs 40.3 us; over 16000: 23.3 vs 24.9; 8
+  // rows over 16000: 23.8 vs 25.5).
+  p.waves = GV >= 512 || GV < kPrefillMinHeads ? 8 : 4;
   if (tuning().waves_per_wg) p.waves = tuning().waves_per_wg;
   // Two column blocks per wave (256 virtual heads per 8-wave block: each
   // K/V fragment read from LDS feeds twice the MFMAs) from 2048 virtual heads
