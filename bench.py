@@ -398,10 +398,12 @@ def main() -> int:
     ap.add_argument("--valu", action="store_true",
                     help="route attention through the VALU kernels (matrix cores off), "
                          "for comparison")
-    ap.add_argument("--traffic", nargs="?", const="f16", choices=("f16", "q4", "q8", "prefill"),
+    ap.add_argument("--traffic", nargs="?", const="f16",
+                    choices=("f16", "q4", "q8", "prefill", "slab_q4", "slab_q8"),
                     help="counter pass: one 256 MiB copy, then 16 eager decode calls on the "
                          "given cache (default f16), or 6 prefill-chunk calls (512 rows over "
-                         "3716, fp16); no timing, no JSON; run under rocprofv3 --pmc")
+                         "3716, fp16), or 6 verify-slab calls (5 rows over 32768, q4 / q8); "
+                         "no timing, no JSON; run under rocprofv3 --pmc")
     ap.add_argument("--summarize-traffic", nargs=3, metavar=("KIND", "FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic_sdpa_dual_v_<KIND>_kv16000.json from the CSV "
                          "directories of the FETCH_SIZE and WRITE_SIZE passes (no GPU)")
@@ -500,6 +502,15 @@ def traffic_pass(torch, lib, dev, kind: str = "f16") -> int:
             calls[i % len(calls)]()
         torch.cuda.synchronize()
         log("traffic pass: copy 268435456 B + 6 prefill calls (512 rows over 3716)")
+        del calls, keep
+        return 0
+    if kind.startswith("slab_"):
+        bits = 4 if kind == "slab_q4" else 8
+        calls, keep = make_q_calls(torch, lib, dev, 2, bits, kv_len=32768, cap=32768, s_q=5)
+        for i in range(6):
+            calls[i % len(calls)]()
+        torch.cuda.synchronize()
+        log(f"traffic pass: copy 268435456 B + 6 q{bits} slab calls (5 rows over 32768)")
         del calls, keep
         return 0
     if kind == "f16":

@@ -426,7 +426,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * 1 only 8-bit slabs; 0 neither), "waves_per_wg" 4 also selects that
  * kernel's 4-wave variant, "qslab_ws" (1, the default: its 8-wave variant
  * runs four producer waves beside four consumer waves; 0: every wave does
- * both), "merge_rows" (1, the default: a merge launch of at least 2048
+ * both), "qslab_sets" (2, the default: its producers hold two steps of
+ * packed data in registers; 3: three, one more step of loads in flight),
+ * "merge_rows" (1, the default: a merge launch of at least 2048
  * partial rows runs one wave per row; 0: one wave per row slice),
  * "prefill_ncb" (column blocks of 16 virtual heads per wave of the 8-wave
  * shared-tile kernels: 0, the default, takes 2 from 2048 virtual heads per

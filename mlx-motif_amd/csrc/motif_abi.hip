@@ -374,6 +374,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.merge_rows = value; });
+  } else if (!strcmp(key, "qslab_sets")) {
+    if (value < 2 || value > 3) {
+      set_error("motif_set_tuning: qslab_sets must be 2 or 3");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.qslab_sets = value; });
   } else if (!strcmp(key, "prefill_min_heads")) {
     if (value < 0) {
       set_error("motif_set_tuning: prefill_min_heads must be >= 0");

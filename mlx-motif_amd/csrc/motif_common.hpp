@@ -42,6 +42,7 @@ struct Tuning {
   int qslab = 2;           // slabs of 17..64 virtual heads, tiles dequantised into LDS: 0 off, 1 q8, 2 q4+q8
   int qslab_ws = 1;        // slab kernel with producer / consumer waves (8 waves): 1 on, 0 off
   int merge_rows = 1;      // row-per-wave merge launch from 2048 partial rows: 1 on, 0 off
+  int qslab_sets = 2;      // producer register sets of the producer / consumer slab kernel (2 or 3)
   int prefill_ncb = 0;     // column blocks per wave of the 8-wave prefill kernel (0 = automatic)
   int prefill_min_heads = 0;  // virtual heads per KV head from which multi-row fp16/bf16 calls take the shared-tile kernel (0: automatic)
 };

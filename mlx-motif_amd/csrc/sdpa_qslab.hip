@@ -5,14 +5,23 @@
 
 namespace motif {
 
+template <int BITS, int GS, int NCB>
+static void launch_qslab_ws(const SdpaArgs& a, int sets, int nblocks, hipStream_t st) {
+  if (sets == 3)
+    hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, NCB, 3>), dim3(nblocks), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, NCB, 2>), dim3(nblocks), dim3(512), 0, st, a);
+}
+
 template <int BITS, int GS>
 static int launch_qslab_gs(const SdpaArgs& a, int ncb, int waves, int nblocks, hipStream_t st) {
   // 8 waves: producer / consumer roles (dequantisation beside the attention)
   if (waves == 8 && tuning().qslab_ws) {
+    const int sets = tuning().qslab_sets;
     if (ncb == 2)
-      hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, 2>), dim3(nblocks), dim3(512), 0, st, a);
+      launch_qslab_ws<BITS, GS, 2>(a, sets, nblocks, st);
     else
-      hipLaunchKernelGGL((sdpa_qslab_ws_kernel<BITS, GS, 4>), dim3(nblocks), dim3(512), 0, st, a);
+      launch_qslab_ws<BITS, GS, 4>(a, sets, nblocks, st);
     return check_launch("sdpa_dual_v_q (slab, producer/consumer)");
   }
   if (ncb == 2 && waves == 8)

@@ -28,6 +28,11 @@
 
 namespace motif {
 
+// Floats per lane of the consumer waves' merge records in LDS: 64 of o,
+// then m and l, padded to a multiple of four so that every lane's float4
+// accesses are 16-byte aligned (68 dwords per lane also put the 16 lanes of
+// one access phase in distinct bank groups).
+constexpr int kQslabMergeFloats = 68;
 
 // Workgroup barrier after this wave's LDS writes completed, without the
 // vector-memory wait of __syncthreads' fence (the packed loads in flight
@@ -150,7 +155,7 @@ sdpa_qslab_kernel(SdpaArgs a) {
   // The same LDS holds the merge of the column blocks' waves at the end; a
   // spare stage is added where the merge needs it.
   constexpr int STAGE_BYTES = NP * 3 * TR * D * 2;
-  constexpr int MERGE_BYTES = NCB * (NP / 2) * 64 * 66 * 4;
+  constexpr int MERGE_BYTES = NCB * (NP / 2) * 64 * kQslabMergeFloats * 4;
   constexpr int NSA = NS * STAGE_BYTES >= MERGE_BYTES ? NS : NS + 1;
   static_assert(NSA * STAGE_BYTES >= MERGE_BYTES, "merge fits the stages");
   __shared__ __attribute__((aligned(16))) uint8_t ring[NSA][NP][3][TR * D * 2];
@@ -241,11 +246,11 @@ sdpa_qslab_kernel(SdpaArgs a) {
   // ring is free after the last barrier), halving the count each round: the
   // upper half of the waves writes, the lower half adds.
   if constexpr (NP > 1) {
-    float* xo = reinterpret_cast<float*>(&ring[0][0][0][0]);  // [NCB][NP / 2][64 lanes][66]
+    float* xo = reinterpret_cast<float*>(&ring[0][0][0][0]);  // [NCB][NP / 2][64 lanes][kQslabMergeFloats]
 #pragma unroll
     for (int half = NP / 2; half >= 1; half /= 2) {
       if (tp >= half && tp < 2 * half) {
-        float* p = xo + ((cb * (NP / 2) + tp - half) * 64 + lane) * 66;
+        float* p = xo + ((cb * (NP / 2) + tp - half) * 64 + lane) * kQslabMergeFloats;
 #pragma unroll
         for (int jx = 0; jx < 8; ++jx) {
           *reinterpret_cast<float4*>(p + 4 * jx) =
@@ -258,7 +263,7 @@ sdpa_qslab_kernel(SdpaArgs a) {
       }
       __syncthreads();
       if (tp < half) {
-        const float* p = xo + ((cb * (NP / 2) + tp) * 64 + lane) * 66;
+        const float* p = xo + ((cb * (NP / 2) + tp) * 64 + lane) * kQslabMergeFloats;
         const float m2 = p[64];
         const float m = fmaxf(acc.m_run, m2);
         const float f1 = fast_exp2(acc.m_run - m);
@@ -313,7 +318,9 @@ sdpa_qslab_kernel(SdpaArgs a) {
 // under an fp16 exponent), a packed subtract leaves u exactly, and a packed
 // fma gives s * u + b rounded once to fp16 -- the value mx.dequantize feeds
 // the reference path's attention (src/mlx_motif/kernels/attention.py:497-499).
-template <int BITS, int GS, int NCB>
+// NSET: register sets of packed step data per producer thread (NSET - 1
+// steps in flight beside the one being dequantised).
+template <int BITS, int GS, int NCB, int NSET = 2>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 sdpa_qslab_ws_kernel(SdpaArgs a) {
   using Acc = SwizzledTileAcc<half_t>;
@@ -328,6 +335,7 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   constexpr int CPT = 3 * NP;        // chunks per producer thread per step
   static_assert(NCB == 2 || NCB == 4, "2 or 4 column blocks");
   static_assert(GS % 16 == 0, "a chunk sits in one scale group");
+  static_assert(NSET == 2 || NSET == 3, "2 or 3 register sets");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -356,7 +364,7 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   // chunk c of row r at byte r * 256 + (c ^ (r % 16)) * 16.  Reused by the
   // consumers' merge at the end.
   constexpr int STAGE_BYTES = NP * 3 * TR * D * 2;
-  constexpr int MERGE_BYTES = NCB * (NP / 2) * 64 * 66 * 4;
+  constexpr int MERGE_BYTES = NCB * (NP / 2) * 64 * kQslabMergeFloats * 4;
   static_assert(2 * STAGE_BYTES >= MERGE_BYTES, "merge fits the stages");
   __shared__ __attribute__((aligned(16))) uint8_t ring[2][NP][3][TR * D * 2];
 
@@ -421,9 +429,13 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
           // bytes 2i%4, 2i%4 + 1 of word i / 2 under the exponent byte 0x64
           x = __builtin_amdgcn_perm(0x64646464u, cw[i / 2], (i & 1) ? 0x04030402u : 0x04010400u);
         } else {
-          // the two nibbles of byte i % 4 of word i / 4
-          const uint32_t by = (cw[i / 4] >> (8 * (i % 4))) & 0xFFu;
-          x = (by & 0xFu) | ((by >> 4) << 16) | 0x64006400u;
+          // the two nibbles of byte k = i % 4 of word i / 4: the word's low
+          // and high nibble planes (shared by its four pairs), then byte k
+          // of each into the low byte of one half and the exponent bits
+          const uint32_t w = cw[i / 4];
+          const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+          const uint32_t k = (uint32_t)(i % 4);
+          x = __builtin_amdgcn_perm(hi, lo, 0x0C000C00u | ((4u + k) << 16) | k) | 0x64006400u;
         }
         const half2_t u = as_h2(x) - k1024;
         h[i] = h2_bits(__builtin_elementwise_fma(u, s2, b2));
@@ -436,41 +448,45 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
     }
   };
 
-  // Producers: step j's data in set A for even j, set B for odd j (loaded
-  // two steps ahead; steps past the last read past the resources' ends:
-  // zeros, no memory access).  The two roles run separate loops with the
+  // Producers: loads of steps past the last read past the resources' ends
+  // (zeros, no memory access).  The two roles run separate loops with the
   // same barriers (one per step, then the merge's), so their registers do
   // not add up; the step count is uniform over the workgroup, so every
   // barrier is reached by all of its threads.
   constexpr int kMergeBarriers = NP == 4 ? 4 : NP == 2 ? 2 : 0;
   if (producer) {
-    Packed PA, PB;
-    // Step 0 alone first (it lands sooner with nothing queued behind it),
-    // then the next two.
-    load(PA, 0);
-    dequant_store(PA, 0);
-    load(PB, 1);
-    load(PA, 2);
-    qslab_barrier();
-    // Unrolled by two, so that the compiler's wait before each set's
-    // dequantisation counts the other set's loads as still in flight.
+    // Step s in set s % NSET, loaded NSET steps ahead; after step 0 (alone
+    // first: it lands sooner with nothing queued behind it), one
+    // dequantisation and one barrier per step s = 1 .. nsteps (the last is
+    // past the end: zeros, never consumed), unrolled by NSET so that the
+    // compiler's wait before each set's dequantisation counts the other
+    // sets' loads as still in flight.  Step s goes to ring stage s & 1.
     // (The scheduling barriers keep the dequantisation of the set due after
     // a barrier from being hoisted above it, where its wait would also
-    // drain the loads of the other set.)
-    int j = 0;
-    for (; j + 1 < nsteps; j += 2) {
-      dequant_store(PB, 1);  // step j + 1
-      load(PB, j + 3);
-      qslab_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      dequant_store(PA, 0);  // step j + 2
-      load(PA, j + 4);
-      qslab_barrier();
-      __builtin_amdgcn_sched_barrier(0);
+    // drain the loads of the other sets.)
+    Packed P[NSET];
+    load(P[0], 0);
+    dequant_store(P[0], 0);
+#pragma unroll
+    for (int u = 1; u < NSET; ++u) load(P[u], u);
+    load(P[0], NSET);
+    qslab_barrier();
+    int st = 1;  // st % NSET == 1 at the top of every pass
+    for (; st + NSET - 1 <= nsteps; st += NSET) {
+#pragma unroll
+      for (int u = 0; u < NSET; ++u) {
+        dequant_store(P[(1 + u) % NSET], (st + u) & 1);
+        load(P[(1 + u) % NSET], st + u + NSET);
+        qslab_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    if (j < nsteps) {
-      dequant_store(PB, 1);
-      qslab_barrier();
+#pragma unroll
+    for (int u = 0; u + 1 < NSET; ++u) {
+      if (st + u <= nsteps) {
+        dequant_store(P[(1 + u) % NSET], (st + u) & 1);
+        qslab_barrier();
+      }
     }
 #pragma unroll
     for (int i = 0; i < kMergeBarriers; ++i) __syncthreads();
@@ -499,11 +515,11 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   // LDS (the ring is free after the last barrier); every wave takes part in
   // the barriers.
   if constexpr (NP > 1) {
-    float* xo = reinterpret_cast<float*>(&ring[0][0][0][0]);  // [NCB][NP / 2][64 lanes][66]
+    float* xo = reinterpret_cast<float*>(&ring[0][0][0][0]);  // [NCB][NP / 2][64 lanes][kQslabMergeFloats]
 #pragma unroll
     for (int half = NP / 2; half >= 1; half /= 2) {
       if (tp >= half && tp < 2 * half) {
-        float* p = xo + ((cb * (NP / 2) + tp - half) * 64 + lane) * 66;
+        float* p = xo + ((cb * (NP / 2) + tp - half) * 64 + lane) * kQslabMergeFloats;
 #pragma unroll
         for (int jx = 0; jx < 8; ++jx) {
           *reinterpret_cast<float4*>(p + 4 * jx) =
@@ -516,7 +532,7 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
       }
       __syncthreads();
       if (tp < half) {
-        const float* p = xo + ((cb * (NP / 2) + tp) * 64 + lane) * 66;
+        const float* p = xo + ((cb * (NP / 2) + tp) * 64 + lane) * kQslabMergeFloats;
         const float m2 = p[64];
         const float m = fmaxf(acc.m_run, m2);
         const float f1 = fast_exp2(acc.m_run - m);

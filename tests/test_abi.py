@@ -114,6 +114,10 @@ def test_workspace_sizing_and_tuning():
         with pytest.raises(_native.MotifNativeError):
             _native.set_tuning("prefill_ncb", bad)
     _native.set_tuning("prefill_ncb", 0)
+    for bad in (1, 4):
+        with pytest.raises(_native.MotifNativeError):
+            _native.set_tuning("qslab_sets", bad)
+    _native.set_tuning("qslab_sets", 2)
     with pytest.raises(_native.MotifNativeError):
         _native.set_tuning("prefill_min_heads", -1)
     # the shared-tile kernel's workspace is covered from 17 heads over 2048+ rows

@@ -26,21 +26,24 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=[(0, 1), (0, 0), (4, 1)], ids=["w8_roles", "w8", "w4"])
+@pytest.fixture(autouse=True, params=[(0, 1, 2), (0, 1, 3), (0, 0, 2), (4, 1, 2)],
+                ids=["w8_roles", "w8_roles_3sets", "w8", "w4"])
 def slab_kernel(request):
     """Every slab on the slab kernel (qslab 2: 4-bit slabs too): 8 waves as
-    producers and consumers (default), 8 waves sharing every step's work,
-    and 4 waves."""
+    producers and consumers (default, and with three producer register
+    sets), 8 waves sharing every step's work, and 4 waves."""
     from mlx_motif import _native
 
-    waves, roles = request.param
+    waves, roles, sets = request.param
     _native.set_tuning("qslab", 2)
     _native.set_tuning("waves_per_wg", waves)
     _native.set_tuning("qslab_ws", roles)
+    _native.set_tuning("qslab_sets", sets)
     yield
     _native.set_tuning("qslab", 2)
     _native.set_tuning("waves_per_wg", 0)
     _native.set_tuning("qslab_ws", 1)
+    _native.set_tuning("qslab_sets", 2)
 
 _CASES = [
     # B, Hq, Hkv, S, cap, kv_len, causal, bits, gs
