@@ -138,3 +138,50 @@ def test_swift_calls_match_the_c_declarations():
                  "motif_gda_decode_proj", "motif_gda_decode_q_proj", "motif_rope_split4",
                  "motif_gda_post_split", "motif_polynorm", "motif_quant_write4"):
         assert name in called, f"no Swift wrapper calls {name}"
+
+
+LAYER = SWIFT.parent / "MotifHIPGroupedAttention.swift"
+
+
+def _swift_funcs(text: str) -> dict[str, list[tuple[str, bool]]]:
+    """name -> [(argument label, has default)] of each `static func` of the
+    wrapper (labels as a call site writes them)."""
+    funcs = {}
+    for m in re.finditer(r"static func (\w+)\s*\(", text):
+        i, depth = m.end(), 1
+        while depth:
+            depth += {"(": 1, ")": -1}.get(text[i], 0)
+            i += 1
+        params = []
+        for p in _split_args(text[m.end():i - 1]):
+            p = p.strip()
+            if not p:
+                continue
+            head = p.split(":", 1)[0].split()
+            params.append((head[0], "=" in p.split(":", 1)[1]))
+        funcs[m.group(1)] = params
+    return funcs
+
+
+def test_swift_layer_calls_match_the_wrapper_labels():
+    """The layer over the wrapper (MotifHIPGroupedAttention.swift) calls each
+    MotifHIP function with its argument labels in declaration order, leaving
+    out only defaulted ones -- what the Swift compiler would check."""
+    funcs = _swift_funcs(re.sub(r"//[^\n]*", "", SWIFT.read_text()))
+    text = re.sub(r"//[^\n]*", "", LAYER.read_text())
+    calls = _calls(text, r"\bMotifHIP\.(\w+)")
+    assert calls, "no MotifHIP calls found in the layer"
+    for name, args in calls:
+        assert name in funcs, f"the layer calls MotifHIP.{name}, which the wrapper lacks"
+        labels = [a.split(":", 1)[0].strip() for a in args]
+        declared = [lab for lab, _ in funcs[name]]
+        required = [lab for lab, dflt in funcs[name] if not dflt]
+        assert labels == [lab for lab in declared if lab in labels], (
+            f"MotifHIP.{name}: labels {labels} out of declaration order {declared}")
+        assert set(required) <= set(labels), (
+            f"MotifHIP.{name}: missing {sorted(set(required) - set(labels))}")
+    called = {n for n, _ in calls}
+    for name in ("gdaDecodeFromProjections", "gdaDecodeQuantizedFromProjections",
+                 "gdaPrefillFromProjections", "ropeSplit4", "gdaDecode",
+                 "gdaDecodeQuantizedAppend", "gdaPostSplit"):
+        assert name in called, f"the layer never calls MotifHIP.{name}"
