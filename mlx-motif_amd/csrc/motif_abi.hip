@@ -298,6 +298,11 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
     const size_t w16 =
         plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 0, 0).workspace_bytes;
     if (w16 > ws) ws = w16;
+    if (S_q == 1 && kv_len <= kShortDecodeRows) {  // short decode calls: 4-wave plan
+      const size_t w4 =
+          plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 4, 1).workspace_bytes;
+      if (w4 > ws) ws = w4;
+    }
     for (int gs = 32; gs <= 128; gs *= 2) {
       const int nb = sdpa_q_blocks((Hkv > 0 ? Hq / Hkv : 1) * S_q, D, gs);
       const SdpaPlan p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),

@@ -94,8 +94,11 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // conditions are those under which the dispatch picks that kernel.
   const bool mfma16 = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
                       tuning().mfma && aligned(q, 16) && kv_len <= kMfmaMaxRows;
+  // Short single-row calls: 4-wave workgroups, one per CU (kShortDecodeRows).
+  const bool short4 = mfma16 && S_q == 1 && kv_len <= kShortDecodeRows;
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
-                       ws_bytes, mfma16 ? kSdpaMfmaGcMax : sdpa_gc_max(D), 0, 0);
+                       ws_bytes, mfma16 ? kSdpaMfmaGcMax : sdpa_gc_max(D), short4 ? 4 : 0,
+                       short4 ? 1 : 0);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
   const int al = sdpa_fp_align(dtype, D);

@@ -182,6 +182,13 @@ QSlabPlan plan_qslab(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
 // first row: they take kv_len <= kMfmaMaxRows (the VALU kernels take the
 // rest).
 constexpr int kMfmaMaxRows = 1 << 22;
+// Single-row fp16/bf16 decode calls over at most this many rows run 4-wave
+// workgroups, one per CU, instead of 8-wave ones: with few rows per split
+// the smaller blocks reach their first tile sooner (32 q-heads over 8 KV
+// heads, D 128, µs per call 8 / 4 waves: 1024 rows 8.84 / 7.51, 2048 9.08 /
+// 8.07, 3204 9.59 / 9.20, 4096 9.97 / 9.69, 6144 12.19 / 12.09, 8192 13.59 /
+// 14.03).
+constexpr int kShortDecodeRows = 4096;
 
 // Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
 // workgroups at one wave per SIMD, one per CU.
