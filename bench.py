@@ -65,14 +65,20 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_calls(torch, calls, steps: int, warmup: int, use_graph: bool = True):
-    """Average µs per call over `steps` calls cycling through `calls`."""
+REPEATS = 7  # timed replays per workload; the median is reported
+
+
+def time_calls_stats(torch, calls, steps: int, warmup: int, use_graph: bool = True,
+                     repeats: int = REPEATS):
+    """µs per call over `steps` calls cycling through `calls`: the graph of
+    the `steps` calls (or the eager sequence) is timed `repeats` times, each
+    between two HIP events on the launch stream.  Returns (median, min, max)
+    over the repeats."""
     for i in range(warmup):
         calls[i % len(calls)]()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    g = None
     if use_graph:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -80,16 +86,26 @@ def time_calls(torch, calls, steps: int, warmup: int, use_graph: bool = True):
                 calls[i % len(calls)]()
         g.replay()  # warm replay
         torch.cuda.synchronize()
+    per_call = []
+    for _ in range(repeats):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        g.replay()
+        if g is not None:
+            g.replay()
+        else:
+            for i in range(steps):
+                calls[i % len(calls)]()
         end.record(stream)
-    else:
-        start.record(stream)
-        for i in range(steps):
-            calls[i % len(calls)]()
-        end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1000.0 / steps
+        torch.cuda.synchronize()
+        per_call.append(start.elapsed_time(end) * 1000.0 / steps)
+    return statistics.median(per_call), min(per_call), max(per_call)
+
+
+def time_calls(torch, calls, steps: int, warmup: int, use_graph: bool = True,
+               repeats: int = REPEATS):
+    """Median µs per call (see time_calls_stats)."""
+    return time_calls_stats(torch, calls, steps, warmup, use_graph, repeats)[0]
 
 
 def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1,
@@ -229,6 +245,39 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     return [(mk_q if bits else mk)(*t) for t in sets], (q1, q2, w, lam, sets, y, o, n, ws)
 
 
+def make_small_step_calls(torch, lib, dev, nsets, kv_len=1024):
+    """The small GDA decode step: q1, q2 (1, 8, 1, D) over k1/k2/v1/v2 (1, 4,
+    kv_len, D) fp16, two motif_sdpa_dual_v calls (GQA 2) then
+    motif_gda_post_split with gr 1 into y (1, 8, 1, 2D)."""
+    from mlx_motif import _native
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    q1, q2 = (torch.randn((1, 8, 1, D), generator=g, device=dev).half() for _ in range(2))
+    w = torch.rand(2 * D, generator=g, device=dev).half()
+    lam = torch.tensor([0.37], dtype=torch.float32, device=dev)
+    sets = [tuple(torch.randn((1, 4, kv_len, D), generator=g, device=dev).half()
+                  for _ in range(4)) for _ in range(nsets)]
+    o, n, y = (torch.empty((1, 8, 1, 2 * D), dtype=torch.float16, device=dev) for _ in range(3))
+    nbytes = lib.motif_sdpa_workspace_bytes(1, 8, 4, 1, kv_len, D)
+    ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+    scale = 1.0 / D ** 0.5
+
+    def mk(k1, k2, v1, v2):
+        def call():
+            st = torch.cuda.current_stream().cuda_stream
+            for q, k, out in ((q1, k1, o), (q2, k2, n)):
+                _native.check(lib.motif_sdpa_dual_v(
+                    q.data_ptr(), k.data_ptr(), v1.data_ptr(), v2.data_ptr(), out.data_ptr(), 0,
+                    1, 8, 4, D, kv_len, kv_len, scale, ws.data_ptr(), ws.numel(), st))
+            _native.check(lib.motif_gda_post_split(
+                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), 0, 1, 8, 8, 1, 1, 2 * D,
+                lam.data_ptr(), 0.8, 1e-5, st))
+        return call
+
+    return [mk(*t) for t in sets], (q1, q2, w, lam, sets, o, n, y, ws)
+
+
 def decode_bytes(kv_len: int, fused: bool, gr: int = 4, bits=None) -> int:
     """Cache bytes of one decode step: 4 streams fused, 6 for the three calls
     (v1 and v2 read by both passes), plus q and y.  A packed row holds
@@ -311,13 +360,19 @@ def cpu_baseline():
                 times.append((t1 - t0) * 1e6)
         return statistics.median(times)
 
-    f16 = lambda n: c_oracle.sdpa_dual_v_f16(q, k, v1, v2, scale, KV_LEN, nthreads=n)  # noqa: E731
-    q4 = lambda n: c_oracle.sdpa_dual_v_q_f16(q, *trips, scale, GS, 4, KV_LEN,  # noqa: E731
-                                              nthreads=n)
+    def f16(n, fast=False):
+        return c_oracle.sdpa_dual_v_f16(q, k, v1, v2, scale, KV_LEN, nthreads=n, fast=fast)
+
+    def q4(n, fast=False):
+        return c_oracle.sdpa_dual_v_q_f16(q, *trips, scale, GS, 4, KV_LEN, nthreads=n, fast=fast)
+
     us = median_us(lambda: f16(threads), 5)
     us_q4 = median_us(lambda: q4(threads), 5)
     us_1 = median_us(lambda: f16(1), 3)
     us_q4_1 = median_us(lambda: q4(1), 3)
+    fus = median_us(lambda: f16(threads, True), 5)
+    fus_q4 = median_us(lambda: q4(threads, True), 5)
+    fus_1 = median_us(lambda: f16(1, True), 3)
     try:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -328,14 +383,19 @@ def cpu_baseline():
         "cores": threads,
         "kind": "port",
         "sample": "one full sdpa_dual_v call (32 heads x 16000 rows, D 128) of the C/OpenMP "
-                  "port oracle/motif_oracle.c (gcc -O2, scalar), fp16 cache (value) and q4 "
-                  "cache, on `cores` OpenMP threads (median of 5 after 2 warm-ups) and on one "
-                  "thread (median of 3)",
+                  "port oracle/motif_oracle.c, fp16 cache (value) and q4 cache, on `cores` "
+                  "OpenMP threads (median of 5 after 2 warm-ups) and on one thread (median of "
+                  "3); value: gcc -O2 -mf16c -ffp-contract=off (scalar, the checker's build); "
+                  "`vectorised`: the same source built gcc -O3 -march=x86-64-v3 -ffast-math",
         "gbps": round(alg_bytes("f16") / us / 1e3, 2),
         "one_thread_us": round(us_1, 1),
         "q4_us": round(us_q4, 1),
         "q4_gbps": round(alg_bytes("q4") / us_q4 / 1e3, 2),
         "q4_one_thread_us": round(us_q4_1, 1),
+        "vectorised": {"us": round(fus, 1), "gbps": round(alg_bytes("f16") / fus / 1e3, 2),
+                       "one_thread_us": round(fus_1, 1), "q4_us": round(fus_q4, 1),
+                       "q4_gbps": round(alg_bytes("q4") / fus_q4 / 1e3, 2),
+                       "flags": "gcc -O3 -fopenmp -march=x86-64-v3 -ffast-math"},
         "cpu_model": _cpu_model(),
         "nproc": os.cpu_count(),
         "affinity_cpus": affinity,
@@ -434,13 +494,14 @@ def main() -> int:
             calls, keep = make_fp16_calls(torch, lib, dev, nsets)
         else:
             calls, keep = make_q_calls(torch, lib, dev, nsets, 4 if kind == "q4" else 8)
-        us = time_calls(torch, calls, args.steps, args.warmup, graph)
+        us, us_min, us_max = time_calls_stats(torch, calls, args.steps, args.warmup, graph)
         gbps = alg_bytes(kind) / us / 1e3
-        res[kind] = {"us_per_call": round(us, 3), "gbps": round(gbps, 1),
+        res[kind] = {"us_per_call": round(us, 3), "us_min": round(us_min, 3),
+                     "us_max": round(us_max, 3), "repeats": REPEATS, "gbps": round(gbps, 1),
                      "pct_peak": round(100 * gbps / PEAK_HBM_GBPS, 1),
                      "alg_bytes": alg_bytes(kind), "buffer_sets": nsets}
-        log(f"{kind}: {us:.3f} us/call  {gbps:.1f} GB/s  ({100 * gbps / PEAK_HBM_GBPS:.1f}% of "
-            f"{PEAK_HBM_GBPS:.0f})")
+        log(f"{kind}: {us:.3f} us/call (median of {REPEATS}; {us_min:.3f}..{us_max:.3f})  "
+            f"{gbps:.1f} GB/s  ({100 * gbps / PEAK_HBM_GBPS:.1f}% of {PEAK_HBM_GBPS:.0f})")
         del calls, keep
         torch.cuda.empty_cache()
 
@@ -449,8 +510,9 @@ def main() -> int:
     sec = None if args.no_secondary else secondary(torch, lib, dev)
 
     f16 = res["f16"]
-    basis = ("algorithmic bytes / us per call; a call is the attention launch plus the "
-             "split-merge launch (HIP events around graph-replayed calls)")
+    basis = ("algorithmic bytes / median us per call; a call is the attention launch plus the "
+             "split-merge launch (HIP events around graph-replayed calls, median of "
+             f"{REPEATS} replays of --steps calls)")
     out = {
         "metric": METRIC,
         "value": f16["us_per_call"],
@@ -603,35 +665,70 @@ def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
     projections (RoPE + 4-slot write + both passes in one launch)."""
     from mlx_motif.kernels import gda_prefill_attention_from_proj
 
+    from mlx_motif.kernels import gda_post_split, polynorm
+
     out = {}
 
-    def hbm(name, us, nbytes):
+    def hbm(name, st, nbytes):
+        us = st[0]
         gbps = nbytes / us / 1e3
-        out[name] = {"us_per_call": round(us, 3), "gbps": round(gbps, 1),
+        out[name] = {"us_per_call": round(us, 3), "us_min": round(st[1], 3),
+                     "us_max": round(st[2], 3), "gbps": round(gbps, 1),
                      "pct_peak_hbm": round(100 * gbps / PEAK_HBM_GBPS, 1)}
 
-    def mfma(name, us, flops):
+    def mfma(name, st, flops):
+        us = st[0]
         tf = flops / us / 1e6
-        out[name] = {"us_per_call": round(us, 3), "tflops": round(tf, 1),
+        out[name] = {"us_per_call": round(us, 3), "us_min": round(st[1], 3),
+                     "us_max": round(st[2], 3), "tflops": round(tf, 1),
                      "pct_peak_f16_mfma": round(100 * tf / PEAK_F16_TFLOPS, 1)}
 
-    calls, keep = make_decode_calls(torch, lib, dev, 6, fused=True)
-    hbm("gda_decode_step_f16_kv16000", time_calls(torch, calls, steps, warm),
-        decode_bytes(KV_LEN, True))
+    timed = lambda calls, n=steps: time_calls_stats(torch, calls, n, warm)  # noqa: E731
+
+    # one GDA decode step of the small layer the CPU reference runs: 8
+    # signal/noise head pairs over 4 KV heads (GQA 2), fp16 cache of 1024
+    # rows; two sdpa_dual_v calls + gda_post_split (gr 1)
+    calls, keep = make_small_step_calls(torch, lib, dev, 16)
+    hbm("gda_step_f16_8pairs_4kv_kv1024", timed(calls), 6 * 4 * 1024 * D * 2 + 16 * D * 2 +
+        3 * 8 * 2 * D * 2)
     del calls, keep
+    # the 12.7B layer call at kv 3204, 48 back-to-back calls over 48
+    # distinct layer buffers
+    calls, keep = make_fp16_calls(torch, lib, dev, 48, kv_len=3204, cap=3328)
+    hbm("sdpa_dual_v_f16_kv3204_x48_layers", timed(calls, 48 * 4), alg_bytes("f16", 3204))
+    del calls, keep
+    torch.cuda.empty_cache()
+    calls, keep = make_decode_calls(torch, lib, dev, 6, fused=True)
+    hbm("gda_decode_step_f16_kv16000", timed(calls), decode_bytes(KV_LEN, True))
+    del calls, keep
+    # the fused epilogues at prefill length 3204
+    g7 = torch.Generator(device=dev)
+    g7.manual_seed(7)
+    o = [torch.randn((1, 16, 3204, 128), generator=g7, device=dev).half() for _ in range(8)]
+    n = [torch.randn((1, 16, 3204, 128), generator=g7, device=dev).half() for _ in range(8)]
+    w = torch.rand(128, generator=g7, device=dev).half()
+    lam = torch.tensor([0.37], device=dev)
+    hbm("gda_post_split_1x16x3204x128",
+        timed([lambda i=i: gda_post_split(o[i], n[i], w, lam, 0.2, 1, 1e-6) for i in range(8)]),
+        3 * 16 * 3204 * 128 * 2)
+    del o, n
+    xs = [torch.randn((3204, 13824), generator=g7, device=dev).half() for _ in range(4)]
+    pw = torch.rand(3, generator=g7, device=dev).half()
+    pb = torch.zeros(1, device=dev).half()
+    hbm("polynorm_3204x13824", timed([lambda i=i: polynorm(xs[i], pw, pb, 1e-6)
+                                      for i in range(4)]), 2 * 3204 * 13824 * 2)
+    del xs
+    torch.cuda.empty_cache()
     calls, keep = make_fp16_calls(torch, lib, dev, 6, kv_len=32768, cap=32768, s_q=5)
-    hbm("verify_slab_f16_5x32768", time_calls(torch, calls, steps, warm),
-        alg_bytes("f16", 32768, s_q=5))
+    hbm("verify_slab_f16_5x32768", timed(calls), alg_bytes("f16", 32768, s_q=5))
     del calls, keep
     torch.cuda.empty_cache()
     calls, keep = make_q_calls(torch, lib, dev, 8, 8, kv_len=32768, cap=32768, s_q=5)
-    hbm("verify_slab_q8_5x32768", time_calls(torch, calls, steps, warm),
-        alg_bytes("q8", 32768, s_q=5))
+    hbm("verify_slab_q8_5x32768", timed(calls), alg_bytes("q8", 32768, s_q=5))
     del calls, keep
     torch.cuda.empty_cache()
     calls, keep = make_fp16_calls(torch, lib, dev, 4, kv_len=3716, cap=3840, s_q=512)
-    mfma("prefill_f16_512x3716_causal", time_calls(torch, calls, steps, warm),
-         2 * HQ * 512 * 3716 * D * 3)
+    mfma("prefill_f16_512x3716_causal", timed(calls), 2 * HQ * 512 * 3716 * D * 3)
     del calls, keep
     torch.cuda.empty_cache()
     g = torch.Generator(device=dev)
@@ -645,7 +742,7 @@ def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
             for _ in range(4)]
     calls = [lambda st=st: gda_prefill_attention_from_proj(st[0], st[1], st[2], st[3], off, 8, 4,
                                                            8, D ** -0.5) for st in sets]
-    mfma("prefill_layer_chunk_f16_512_at_3204", time_calls(torch, calls, steps, warm),
+    mfma("prefill_layer_chunk_f16_512_at_3204", timed(calls),
          2 * (HQ + HKV) * D * 3 * sum(off + s + 1 for s in range(S)))
     del calls, sets
     torch.cuda.empty_cache()

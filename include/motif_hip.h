@@ -42,6 +42,7 @@ extern "C" {
 #define MOTIF_ERR_UNSUPPORTED (-2) /* legal shape with no compiled variant     */
 #define MOTIF_ERR_WORKSPACE (-3)   /* workspace missing or too small           */
 #define MOTIF_ERR_HIP (-4)         /* HIP runtime error (launch, device query) */
+#define MOTIF_ERR_INTERNAL (-5)    /* library plan inconsistency; nothing launched */
 
 #define MOTIF_F16 0
 #define MOTIF_BF16 1
@@ -85,8 +86,9 @@ int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* 
  * serving loops, harnesses that forbid hipMalloc).  The split partials and
  * counters live in a static device array of 8 MiB per device (held until
  * the process ends), whose first 64 KiB of counters are cleared by one fill
- * kernel on the device's first call.  A call needing more
- * (motif_sdpa_workspace_bytes > 8 MiB, or more than 16384 B*Hq rows)
+ * kernel on the device's first call; the partials of every call follow
+ * that counter area.  A call needing more (64 KiB + the partial bytes of
+ * motif_sdpa_workspace_bytes > 8 MiB, or more than 16384 B*Hq rows)
  * returns MOTIF_ERR_WORKSPACE before touching the GPU.  All calls on one
  * device share the array: calls that may overlap on a device (several
  * streams, or several threads) race, so order them; results equal
@@ -441,6 +443,18 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.
  * ------------------------------------------------------------------------ */
 int motif_set_tuning(const char* key, int value);
+
+/* ------------------------------------------------------------------------ *
+ * Host-only self-check of the launch planners; no reference counterpart.
+ * Walks every planner over decode, slab and prefill shapes without any HIP
+ * call and checks that each plan of more than one split gets a workspace
+ * holding its counters and partials, that the kernels would receive non-null
+ * partial buffers inside it, that a missing workspace is refused before any
+ * launch, and that motif_sdpa_workspace_bytes covers every plan it sizes.
+ * Returns MOTIF_OK, or MOTIF_ERR_INTERNAL with the failing plan in
+ * motif_last_error().  For tests and for callers that change the tuning.
+ * ------------------------------------------------------------------------ */
+int motif_plan_selfcheck(void);
 
 #ifdef __cplusplus
 }

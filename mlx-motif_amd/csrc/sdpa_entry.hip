@@ -21,12 +21,58 @@ int sdpa_q_align(int D, int bits) {
 
 static bool aligned(const void* p, int a) { return ((uintptr_t)p % (uintptr_t)a) == 0; }
 
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Workspace of a split call: vrows u32 arrival counters (at least
+// counter_reserve bytes of them), then the partial outputs (vrows, nsplit,
+// 2D) fp32, then the partial (m, l) pairs (vrows, nsplit, 2) fp32, each
+// region 256-byte aligned.  counter_reserve > 0 keeps the partials of every
+// call clear of a fixed counter area (the no-alloc scratch, whose counters
+// are cleared once and shared by calls of any size).
+static size_t split_ws_bytes(size_t vrows, int nsplit, int D, size_t counter_reserve) {
+  const size_t c = round256(vrows * sizeof(unsigned));
+  return (c > counter_reserve ? c : counter_reserve) +
+         round256(vrows * nsplit * 2 * D * sizeof(float)) +
+         round256(vrows * nsplit * 2 * sizeof(float));
+}
+
+static int carve_split_ws(const char* name, SdpaArgs& a, void* ws, size_t ws_bytes, size_t vrows,
+                          int nsplit, int D, size_t counter_reserve) {
+  const size_t need = split_ws_bytes(vrows, nsplit, D, counter_reserve);
+  if (ws == nullptr || ws_bytes < need) {
+    set_error("%s: workspace of %zu bytes needed, %zu given", name, need,
+              ws == nullptr ? (size_t)0 : ws_bytes);
+    return MOTIF_ERR_WORKSPACE;
+  }
+  MOTIF_REQUIRE(aligned(ws, 256), "%s: workspace must be 256-byte aligned", name);
+  size_t c = round256(vrows * sizeof(unsigned));
+  if (c < counter_reserve) c = counter_reserve;
+  char* w = (char*)ws;
+  a.counters = (unsigned*)w;
+  a.part_o = (float*)(w + c);
+  a.part_ml = (float*)(w + c + round256(vrows * nsplit * 2 * D * sizeof(float)));
+  return MOTIF_OK;
+}
+
+// Last check before a launch: a kernel that publishes split partials (every
+// plan of more than one split, and the fused decode kernels always) must have
+// somewhere to publish them.  A plan that fails it is a library bug; the call
+// returns before any launch instead of handing a kernel a null base.
+static int check_partials(const char* name, const SdpaArgs& a, bool always) {
+  if (!always && a.nsplit <= 1) return MOTIF_OK;
+  if (a.part_o != nullptr && a.part_ml != nullptr && (!a.fused_merge || a.counters != nullptr))
+    return MOTIF_OK;
+  set_error("%s: internal error: a plan of %d split(s) has no partial buffers (nothing was "
+            "launched)", name, a.nsplit);
+  return MOTIF_ERR_INTERNAL;
+}
+
 // Shared shape checks (the reference asserts of attention.py:237-243, 556-564)
 // and plan/workspace set-up.
 static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, int B, int Hq,
                        int Hkv, int S_q, int D, int kv_cap, int kv_len, int causal, float scale,
                        void* ws, size_t ws_bytes, int gc_max, int waves_pref, int wgs_per_cu,
-                       int gc_fixed = 0) {
+                       int gc_fixed = 0, size_t counter_reserve = 0) {
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "%s: unknown dtype code %d", name, dtype);
   MOTIF_REQUIRE(B >= 1 && Hq >= 1 && Hkv >= 1 && S_q >= 1, "%s: B, H_q, H_kv, S_q must be >= 1",
@@ -54,20 +100,9 @@ static int sdpa_common(const char* name, SdpaArgs& a, SdpaPlan& p, int dtype, in
   a.part_o = nullptr;
   a.part_ml = nullptr;
   a.counters = nullptr;
-  if (p.nsplit > 1) {
-    if (ws == nullptr || ws_bytes < p.workspace_bytes) {
-      set_error("%s: workspace of %zu bytes needed, %zu given", name, p.workspace_bytes,
-                ws == nullptr ? (size_t)0 : ws_bytes);
-      return MOTIF_ERR_WORKSPACE;
-    }
-    MOTIF_REQUIRE(aligned(ws, 256), "%s: workspace must be 256-byte aligned", name);
-    char* w = (char*)ws;
-    a.counters = (unsigned*)w;
-    const size_t vrows = (size_t)B * Hq * S_q;
-    const size_t o_bytes = (vrows * p.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
-    a.part_o = (float*)(w + p.counter_bytes);
-    a.part_ml = (float*)(w + p.counter_bytes + o_bytes);
-  }
+  if (p.nsplit > 1)
+    return carve_split_ws(name, a, ws, ws_bytes, (size_t)B * Hq * S_q, p.nsplit, D,
+                          counter_reserve);
   return MOTIF_OK;
 }
 
@@ -84,7 +119,7 @@ static int sdpa_merge(const SdpaArgs& a, int dtype, int D, hipStream_t s) {
 static int sdpa_fp_run(const char* name, const void* q, const void* k, const void* v1,
                        const void* v2, void* y, int dtype, int B, int Hq, int Hkv, int S_q, int D,
                        int kv_cap, int kv_len, int causal, float scale, void* ws,
-                       size_t ws_bytes, void* stream) {
+                       size_t ws_bytes, void* stream, size_t counter_reserve = 0) {
   CallScope scope;
   clear_error();
   SdpaArgs a{};
@@ -98,7 +133,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   const bool short4 = mfma16 && S_q == 1 && kv_len <= kShortDecodeRows;
   int rc = sdpa_common(name, a, p, dtype, B, Hq, Hkv, S_q, D, kv_cap, kv_len, causal, scale, ws,
                        ws_bytes, mfma16 ? kSdpaMfmaGcMax : sdpa_gc_max(D), short4 ? 4 : 0,
-                       short4 ? 1 : 0);
+                       short4 ? 1 : 0, 0, counter_reserve);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q && y && (kv_cap == 0 || (k && v1 && v2)), "%s: null tensor pointer", name);
   const int al = sdpa_fp_align(dtype, D);
@@ -114,33 +149,30 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // the kernel with LDS-shared K/V tiles reads the cache once per block of
   // up to 128 heads instead of once per 8.
   if ((dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
-      use_shared_tiles(a.GV, kv_len) &&
+      use_shared_tiles(a.GV, kv_len) && tile_softmax_scale_ok(a.qscale) &&
       aligned(q, 16) && aligned(y, 16) && aligned(k, 16) && aligned(v1, 16) &&
       aligned(v2, 16)) {
     const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
-    if (pp.nsplit > 1 && (ws == nullptr || ws_bytes < pp.workspace_bytes)) {
-      set_error("%s: workspace of %zu bytes needed, %zu given", name, pp.workspace_bytes,
-                ws == nullptr ? (size_t)0 : ws_bytes);
-      return MOTIF_ERR_WORKSPACE;
-    }
     a.nchunk = pp.nqb;
     a.nsplit = pp.nsplit;
     a.rows_per_split = pp.rows_per_split;
     a.fused_merge = 0;
+    a.counters = nullptr;
+    a.part_o = a.part_ml = nullptr;
     if (pp.nsplit > 1) {
-      char* w = (char*)ws;
-      const size_t vrows = (size_t)B * Hq * S_q;
-      const size_t cbytes = (vrows * sizeof(unsigned) + 255) / 256 * 256;
-      const size_t obytes = (vrows * pp.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
-      a.counters = (unsigned*)w;
-      a.part_o = (float*)(w + cbytes);
-      a.part_ml = (float*)(w + cbytes + obytes);
+      rc = carve_split_ws(name, a, ws, ws_bytes, (size_t)B * Hq * S_q, pp.nsplit, D,
+                          counter_reserve);
+      if (rc != MOTIF_OK) return rc;
     }
+    rc = check_partials(name, a, false);
+    if (rc != MOTIF_OK) return rc;
     const int nblocks = sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit);
     rc = dtype == MOTIF_F16 ? launch_sdpa_prefill_f16(a, pp.waves, pp.ncb, nblocks, s)
                             : launch_sdpa_prefill_bf16(a, pp.waves, pp.ncb, nblocks, s);
     return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
   }
+  rc = check_partials(name, a, false);
+  if (rc != MOTIF_OK) return rc;
   switch (dtype) {
     case MOTIF_F16: rc = dispatch_sdpa_fp_f16(a, p, D, s); break;
     case MOTIF_BF16: rc = dispatch_sdpa_fp_bf16(a, p, D, s); break;
@@ -213,31 +245,28 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   // 49.0 us in head chunks, q4 35.3 against 43.6 us).
   if (dtype == MOTIF_F16 && D == 128 && tuning().mfma && tuning().qslab >= (bits == 8 ? 1 : 2) &&
       a.GV >= kQSlabMinHeads && a.GV <= kQSlabMaxHeads && kv_len <= kMfmaMaxRows &&
+      tile_softmax_scale_ok(a.qscale) &&
       aligned(q, 16) && aligned(y, 16) && aligned(kd, bits == 8 ? 16 : 8) &&
       aligned(v1d, bits == 8 ? 16 : 8) && aligned(v2d, bits == 8 ? 16 : 8)) {
     const QSlabPlan qp = plan_qslab(B, Hq, Hkv, S_q, kv_len, D);
+    a.counters = nullptr;
+    a.part_o = a.part_ml = nullptr;
     if (qp.nsplit > 1) {
-      if (ws == nullptr || ws_bytes < qp.workspace_bytes) {
-        set_error("%s: workspace of %zu bytes needed, %zu given", name, qp.workspace_bytes,
-                  ws == nullptr ? (size_t)0 : ws_bytes);
-        return MOTIF_ERR_WORKSPACE;
-      }
-      char* w = (char*)ws;
-      const size_t vrows = (size_t)B * Hq * S_q;
-      const size_t cbytes = (vrows * sizeof(unsigned) + 255) / 256 * 256;
-      const size_t obytes = (vrows * qp.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
-      a.counters = (unsigned*)w;
-      a.part_o = (float*)(w + cbytes);
-      a.part_ml = (float*)(w + cbytes + obytes);
+      rc = carve_split_ws(name, a, ws, ws_bytes, (size_t)B * Hq * S_q, qp.nsplit, D, 0);
+      if (rc != MOTIF_OK) return rc;
     }
     a.nchunk = qp.nchunk;
     a.nsplit = qp.nsplit;
     a.rows_per_split = qp.rows_per_split;
     a.fused_merge = 0;
+    rc = check_partials(name, a, false);
+    if (rc != MOTIF_OK) return rc;
     rc = launch_sdpa_qslab(a, bits, gs, qp.ncb, qp.waves,
                            sdpa_grid_blocks(B * Hkv, qp.nchunk, qp.nsplit), s);
     return rc == MOTIF_OK ? sdpa_merge(a, dtype, D, s) : rc;
   }
+  rc = check_partials(name, a, false);
+  if (rc != MOTIF_OK) return rc;
   switch (dtype) {
     case MOTIF_F16: rc = dispatch_sdpa_q_f16(a, p, D, bits, s); break;
     case MOTIF_BF16: rc = dispatch_sdpa_q_bf16(a, p, D, bits, s); break;
@@ -254,8 +283,6 @@ struct GdaDecodeLayout {
   size_t counter_bytes, o_bytes, ml_bytes, fused_bytes;
   size_t sdpa_bytes, yo_bytes, yn_bytes, composed_bytes;
 };
-
-static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int D) {
   GdaDecodeLayout L{};
@@ -445,6 +472,8 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
       a.append = 1;
     }
     const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+    rc = check_partials(name, a, true);
+    if (rc != MOTIF_OK) return rc;
     return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks, s)
                               : launch_gda_decode_bf16(a, gda_columns(gr), nblocks, s);
   }
@@ -540,6 +569,8 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
   a.q_origin_first = origin_first != 0;
   a.rope_log2_theta = log2f(theta);
   const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+  rc = check_partials(name, a, true);
+  if (rc != MOTIF_OK) return rc;
   return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks,
                                                     (hipStream_t)stream)
                             : launch_gda_decode_bf16(a, gda_columns(gr), nblocks,
@@ -559,14 +590,17 @@ int motif_sdpa_dual_v_noalloc(const void* q, const void* k, const void* v1, cons
   CallScope scope;
   clear_error();
   // Size first (host arithmetic only): a call that needs more than the
-  // static scratch is refused before any HIP call.
+  // static scratch is refused before any HIP call.  The counters keep the
+  // first kScratchClearBytes whatever the call's size, and the partials
+  // follow them, so no call's partials land on another call's counters.
   const size_t need = motif_sdpa_workspace_bytes(B, Hq, Hkv, 1, kv_len, D);
-  if (need > kNoAllocScratchBytes || motif_sdpa_counter_bytes(B, Hq, Hkv, 1) > kScratchClearBytes) {
+  const size_t cbytes = motif_sdpa_counter_bytes(B, Hq, Hkv, 1);
+  const size_t total = need > cbytes ? kScratchClearBytes + (need - cbytes) : kScratchClearBytes;
+  if (total > kNoAllocScratchBytes || cbytes > kScratchClearBytes) {
     set_error("sdpa_dual_v_noalloc: this call needs %zu bytes of scratch (%zu bytes of "
               "counters); the static scratch holds %zu (%zu of counters): use "
               "motif_sdpa_dual_v with a workspace",
-              need, motif_sdpa_counter_bytes(B, Hq, Hkv, 1), kNoAllocScratchBytes,
-              kScratchClearBytes);
+              total, cbytes, kNoAllocScratchBytes, kScratchClearBytes);
     return MOTIF_ERR_WORKSPACE;
   }
   void* ws = nullptr;
@@ -575,7 +609,8 @@ int motif_sdpa_dual_v_noalloc(const void* q, const void* k, const void* v1, cons
     if (rc != MOTIF_OK) return rc;
   }
   return sdpa_fp_run("sdpa_dual_v_noalloc", q, k, v1, v2, y, dtype, B, Hq, Hkv, 1, D, kv_cap,
-                     kv_len, 0, scale, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
+                     kv_len, 0, scale, ws, need > 0 ? kNoAllocScratchBytes : 0, stream,
+                     kScratchClearBytes);
 }
 
 int motif_sdpa_dual_v_rows(const void* q, const void* k, const void* v1, const void* v2, void* y,
@@ -706,6 +741,8 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
       a.new_k1 = new_kv[0]; a.new_k2 = new_kv[1]; a.new_v1 = new_kv[2]; a.new_v2 = new_kv[3];
       a.append = 1;
     }
+    rc = check_partials(name, a, true);
+    if (rc != MOTIF_OK) return rc;
     return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
   }
   if (new_kv) {
@@ -828,6 +865,8 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
   a.from_proj = 1;
   a.q_origin_first = origin_first != 0;
   a.rope_log2_theta = log2f(theta);
+  rc = check_partials(name, a, true);
+  if (rc != MOTIF_OK) return rc;
   return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit),
                                  (hipStream_t)stream);
 }
@@ -870,14 +909,19 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
   MOTIF_REQUIRE((long)B * k_groups * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
   MOTIF_REQUIRE(q_proj && k_proj && v_proj && k1 && k2 && v1 && v2 && y_origin && y_noise,
                 "%s: null pointer", name);
+  // kv_len <= kMfmaMaxRows: the kernel's byte offsets into a KV head's rows
+  // are 32-bit, as in the other matrix-core entry points.
   const bool ok = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
+                  (long)offset + S <= kMfmaMaxRows &&
+                  tile_softmax_scale_ok(scale * 1.4426950408889634f) &&
                   (long)S * 2 * k_groups * D * 2 < (1L << 31) && aligned(q_proj, 16) &&
                   aligned(k_proj, 16) && aligned(v_proj, 16) && aligned(k1, 16) &&
                   aligned(k2, 16) && aligned(v1, 16) && aligned(v2, 16) && aligned(y_origin, 16) &&
                   aligned(y_noise, 16);
   if (!ok) {
-    set_error("%s: no fused variant for this shape (dtype %d, D=%d); use motif_rope_split4 and "
-              "motif_sdpa_dual_v_rows", name, dtype, D);
+    set_error("%s: no fused variant for this call (dtype %d, D=%d, %d rows, scale %g); use "
+              "motif_rope_split4 and motif_sdpa_dual_v_rows", name, dtype, D, offset + S,
+              (double)scale);
     return MOTIF_ERR_UNSUPPORTED;
   }
   const int kv_len = offset + S;
@@ -903,29 +947,164 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
   a.rope_pos0 = offset;
   a.y2_row0 = (long)B * Hq_o * S;
   if (pp.nsplit > 1) {
-    if (workspace == nullptr || workspace_bytes < pp.workspace_bytes) {
-      set_error("%s: workspace of %zu bytes needed, %zu given", name, pp.workspace_bytes,
-                workspace == nullptr ? (size_t)0 : workspace_bytes);
-      return MOTIF_ERR_WORKSPACE;
-    }
-    MOTIF_REQUIRE(aligned(workspace, 256), "%s: workspace must be 256-byte aligned", name);
-    const size_t vrows = (size_t)B * (Hq_o + q_groups) * S;
-    char* w = (char*)workspace;
-    const size_t cbytes = (vrows * sizeof(unsigned) + 255) / 256 * 256;
-    const size_t obytes = (vrows * pp.nsplit * 2 * D * sizeof(float) + 255) / 256 * 256;
-    a.counters = (unsigned*)w;
-    a.part_o = (float*)(w + cbytes);
-    a.part_ml = (float*)(w + cbytes + obytes);
+    const int rc = carve_split_ws(name, a, workspace, workspace_bytes,
+                                  (size_t)B * (Hq_o + q_groups) * S, pp.nsplit, D, 0);
+    if (rc != MOTIF_OK) return rc;
   }
+  int rc = check_partials(name, a, false);
+  if (rc != MOTIF_OK) return rc;
   hipStream_t s = (hipStream_t)stream;
   const int nblocks = sdpa_grid_blocks(B * k_groups, a.nchunk, pp.nsplit);
-  int rc = dtype == MOTIF_F16 ? launch_gda_prefill_proj_f16(a, pp.waves, pp.ncb, nblocks, s)
+  rc = dtype == MOTIF_F16 ? launch_gda_prefill_proj_f16(a, pp.waves, pp.ncb, nblocks, s)
                               : launch_gda_prefill_proj_bf16(a, pp.waves, pp.ncb, nblocks, s);
   if (rc != MOTIF_OK || pp.nsplit == 1) return rc;
   // One merge over both passes' partial rows (noise rows into y_noise).
   SdpaArgs m = a;
   m.Hq = Hq_o + q_groups;
   return sdpa_merge(m, dtype, D, s);
+}
+
+// Host-only walk of every launch planner over decode, slab and prefill
+// shapes (no HIP call): each plan of more than one split must have a
+// workspace that holds its counters and partials, carving it must give the
+// kernels non-null partial buffers inside it (check_partials passes), a
+// missing workspace must be refused, and the public size query must cover
+// the plans of the routes it serves.  The no-alloc layout must keep every
+// call's partials past its fixed counter area.  Returns MOTIF_OK or
+// MOTIF_ERR_INTERNAL with the failing plan in motif_last_error().
+int motif_plan_selfcheck(void) {
+  CallScope scope;
+  clear_error();
+  char* const fake = (char*)(uintptr_t)0x10000000u;  // never dereferenced
+  auto fail = [](const char* what, int B, int Hq, int Hkv, int S_q, int kv_len, int ns) {
+    set_error("plan_selfcheck: %s (B=%d Hq=%d Hkv=%d S_q=%d kv_len=%d nsplit=%d)", what, B, Hq,
+              Hkv, S_q, kv_len, ns);
+    return MOTIF_ERR_INTERNAL;
+  };
+  // One plan: nsplit in range; split plans carve cleanly and are guarded.
+  auto check_plan = [&](const char* what, size_t vrows, int nsplit, size_t ws_bytes, int B,
+                        int Hq, int Hkv, int S_q, int kv_len, size_t reserve) -> int {
+    if (nsplit < 1 || nsplit > kMaxSplits) return fail(what, B, Hq, Hkv, S_q, kv_len, nsplit);
+    SdpaArgs a{};
+    a.nsplit = nsplit;
+    if (nsplit == 1) return MOTIF_OK;
+    const size_t need = split_ws_bytes(vrows, nsplit, 128, reserve);
+    if (reserve == 0 && ws_bytes < need) return fail(what, B, Hq, Hkv, S_q, kv_len, nsplit);
+    if (carve_split_ws(what, a, nullptr, 0, vrows, nsplit, 128, reserve) != MOTIF_ERR_WORKSPACE)
+      return fail("missing workspace accepted", B, Hq, Hkv, S_q, kv_len, nsplit);
+    if (carve_split_ws(what, a, fake, need, vrows, nsplit, 128, reserve) != MOTIF_OK ||
+        check_partials(what, a, false) != MOTIF_OK)
+      return fail(what, B, Hq, Hkv, S_q, kv_len, nsplit);
+    const char* o = (const char*)a.part_o;
+    const char* ml = (const char*)a.part_ml;
+    const size_t o_end = (size_t)(o - fake) + vrows * nsplit * 2 * 128 * sizeof(float);
+    const size_t ml_end = (size_t)(ml - fake) + vrows * nsplit * 2 * sizeof(float);
+    if ((size_t)(o - fake) < vrows * sizeof(unsigned) || (size_t)(o - fake) < reserve ||
+        o_end > (size_t)(ml - fake) || ml_end > need)
+      return fail(what, B, Hq, Hkv, S_q, kv_len, nsplit);
+    clear_error();
+    return MOTIF_OK;
+  };
+  // The guard itself refuses split plans without partial buffers.
+  {
+    SdpaArgs a{};
+    a.nsplit = 2;
+    if (check_partials("selfcheck", a, false) != MOTIF_ERR_INTERNAL)
+      return fail("guard let a split plan without partials through", 0, 0, 0, 0, 0, 2);
+    a.nsplit = 1;
+    if (check_partials("selfcheck", a, true) != MOTIF_ERR_INTERNAL)
+      return fail("guard let a fused plan without partials through", 0, 0, 0, 0, 0, 1);
+    clear_error();
+  }
+  const int heads[][2] = {{32, 8}, {40, 8}, {8, 8}, {4, 4}, {16, 4}, {64, 8}, {128, 8}};
+  const int rows_q[] = {1, 2, 5, 17, 37, 128, 512};
+  const int lens[] = {0, 1, 15, 16, 17, 300, 1024, 2047, 2048, 3204, 4096, 4097, 16000, 32768,
+                      131072};
+  constexpr int D = 128;
+  for (int B = 1; B <= 2; ++B)
+    for (const auto& h : heads)
+      for (int S_q : rows_q)
+        for (int kv_len : lens) {
+          const int Hq = h[0], Hkv = h[1];
+          if (kv_len < S_q && S_q > 1) continue;
+          const size_t vrows = (size_t)B * Hq * S_q;
+          const size_t pub = motif_sdpa_workspace_bytes(B, Hq, Hkv, S_q, kv_len, D);
+          int rc;
+          // fp kernels (VALU, 16-column matrix-core, short 4-wave decode)
+          const SdpaPlan p0 = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0);
+          const SdpaPlan p1 = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 0, 0);
+          const SdpaPlan p2 = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 4, 1);
+          for (const SdpaPlan* p : {&p0, &p1, &p2}) {
+            if (pub < p->workspace_bytes && (p != &p2 || (S_q == 1 && kv_len <= kShortDecodeRows)))
+              return fail("size query below an fp plan", B, Hq, Hkv, S_q, kv_len, p->nsplit);
+            if ((rc = check_plan("fp plan", vrows, p->nsplit, p->workspace_bytes, B, Hq, Hkv, S_q,
+                                 kv_len, 0)) != MOTIF_OK)
+              return rc;
+          }
+          if (S_q == 1 &&
+              (rc = check_plan("no-alloc plan", vrows, p1.nsplit, 0, B, Hq, Hkv, S_q, kv_len,
+                               kScratchClearBytes)) != MOTIF_OK)
+            return rc;
+          // packed-cache matrix-core kernels, every group size
+          for (int gs = 32; gs <= 128; gs *= 2) {
+            const int nb = sdpa_q_blocks(Hq / Hkv * S_q, D, gs);
+            const SdpaPlan pq = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),
+                                          kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu,
+                                          nb > 1 ? nb * sdpa_gc_max_q(D, gs) : 0);
+            if (pub < pq.workspace_bytes)
+              return fail("size query below a packed plan", B, Hq, Hkv, S_q, kv_len, pq.nsplit);
+            if ((rc = check_plan("packed plan", vrows, pq.nsplit, pq.workspace_bytes, B, Hq, Hkv,
+                                 S_q, kv_len, 0)) != MOTIF_OK)
+              return rc;
+          }
+          // shared-tile kernel (prefill chunks, long slabs)
+          if (use_shared_tiles(Hq / Hkv * S_q, kv_len)) {
+            const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
+            if (pub < pp.workspace_bytes)
+              return fail("size query below a shared-tile plan", B, Hq, Hkv, S_q, kv_len,
+                          pp.nsplit);
+            if ((rc = check_plan("shared-tile plan", vrows, pp.nsplit, pp.workspace_bytes, B, Hq,
+                                 Hkv, S_q, kv_len, 0)) != MOTIF_OK)
+              return rc;
+          }
+          // packed slab kernel
+          const int gv = Hq / Hkv * S_q;
+          if (gv >= kQSlabMinHeads && gv <= kQSlabMaxHeads) {
+            const QSlabPlan qp = plan_qslab(B, Hq, Hkv, S_q, kv_len, D);
+            if (pub < qp.workspace_bytes)
+              return fail("size query below a slab plan", B, Hq, Hkv, S_q, kv_len, qp.nsplit);
+            if ((rc = check_plan("slab plan", vrows, qp.nsplit, qp.workspace_bytes, B, Hq, Hkv,
+                                 S_q, kv_len, 0)) != MOTIF_OK)
+              return rc;
+          }
+          // a GDA layer's prefill chunk from the projections (gr = G / 4)
+          if (S_q > 1 && Hq / Hkv >= 2) {
+            const int gr = Hq / Hkv >= 4 ? 4 : 2, q_groups = Hq / gr;
+            if (q_groups % Hkv == 0) {
+              const int G_o = q_groups * gr / Hkv, G_n = q_groups / Hkv;
+              const GdaPrefillPlan gp = plan_gda_prefill(B, Hkv, G_o, G_n, S_q, kv_len);
+              const size_t gv_rows = (size_t)B * (q_groups * gr + q_groups) * S_q;
+              if ((rc = check_plan("gda prefill plan", gv_rows, gp.nsplit, gp.workspace_bytes, B,
+                                   Hq, Hkv, S_q, kv_len, 0)) != MOTIF_OK)
+                return rc;
+            }
+          }
+          // the fused decode step: partials are always published
+          if (S_q == 1 && Hq / Hkv >= 2) {
+            const int gr = Hq / Hkv - 1 > 0 ? Hq / Hkv - 1 : 1;
+            const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+            const size_t prow = (size_t)B * Hkv * (gr + 1);
+            for (const SdpaPlan* p : {&L.plan, &L.plan_q}) {
+              if (p->nsplit < 1 || p->nsplit > kMaxSplits ||
+                  L.o_bytes < prow * p->nsplit * 2 * D * sizeof(float) ||
+                  L.ml_bytes < prow * p->nsplit * 2 * sizeof(float) ||
+                  L.fused_bytes != L.counter_bytes + L.o_bytes + L.ml_bytes)
+                return fail("fused decode layout", B, Hq, Hkv, S_q, kv_len, p->nsplit);
+            }
+          }
+        }
+  clear_error();
+  return MOTIF_OK;
 }
 
 }  // extern "C"

@@ -70,7 +70,8 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
     if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16) {
       // Paired-tile kernel: 4-bit by default (qpair 1); 8-bit too with
       // qpair 2 (slower than the per-tile kernel there).
-      if (tuning().qpair >= (bits == 4 ? 1 : 2) && ng <= 2 && ((uintptr_t)a.q & 15u) == 0)
+      if (tuning().qpair >= (bits == 4 ? 1 : 2) && ng <= 2 && ((uintptr_t)a.q & 15u) == 0 &&
+          tile_softmax_scale_ok(a.qscale))
         return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
     }

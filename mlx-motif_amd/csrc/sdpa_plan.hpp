@@ -182,6 +182,17 @@ QSlabPlan plan_qslab(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
 // first row: they take kv_len <= kMfmaMaxRows (the VALU kernels take the
 // rest).
 constexpr int kMfmaMaxRows = 1 << 22;
+
+// The tile-softmax kernels (shared-tile prefill and slab kernels, the packed
+// slab kernel, the paired-tile q4 kernel and the fused prefill chunk) take
+// each tile's running maximum over the unscaled scores and scale it after,
+// which is the maximum of the scaled scores only for a positive, finite
+// scale.  Calls with any other scale (the reference accepts every float)
+// take the per-tile kernels, which scale every score before the maximum.
+// qscale is the softmax scale times log2(e).
+inline bool tile_softmax_scale_ok(float qscale) {
+  return qscale > 0.f && qscale <= 3.4028234663852886e38f;
+}
 // Single-row fp16/bf16 decode calls over at most this many rows run 4-wave
 // workgroups, one per CU, instead of 8-wave ones: with few rows per split
 // the smaller blocks reach their first tile sooner (32 q-heads over 8 KV

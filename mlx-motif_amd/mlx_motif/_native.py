@@ -23,6 +23,7 @@ MOTIF_ERR_CONTRACT = -1
 MOTIF_ERR_UNSUPPORTED = -2
 MOTIF_ERR_WORKSPACE = -3
 MOTIF_ERR_HIP = -4
+MOTIF_ERR_INTERNAL = -5
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 
@@ -38,6 +39,7 @@ _SIGNATURES = {
     "motif_abi_version": (_c_int, []),
     "motif_last_error": (ctypes.c_char_p, []),
     "motif_sdpa_counter_bytes": (_c_sz, [_c_int] * 4),
+    "motif_plan_selfcheck": (_c_int, []),
     "motif_sdpa_workspace_bytes": (_c_sz, [_c_int] * 6),
     "motif_sdpa_dual_v": (
         _c_int,

@@ -224,3 +224,17 @@ def test_prefill_planner_choices_through_workspace_sizes():
     finally:
         _native.set_tuning("prefill_ncb", 0)
     assert lib.motif_sdpa_workspace_bytes(1, 32, 8, 512, 3716, 128) >= parts(32 * 512, 4)
+
+
+def test_plan_selfcheck():
+    """Every launch planner, walked on the host over decode, slab and prefill
+    shapes: split plans get counters and partials inside their workspace,
+    the pre-launch guard refuses a split plan without partial buffers (the
+    fault class of a one-split slab staging partials through a null base),
+    a missing workspace is refused, and the size query covers every plan.
+    The no-alloc layout keeps partials past its fixed counter area."""
+    from mlx_motif import _native
+
+    lib = _native.lib()
+    rc = lib.motif_plan_selfcheck()
+    assert rc == _native.MOTIF_OK, lib.motif_last_error().decode()

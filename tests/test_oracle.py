@@ -410,3 +410,21 @@ def test_gda_prefill_from_proj_per_head_loop(rng):
             qrows = qr[b, :, h * (gr + 1) + gr]
             np.testing.assert_allclose(y_n[b, h], att(qrows, 1, h // G_n, b), rtol=1e-12,
                                        atol=1e-12)
+
+
+def test_vectorised_c_port_matches_scalar_build():
+    """The -O3 -ffast-math build of the C port (timed by bench.py's CPU
+    baseline only) computes what the scalar checker build computes, to
+    fp32 reassociation error."""
+    from oracle import c_oracle
+
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((1, 8, 1, 128)).astype(np.float16)
+    k, v1, v2 = (rng.standard_normal((1, 2, 700, 128)).astype(np.float16) for _ in range(3))
+    a = c_oracle.sdpa_dual_v_f16(q, k, v1, v2, 128 ** -0.5, 650)
+    b = c_oracle.sdpa_dual_v_f16(q, k, v1, v2, 128 ** -0.5, 650, fast=True)
+    assert np.max(np.abs(a - b)) <= 1e-5
+    trips = [c_oracle.quantize_f16(t, 64, 4) for t in (k, v1, v2)]
+    a = c_oracle.sdpa_dual_v_q_f16(q, *trips, 128 ** -0.5, 64, 4, 650)
+    b = c_oracle.sdpa_dual_v_q_f16(q, *trips, 128 ** -0.5, 64, 4, 650, fast=True)
+    assert np.max(np.abs(a - b)) <= 1e-5

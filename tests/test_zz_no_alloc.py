@@ -77,3 +77,24 @@ def test_noalloc_bf16_and_small_shapes(gpu):
                                           (3, 32, 8, 4096, 4096, 5)):
         y_ws, y_na = _call_both(gpu, torch.bfloat16, B, Hq, Hkv, cap, kv_len, seed)
         assert torch.equal(_bits(y_ws), _bits(y_na)), (B, Hq, kv_len)
+
+
+def test_noalloc_counters_survive_a_small_call(gpu):
+    """In-kernel merge (its arrival counters live in the scratch): a call with
+    few rows, then a split call with more than 64 (b, KV head) units.  The
+    first call's partials must not land on the counters the second one uses,
+    or the second call's last workgroups never see their final ticket and
+    leave rows unwritten."""
+    import torch
+
+    from mlx_motif import _native
+
+    _native.set_tuning("fused_merge", 1)
+    try:
+        for B, Hq, Hkv, cap, kv_len, seed in ((1, 32, 8, 16128, 16000, 6),
+                                              (4, 32, 32, 3072, 3000, 7),
+                                              (1, 32, 8, 16128, 16000, 8)):
+            y_ws, y_na = _call_both(gpu, torch.float16, B, Hq, Hkv, cap, kv_len, seed)
+            assert torch.equal(_bits(y_ws), _bits(y_na)), (B, Hq, Hkv, kv_len)
+    finally:
+        _native.set_tuning("fused_merge", 0)
