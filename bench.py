@@ -288,21 +288,24 @@ def decode_bytes(kv_len: int, fused: bool, gr: int = 4, bits=None) -> int:
     return streams * B * HKV * kv_len * row + heads * D * 2 + HKV * gr * 2 * D * 2
 
 
-def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1):
+def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=HKV, s_q=1,
+                 bf16=False):
+    """Packed-cache calls (``bf16``: bf16 activations, scales and biases)."""
     from mlx_motif import _native
     from mlx_motif.kernels import quantize
 
+    dt, code = (torch.bfloat16, 1) if bf16 else (torch.float16, 0)
     g = torch.Generator(device=dev)
     g.manual_seed(4321 + bits)
-    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).half()
+    q = torch.randn((B, hq, s_q, D), generator=g, device=dev).to(dt)
     sets = []
     for _ in range(nsets):
         trips = []
         for _ in range(3):
-            x = torch.randn((B, hkv, cap, D), generator=g, device=dev).half()
+            x = torch.randn((B, hkv, cap, D), generator=g, device=dev).to(dt)
             trips.append(quantize(x, group_size=GS, bits=bits))
             del x
-        sets.append((trips, torch.empty((B, hq, s_q, 2 * D), dtype=torch.float16, device=dev)))
+        sets.append((trips, torch.empty((B, hq, s_q, 2 * D), dtype=dt, device=dev)))
     nbytes = lib.motif_sdpa_workspace_bytes(B, hq, hkv, s_q, kv_len, D)
     ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
     scale = 1.0 / D ** 0.5
@@ -313,11 +316,11 @@ def make_q_calls(torch, lib, dev, nsets, bits, kv_len=KV_LEN, cap=CAP, hq=HQ, hk
         def call():
             stream = torch.cuda.current_stream().cuda_stream
             if s_q == 1:
-                st = lib.motif_sdpa_dual_v_q(q.data_ptr(), *ptrs, y.data_ptr(), 0, B, hq, hkv, D,
-                                             cap, kv_len, bits, GS, scale, ws.data_ptr(),
+                st = lib.motif_sdpa_dual_v_q(q.data_ptr(), *ptrs, y.data_ptr(), code, B, hq, hkv,
+                                             D, cap, kv_len, bits, GS, scale, ws.data_ptr(),
                                              ws.numel(), stream)
             else:
-                st = lib.motif_sdpa_dual_v_q_rows(q.data_ptr(), *ptrs, y.data_ptr(), 0, B, hq,
+                st = lib.motif_sdpa_dual_v_q_rows(q.data_ptr(), *ptrs, y.data_ptr(), code, B, hq,
                                                   hkv, s_q, D, cap, kv_len, 1, bits, GS, scale,
                                                   ws.data_ptr(), ws.numel(), stream)
             _native.check(st)
@@ -701,6 +704,12 @@ def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
     calls, keep = make_decode_calls(torch, lib, dev, 6, fused=True)
     hbm("gda_decode_step_f16_kv16000", timed(calls), decode_bytes(KV_LEN, True))
     del calls, keep
+    # the packed 16k decode with bf16 activations, scales and biases
+    for bits, nsets in ((4, 24), (8, 16)):
+        calls, keep = make_q_calls(torch, lib, dev, nsets, bits, bf16=True)
+        hbm(f"sdpa_dual_v_q{bits}_bf16_kv16000", timed(calls), alg_bytes(f"q{bits}"))
+        del calls, keep
+        torch.cuda.empty_cache()
     # the fused epilogues at prefill length 3204
     g7 = torch.Generator(device=dev)
     g7.manual_seed(7)

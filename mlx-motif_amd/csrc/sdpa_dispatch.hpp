@@ -19,11 +19,17 @@ int dispatch_sdpa_q_f16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, h
 int dispatch_sdpa_q_bf16(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, hipStream_t s);
 
-// Packed cache, fp16 scales, head_dim 128, group size 64 or 128: the
-// paired-tile matrix-core kernel (sdpa_qpair.hip).  gc heads per workgroup
-// with gc * 128 / gs <= 16, waves 4 or 8.
+// Packed cache, head_dim 128, group size 64 or 128, fp16 (or, with bf16,
+// bf16) activations, scales and biases: the paired-tile matrix-core kernel
+// (sdpa_qpair.hip).  gc heads per workgroup with gc * 128 / gs <= 16, waves 4
+// or 8.
 int launch_sdpa_qpair(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
-                      hipStream_t s);
+                      hipStream_t s, bool bf16 = false);
+
+// The paired-tile kernel takes this bf16 call: head_dim 128, group size 64
+// or 128, the pointer alignment and row bounds of the matrix-core kernels,
+// and a scale its tile softmax handles.
+bool qpair_bf16_ok(const SdpaArgs& a, int D, int gs);
 
 // Packed cache (fp16 scales, head dim 128), a verify slab of 17..64 virtual
 // heads per KV head: tiles dequantised once per workgroup into LDS

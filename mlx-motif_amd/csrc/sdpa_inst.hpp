@@ -76,6 +76,12 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
     }
   }
+  if constexpr (std::is_same<MOTIF_ELEM, bf16_t>::value) {
+    // bf16 activations: the paired-tile kernel for 4- and 8-bit caches
+    // (sdpa_q_run planned it: 4-wave workgroups, one per CU).
+    if (qpair_bf16_ok(a, D, a.group_size) && p.gc * (D / a.group_size) <= 16)
+      return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s, true);
+  }
   if (bits == 4) {
     switch (D) {
       case 32: return launch_sdpa_gc<QFmt<MOTIF_ELEM, 32, 4>>(a, p.gc, p.waves, nblocks, s);

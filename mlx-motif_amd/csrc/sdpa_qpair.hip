@@ -8,13 +8,21 @@
 namespace motif {
 
 int launch_sdpa_qpair(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
-                      hipStream_t st) {
-  if (bits == 4) {
-    if (gs == 64) return launch_sdpa_qpair_gs<4, 64>(a, gc, waves, nblocks, st);
-    if (gs == 128) return launch_sdpa_qpair_gs<4, 128>(a, gc, waves, nblocks, st);
+                      hipStream_t st, bool bf16) {
+  if (bf16) {
+    if (bits == 4) {
+      if (gs == 64) return launch_sdpa_qpair_gs<4, 64, bf16_t>(a, gc, waves, nblocks, st);
+      if (gs == 128) return launch_sdpa_qpair_gs<4, 128, bf16_t>(a, gc, waves, nblocks, st);
+    } else {
+      if (gs == 64) return launch_sdpa_qpair_gs<8, 64, bf16_t>(a, gc, waves, nblocks, st);
+      if (gs == 128) return launch_sdpa_qpair_gs<8, 128, bf16_t>(a, gc, waves, nblocks, st);
+    }
+  } else if (bits == 4) {
+    if (gs == 64) return launch_sdpa_qpair_gs<4, 64, half_t>(a, gc, waves, nblocks, st);
+    if (gs == 128) return launch_sdpa_qpair_gs<4, 128, half_t>(a, gc, waves, nblocks, st);
   } else {
-    if (gs == 64) return launch_sdpa_qpair_gs<8, 64>(a, gc, waves, nblocks, st);
-    if (gs == 128) return launch_sdpa_qpair_gs<8, 128>(a, gc, waves, nblocks, st);
+    if (gs == 64) return launch_sdpa_qpair_gs<8, 64, half_t>(a, gc, waves, nblocks, st);
+    if (gs == 128) return launch_sdpa_qpair_gs<8, 128, half_t>(a, gc, waves, nblocks, st);
   }
   set_error("sdpa_dual_v_q: no paired MFMA variant for group size %d", gs);
   return MOTIF_ERR_UNSUPPORTED;

@@ -30,6 +30,13 @@
 // exp2 of fma(t, qscale', -m); rows past a column's limit are masked only
 // in the pair that crosses it.  The workgroup epilogue is shared with the
 // other split-KV kernels.
+//
+// bf16 activations (T = bf16_t: q, scales, biases and y in bf16) run the same
+// fp16 matrix-core products: q is converted to fp16 once per workgroup after
+// a power-of-two scaling per head that keeps its largest element below 2^15
+// (exact; the factor is folded into that head's softmax scale), the V scales
+// are converted to fp16 as they are staged in LDS (exact in fp16's normal
+// range), and the K scale and both bias terms are taken in fp32.
 #pragma once
 
 #include "sdpa_mfma_q.hpp"
@@ -87,9 +94,25 @@ struct QPair {
 // Packed cache, head_dim 128, fp16 scales; heads x groups <= 16 columns.
 // GC heads per workgroup (column n = NG*h + g), NW waves, POL cache policy
 // (cached when several head chunks read the same rows).
-template <int BITS, int GS, int GC, int NW, int POL = kCachePolicyStream>
+template <typename T>
+__device__ inline float pair_lo_f32(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w << 16);
+  return (float)as_h2(w).x;
+}
+template <typename T>
+__device__ inline float pair_hi_f32(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w & 0xFFFF0000u);
+  return (float)as_h2(w).y;
+}
+// Two floats as an fp16 pair (round to nearest even).
+__device__ inline uint32_t f16_pair(float lo, float hi) {
+  return h2_bits(half2_t{(_Float16)lo, (_Float16)hi});
+}
+
+template <int BITS, int GS, int GC, int NW, int POL = kCachePolicyStream, typename E = half_t>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 sdpa_qpair_kernel(SdpaArgs a) {
+  constexpr bool kBf16 = std::is_same<E, bf16_t>::value;
   constexpr int D = 128;
   constexpr int NG = D / GS;
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
@@ -191,6 +214,7 @@ sdpa_qpair_kernel(SdpaArgs a) {
   load_pair(P0, 0);  // issued before q, so their latencies overlap
   half8_t qb[4];
   float qs;
+  int q_exp = 0;  // bf16: this head's q was scaled by 2^-q_exp
   {
     const bool mine = used && (32 * blk) / GS == g;
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (used ? hh : 0)) * D + 32 * blk;
@@ -199,6 +223,22 @@ sdpa_qpair_kernel(SdpaArgs a) {
     for (int i = 0; i < 4; ++i) {
       const uint4 x = *reinterpret_cast<const uint4*>(qp + 8 * i);
       raw[4 * i] = x.x; raw[4 * i + 1] = x.y; raw[4 * i + 2] = x.z; raw[4 * i + 3] = x.w;
+    }
+    if constexpr (kBf16) {
+      // Head scale 2^-e with e the smallest >= 0 that brings the head's
+      // largest |q| below 2^15 (the four lanes of a column hold the head's
+      // 128 channels), then q * 2^-e as fp16 pairs.
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        mx = fmaxf(mx, fmaxf(fabsf(pair_lo_f32<E>(raw[i])), fabsf(pair_hi_f32<E>(raw[i]))));
+      mx = rows4_max(mx);
+      const int ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFFu) - 127;
+      q_exp = ex > 14 ? ex - 14 : 0;  // 0 for zero, subnormal and small heads
+      const float f = __builtin_bit_cast(float, (uint32_t)(127 - q_exp) << 23);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        raw[i] = f16_pair(pair_lo_f32<E>(raw[i]) * f, pair_hi_f32<E>(raw[i]) * f);
     }
     float sum = 0.f;
     const half2_t one2 = half2_t{(_Float16)1.f, (_Float16)1.f};
@@ -221,7 +261,8 @@ sdpa_qpair_kernel(SdpaArgs a) {
       qb[s] = __builtin_bit_cast(half8_t, make_uint4(w[0], w[1], w[2], w[3]));
     }
   }
-  const float qscale = a.qscale * 0x1p24f;  // scores are sums of q * u * 2^-24
+  // Scores are sums of q * u * 2^-24 (times 2^-q_exp for a scaled bf16 head).
+  const float qscale = a.qscale * 0x1p24f * __builtin_bit_cast(float, (uint32_t)(127 + q_exp) << 23);
 
   floatx4 acc1[8], acc2[8], accl;
 #pragma unroll
@@ -268,6 +309,9 @@ sdpa_qpair_kernel(SdpaArgs a) {
           const int row = r0 + 2 * lane;
           w = row + 1 < max_lim ? w : (row < max_lim ? (w & 0xFFFFu) : 0u);
         }
+        if constexpr (kBf16) {  // V scales as fp16 pairs for the weight products
+          if (t == 2 || t == 4) w = f16_pair(pair_lo_f32<E>(w), pair_hi_f32<E>(w));
+        }
         sbuf[t * SWT + lane] = w;
       }
     }
@@ -307,10 +351,10 @@ sdpa_qpair_kernel(SdpaArgs a) {
       uint32_t sk[2], sb[2];
       scales(sk, 0, T, k);
       scales(sb, 1, T, k);
-      const half2_t k01 = as_h2(sk[0]), k23 = as_h2(sk[1]);
-      const half2_t b01 = as_h2(sb[0]), b23 = as_h2(sb[1]);
-      const float skr[4] = {(float)k01.x, (float)k01.y, (float)k23.x, (float)k23.y};
-      const float bkr[4] = {(float)b01.x, (float)b01.y, (float)b23.x, (float)b23.y};
+      const float skr[4] = {pair_lo_f32<E>(sk[0]), pair_hi_f32<E>(sk[0]), pair_lo_f32<E>(sk[1]),
+                            pair_hi_f32<E>(sk[1])};
+      const float bkr[4] = {pair_lo_f32<E>(sb[0]), pair_hi_f32<E>(sb[0]), pair_lo_f32<E>(sb[1]),
+                            pair_hi_f32<E>(sb[1])};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float tt = BITS == 4 ? fmaf(t_hi[r], 0.0625f, t_lo[r]) : t_lo[r];
@@ -375,8 +419,14 @@ sdpa_qpair_kernel(SdpaArgs a) {
         const half2_t p = as_h2(pw[2 * T + h]);
         w1[2 * T + h] = h2_bits(p * as_h2(s1[h]));
         w2[2 * T + h] = h2_bits(p * as_h2(s2[h]));
-        beta1 = __builtin_amdgcn_fdot2(p, as_h2(c1[h]), beta1, false);
-        beta2 = __builtin_amdgcn_fdot2(p, as_h2(c2[h]), beta2, false);
+        if constexpr (kBf16) {  // bf16 biases: fp32 products of the same fp16 weights
+          const float p0 = (float)p.x, p1 = (float)p.y;
+          beta1 = fmaf(p1, pair_hi_f32<E>(c1[h]), fmaf(p0, pair_lo_f32<E>(c1[h]), beta1));
+          beta2 = fmaf(p1, pair_hi_f32<E>(c2[h]), fmaf(p0, pair_lo_f32<E>(c2[h]), beta2));
+        } else {
+          beta1 = __builtin_amdgcn_fdot2(p, as_h2(c1[h]), beta1, false);
+          beta2 = __builtin_amdgcn_fdot2(p, as_h2(c2[h]), beta2, false);
+        }
       }
     }
     const half8_t W1 = __builtin_bit_cast(half8_t, make_uint4(w1[0], w1[1], w1[2], w1[3]));
@@ -462,35 +512,37 @@ sdpa_qpair_kernel(SdpaArgs a) {
     lds_l[wave][hh] = accl[0];
   }
   __syncthreads();
-  wg_epilogue<half_t, D, GC, NW, false, true>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
+  wg_epilogue<E, D, GC, NW, false, true>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
-// Heads per workgroup gc (a power of two, gc * 128 / gs <= 16), waves 4 or 8.
-template <int BITS, int GS>
+// Heads per workgroup gc (a power of two, gc * 128 / gs <= 16), waves 4 or 8;
+// E: element type of q, scales, biases and y (half_t or bf16_t).
+template <int BITS, int GS, typename E>
 int launch_sdpa_qpair_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;
   constexpr int GCM = 16 / NG < 8 ? 16 / NG : 8;
+  constexpr int S = kCachePolicyStream;
   if (a.nchunk > 1 && gc == GCM && waves == 4) {
-    hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, GCM, 4, 0>), dim3(nblocks), dim3(256), 0, st,
-                       a);
+    hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, GCM, 4, 0, E>), dim3(nblocks), dim3(256), 0,
+                       st, a);
     return check_launch("sdpa_dual_v_q (pairs, chunks)");
   }
   switch (gc) {
     case 1:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 1, 8>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 1, 4>), dim3(nblocks), dim3(256), 0, st, a);
+      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 1, 8, S, E>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 1, 4, S, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 2:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 2, 8>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 2, 4>), dim3(nblocks), dim3(256), 0, st, a);
+      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 2, 8, S, E>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 2, 4, S, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 4:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 4, 8>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 4, 4>), dim3(nblocks), dim3(256), 0, st, a);
+      if (waves == 8) hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 4, 8, S, E>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 4, 4, S, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 8:
       if constexpr (8 * NG <= 16) {
-        hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 8, 4>), dim3(nblocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((sdpa_qpair_kernel<BITS, GS, 8, 4, S, E>), dim3(nblocks), dim3(256), 0, st, a);
         break;
       }
       [[fallthrough]];

@@ -285,3 +285,60 @@ def test_paired_kernel_agrees_with_per_tile(gpu, Hq, Hkv, cap, kv_len, gs, bits)
         ys.append(torch_to_np(y))
     assert max(errs) <= 2e-3, errs
     assert np.max(np.abs(ys[0] - ys[1])) <= 2e-3
+
+
+# bf16 activations, scales and biases: the paired-tile kernel (fp16 matrix-
+# core products after an exact per-head power-of-two scaling of q) against
+# the VALU kernel on the same inputs, both within the bf16 bar of the oracle
+# and of each other.  Reference: the kernel tests of sdpa_dual_v_q4 run bf16
+# (tests/test_kernels_sdpa_dual_v_q4.py:34).
+@pytest.mark.parametrize("Hq,Hkv,cap,kv_len", [
+    (32, 8, 64, 1), (32, 8, 64, 17), (32, 8, 128, 100), (8, 8, 1024, 1000),
+    (64, 8, 4096, 3001), (16, 4, 512, 511), (40, 8, 1024, 1024), (32, 8, 16128, 16000),
+])
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_bf16_paired_kernel_agrees_with_valu(gpu, Hq, Hkv, cap, kv_len, gs, bits):
+    from mlx_motif import _native
+
+    errs, ys = [], []
+    for mfma in (1, 0):
+        _native.set_tuning("mfma", mfma)
+        try:
+            print(f"bf16 mfma={mfma} Hq={Hq} kv_len={kv_len} gs={gs} bits={bits}", flush=True)
+            err, y, _ = _run(gpu, np.random.default_rng(13), 1, Hq, Hkv, cap, kv_len, 128, bits,
+                             gs, "bf16", poison=True)
+        finally:
+            _native.set_tuning("mfma", 1)
+        assert np.isfinite(torch_to_np(y)).all()
+        errs.append(err)
+        ys.append(torch_to_np(y))
+    assert max(errs) <= TOL["bf16"], errs
+    assert np.max(np.abs(ys[0] - ys[1])) <= TOL["bf16"]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_bf16_q_beyond_fp16_range(gpu, rng, bits):
+    """bf16 queries far outside fp16's range (|q| up to ~1e6) and far below
+    it (~1e-6): the per-head power-of-two scaling keeps the fp16 products
+    finite and exact in the large heads, and the small heads' scores stay
+    within the bar (a near-uniform softmax)."""
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v_q4
+
+    B, Hq, Hkv, D, cap, kv_len, gs = 1, 32, 8, 128, 2048, 2000, 64
+    q = randn(rng, (B, Hq, 1, D), "bf16")
+    q[:, 0:4] *= 3e5
+    q[:, 4:8] *= 1e-6
+    q = O.round_to(q, "bf16").astype(np.float32)
+    k, v1, v2 = (randn(rng, (B, Hkv, cap, D), "bf16") for _ in range(3))
+    kq, v1q, v2q = (_quant(t, gs, bits, "bf16") for t in (k, v1, v2))
+    scale = 1.0 / np.sqrt(D)
+    y = sdpa_dual_v_q4(np_to_torch(q, torch.bfloat16, gpu), _to_gpu(kq, "bf16", gpu),
+                       _to_gpu(v1q, "bf16", gpu), _to_gpu(v2q, "bf16", gpu), scale,
+                       group_size=gs, bits=bits, kv_len=kv_len)
+    ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, scale, gs, bits, kv_len)
+    got = torch_to_np(y)
+    assert np.isfinite(got).all()
+    assert np.max(np.abs(got - ref)) <= TOL["bf16"], np.max(np.abs(got - ref))
