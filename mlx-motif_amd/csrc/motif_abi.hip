@@ -379,6 +379,12 @@ int motif_set_tuning(const char* key, int value) {
       return MOTIF_ERR_CONTRACT;
     }
     update_tuning([&](Tuning& t) { t.merge_rows = value; });
+  } else if (!strcmp(key, "part_f16")) {
+    if (value < 0 || value > 1) {
+      set_error("motif_set_tuning: part_f16 must be 0 or 1");
+      return MOTIF_ERR_CONTRACT;
+    }
+    update_tuning([&](Tuning& t) { t.part_f16 = value; });
   } else if (!strcmp(key, "qslab_sets")) {
     if (value < 2 || value > 3) {
       set_error("motif_set_tuning: qslab_sets must be 2 or 3");

@@ -176,6 +176,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
                           counter_reserve);
       if (rc != MOTIF_OK) return rc;
     }
+    a.part_f16 = use_part_f16((long)B * Hq * S_q, pp.nsplit) ? 1 : 0;
     rc = check_partials(name, a, false);
     if (rc != MOTIF_OK) return rc;
     const int nblocks = sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit);
@@ -974,6 +975,7 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
                                   (size_t)B * (Hq_o + q_groups) * S, pp.nsplit, D, 0);
     if (rc != MOTIF_OK) return rc;
   }
+  a.part_f16 = use_part_f16((long)B * (Hq_o + q_groups) * S, pp.nsplit) ? 1 : 0;
   int rc = check_partials(name, a, false);
   if (rc != MOTIF_OK) return rc;
   hipStream_t s = (hipStream_t)stream;

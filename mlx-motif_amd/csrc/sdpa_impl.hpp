@@ -28,6 +28,21 @@ namespace motif {
 
 constexpr float kNegSentinel = -1e30f;
 
+// Four floats as fp16 (round to nearest even), packed in two words, and back.
+__device__ inline uint2 half4_bits(float4 v) {
+  return make_uint2(
+      (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.x) |
+          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.y) << 16),
+      (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.z) |
+          ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.w) << 16));
+}
+__device__ inline float4 half4_floats(uint2 w) {
+  return make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(w.x & 0xFFFFu)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(w.x >> 16)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y & 0xFFFFu)),
+                     (float)__builtin_bit_cast(_Float16, (uint16_t)(w.y >> 16)));
+}
+
 // Cross-workgroup hand-off of split partials without whole-cache maintenance.
 // Partials are stored and re-loaded through raw buffer operations with the
 // sc0|sc1 cache policy: stores are written through the XCD's L2 to memory,
@@ -573,17 +588,16 @@ __global__ void __launch_bounds__(64) sdpa_merge_kernel(SdpaArgs a) {
 // every load of a batch issued before any is consumed, and the running
 // maximum rescales earlier batches.  With at most 8 splits the result is
 // sum_s o_s * exp2(m_s - M) in split order, M the largest m_s.
-constexpr int kMergeRowsMin = 2048;  // rows from which the row-per-wave merge runs
-template <typename T, int D>
-__global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long rows) {
+// F16: the partials are fp16 o / l (SdpaArgs::part_f16); split s then weighs
+// l_s * exp2(m_s - M) instead of exp2(m_s - M).
+template <typename T, int D, bool F16>
+__device__ inline void merge_rows(const SdpaArgs& a, long vrow, int lane) {
   constexpr int C4 = 2 * D / 4;
   constexpr int CPL = (C4 + 63) / 64;  // float4 columns per lane
   constexpr int NB = 8;                // splits per batch
-  const int lane = threadIdx.x & 63;
-  const long vrow = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (vrow >= rows) return;
   const int ns = a.nsplit;
   const float4* po = reinterpret_cast<const float4*>(a.part_o + vrow * ns * 2 * D);
+  const uint2* ph = reinterpret_cast<const uint2*>((const uint16_t*)a.part_o + vrow * ns * 2 * D);
   const float2* pml = reinterpret_cast<const float2*>(a.part_ml + vrow * ns * 2);
   float4 acc[CPL];
 #pragma unroll
@@ -599,7 +613,11 @@ __global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long r
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
         const int c = lane + 64 * k;
-        v[j][k] = s < ns && c < C4 ? po[(long)s * C4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool in = s < ns && c < C4;
+        if constexpr (F16)
+          v[j][k] = in ? half4_floats(ph[(long)s * C4 + c]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        else
+          v[j][k] = in ? po[(long)s * C4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
     float Mb = M;
@@ -619,8 +637,9 @@ __global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long r
     M = Mb;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const float f = fast_exp2(ml[j].x - M);  // 0 for splits past ns (sentinel m)
-      L = fmaf(ml[j].y, f, L);
+      const float e = fast_exp2(ml[j].x - M);  // 0 for splits past ns (sentinel m)
+      L = fmaf(ml[j].y, e, L);
+      const float f = F16 ? ml[j].y * e : e;
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
         acc[k].x = fmaf(v[j][k].x, f, acc[k].x);
@@ -642,11 +661,28 @@ __global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long r
 }
 
 template <typename T, int D>
+__global__ void __launch_bounds__(256) sdpa_merge_rows_kernel(SdpaArgs a, long rows) {
+  const int lane = threadIdx.x & 63;
+  const long vrow = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (vrow >= rows) return;
+  if (a.part_f16)
+    merge_rows<T, D, true>(a, vrow, lane);
+  else
+    merge_rows<T, D, false>(a, vrow, lane);
+}
+
+// The merge launch takes the row-per-wave kernel for this call (many partial
+// rows, or fp16 partials, which only that kernel reads).
+inline bool merge_uses_rows_kernel(const SdpaArgs& a) {
+  return a.part_f16 || ((long)a.B * a.Hq * a.S_q >= kMergeRowsMin && tuning().merge_rows);
+}
+
+template <typename T, int D>
 int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
   constexpr int C4 = 2 * D / 4;
   constexpr int NSL = C4 / (C4 < 16 ? C4 : 16);
   const long rows = (long)a.B * a.Hq * a.S_q;
-  if (rows >= kMergeRowsMin && tuning().merge_rows) {
+  if (merge_uses_rows_kernel(a)) {
     hipLaunchKernelGGL((sdpa_merge_rows_kernel<T, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256),
                        0, s, a, rows);
     return check_launch("sdpa split merge (rows)");

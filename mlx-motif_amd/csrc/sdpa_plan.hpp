@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "motif_common.hpp"
+
 namespace motif {
 
 // Everything a split-KV launch needs, shared by every cache format.
@@ -41,6 +43,10 @@ struct SdpaArgs {
   int nsplit, rows_per_split;
   int group_size;
   int fused_merge;  // 1: last-arriving workgroup merges; 0: sdpa_merge_kernel does
+  // Split partial outputs stored as fp16 o / l (the shared-tile kernels of
+  // prefill chunks, whose partials the row-per-wave merge reads) instead of
+  // fp32 o: half the bytes written and read back.
+  int part_f16;
   float qscale;     // softmax scale * log2(e)
   // Fused GDA decode step (origin and noise passes in one launch, then the
   // merge applies gda_post_split): q holds the origin queries (B, Hq, 1, D)
@@ -182,6 +188,15 @@ QSlabPlan plan_qslab(int B, int Hq, int Hkv, int S_q, int kv_len, int D);
 // first row: they take kv_len <= kMfmaMaxRows (the VALU kernels take the
 // rest).
 constexpr int kMfmaMaxRows = 1 << 22;
+
+// Partial rows (B * Hq * S_q) from which a split call's merge launch runs one
+// wave per row (tuning merge_rows) instead of one wave per row slice.
+constexpr int kMergeRowsMin = 2048;
+// The shared-tile kernels store split partials as fp16 o / l (SdpaArgs::
+// part_f16) when the row-per-wave merge will read them.
+inline bool use_part_f16(long rows, int nsplit) {
+  return nsplit > 1 && rows >= kMergeRowsMin && tuning().merge_rows && tuning().part_f16;
+}
 
 // The tile-softmax kernels (shared-tile prefill and slab kernels, the packed
 // slab kernel, the paired-tile q4 kernel and the fused prefill chunk) take

@@ -225,11 +225,13 @@ struct SwizzledTileAcc {
 
   // Column vrow's result: y (normalised, nsplit == 1) or its split partial.
   __device__ __forceinline__ void store(const SdpaArgs& a, long vrow, int split, int blk) const {
-    store_to(a.y, vrow, a.part_o, a.part_ml, vrow, a.nsplit, split, blk);
+    store_to(a.y, vrow, a.part_o, a.part_ml, vrow, a.nsplit, split, blk, a.part_f16);
   }
-  // The same into row yrow of y (nsplit == 1) or partial row prow.
+  // The same into row yrow of y (nsplit == 1) or partial row prow (fp32 o,
+  // or fp16 o / l with f16).
   __device__ __forceinline__ void store_to(void* y, long yrow, float* part_o, float* part_ml,
-                                           long prow, int nsplit, int split, int blk) const {
+                                           long prow, int nsplit, int split, int blk,
+                                           bool f16) const {
     constexpr int D = 128;
     const float l = accl[0];
     if (nsplit == 1) {
@@ -250,6 +252,19 @@ struct SwizzledTileAcc {
         *reinterpret_cast<uint4*>(yp + 8 * p) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
         *reinterpret_cast<uint4*>(yp + D + 8 * p) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
       }
+    } else if (f16) {
+      const int ns = nsplit;
+      const float inv = l == 0.f ? 0.f : 1.f / l;
+      uint16_t* po = (uint16_t*)part_o + (prow * ns + split) * 2 * D + 32 * blk;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        *reinterpret_cast<uint2*>(po + 4 * j) = half4_bits(
+            make_float4(acc1[j][0] * inv, acc1[j][1] * inv, acc1[j][2] * inv, acc1[j][3] * inv));
+        *reinterpret_cast<uint2*>(po + D + 4 * j) = half4_bits(
+            make_float4(acc2[j][0] * inv, acc2[j][1] * inv, acc2[j][2] * inv, acc2[j][3] * inv));
+      }
+      if (blk == 0)
+        *reinterpret_cast<float2*>(part_ml + (prow * ns + split) * 2) = make_float2(m_run, l);
     } else {
       const int ns = nsplit;
       float* po = part_o + (prow * ns + split) * 2 * D + 32 * blk;
@@ -269,19 +284,24 @@ struct SwizzledTileAcc {
 // Split partials of a wave's 16 columns staged through LDS: lane (col, blk)
 // holds channels 32*blk + 4*j .. +3 of its column, so direct stores write
 // 16-byte pieces of 16 rows per instruction; staged, each store instruction
-// writes two whole 512-byte halves of partial rows.  lds: this wave's 16
-// rows of 132 floats (16 bytes of padding per row put the 16 columns' writes
-// in distinct bank groups).  Column c's partial row is prow0 + c, stored for
-// c < ncols.
+// writes two whole 512-byte halves of partial rows (f16: fp16 o / l, two
+// 256-byte halves).  lds: this wave's 16 rows of 132 floats (16 bytes of
+// padding per row put the 16 columns' writes in distinct bank groups; with
+// f16 the padding's first float carries the column's 1 / l).  Column c's
+// partial row is prow0 + c, stored for c < ncols.
 constexpr int kStageRowFloats = 132;
 constexpr int kStageWaveBytes = 16 * kStageRowFloats * 4;
 template <typename T>
 __device__ __forceinline__ void store_partials_staged(const SwizzledTileAcc<T>& acc, float* lds,
                                                       float* part_o, float* part_ml, long prow0,
                                                       int ncols, int nsplit, int split, int col,
-                                                      int blk) {
+                                                      int blk, bool f16 = false) {
   constexpr int D = 128;
   const int lane = col + 16 * blk;
+  if (f16 && blk == 0) {
+    const float l = acc.accl[0];
+    lds[col * kStageRowFloats + 128] = l == 0.f ? 0.f : 1.f / l;
+  }
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     const floatx4* src = half ? acc.acc2 : acc.acc1;
@@ -295,9 +315,15 @@ __device__ __forceinline__ void store_partials_staged(const SwizzledTileAcc<T>& 
       const int row = 2 * i + (lane >> 5);
       const int q = lane & 31;
       const float4 v = *reinterpret_cast<const float4*>(lds + row * kStageRowFloats + 4 * q);
-      if (row < ncols)
-        *reinterpret_cast<float4*>(part_o + ((prow0 + row) * nsplit + split) * 2 * D + half * D +
-                                   4 * q) = v;
+      if (row >= ncols) continue;
+      const long e = ((prow0 + row) * nsplit + split) * 2 * D + half * D + 4 * q;
+      if (f16) {
+        const float inv = lds[row * kStageRowFloats + 128];
+        *reinterpret_cast<uint2*>((uint16_t*)part_o + e) =
+            half4_bits(make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv));
+      } else {
+        *reinterpret_cast<float4*>(part_o + e) = v;
+      }
     }
   }
   if (blk == 0 && col < ncols)
@@ -525,7 +551,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
     for (int cb = 0; cb < NCB; ++cb) {
       const int c0 = vh[cb] - col;  // the block's first virtual head
       store_partials_staged<T>(st_acc[cb], lds, a.part_o, a.part_ml, qrow0 + c0,
-                               min(16, a.GV - c0), a.nsplit, split, col, blk);
+                               min(16, a.GV - c0), a.nsplit, split, col, blk, a.part_f16);
     }
     return;
   }
@@ -891,7 +917,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       const int c0 = vh[cb] - col;
       store_partials_staged<T>(st_acc[cb], lds, a.part_o, a.part_ml,
                                (noise ? a.y2_row0 : 0) + yrow0 + c0, min(16, GV - c0), a.nsplit,
-                               split, col, blk);
+                               split, col, blk, a.part_f16);
     }
     return;
   }
@@ -900,7 +926,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     if (!col_ok[cb]) continue;
     const long yrow = yrow0 + vh[cb];
     st_acc[cb].store_to(noise ? a.y2 : a.y, yrow, a.part_o, a.part_ml,
-                        (noise ? a.y2_row0 : 0) + yrow, a.nsplit, split, blk);
+                        (noise ? a.y2_row0 : 0) + yrow, a.nsplit, split, blk, a.part_f16);
   }
 }
 

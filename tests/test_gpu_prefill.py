@@ -149,3 +149,35 @@ def test_prefill_column_blocks_per_wave(gpu, rng, B, Hq, Hkv, S, cap, kv_len, ta
     finally:
         _native.set_tuning("prefill_ncb", 0)
     assert err <= (2e-3 if tag == "f16" else 1e-2), f"ncb={ncb} S={S} {tag}: {err:.3e}"
+
+
+@pytest.mark.parametrize("S,cap,kv_len,tag", [
+    (64, 3328, 3204, "f16"),     # 2048 partial rows over 16 splits
+    (512, 3840, 3716, "f16"),    # the 512-row chunk
+    (512, 3840, 3716, "bf16"),
+    (512, 1024, 600, "f16"),     # causal rows of splits that see no key
+])
+def test_fp16_split_partials(gpu, rng, S, cap, kv_len, tag):
+    """The shared-tile kernels store split partials as fp16 o / l when the
+    row-per-wave merge reads them (half the partial bytes); the result stays
+    within the oracle bar and within 1e-3 (bf16: 8e-3) of fp32 partials."""
+    import torch
+
+    from conftest import torch_dtype
+    from mlx_motif import _native
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    err, y, (q, k, v1, v2) = _run(gpu, rng, 1, 32, 8, S, cap, kv_len, True, tag=tag)
+    assert err <= (2e-3 if tag == "f16" else 1e-2), f"{err:.3e}"
+    T = lambda a: np_to_torch(a, torch_dtype(tag), gpu)  # noqa: E731
+    _native.set_tuning("part_f16", 0)
+    try:
+        y2 = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(128), kv_len=kv_len,
+                              causal=True)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning("part_f16", 1)
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(128), kv_len, True)
+    assert float(np.max(np.abs(torch_to_np(y2) - ref))) <= (2e-3 if tag == "f16" else 1e-2)
+    d = float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2))))
+    assert d <= (1e-3 if tag == "f16" else 8e-3), f"{d:.3e}"
