@@ -203,6 +203,22 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
                       int k_groups, int kr, int D, int cap, int row0, int pos0, float theta,
                       int origin_first, void* stream);
 
+/* RoPE scaling.  The reference builds its rope with
+ * initialize_rope(..., scaling_config=args.rope_scaling) (model.py:414-419;
+ * mlx-lm 0.29.1), and a "linear" config of factor f ropes position p at
+ * p / f (nn.RoPE's scale = 1 / f; the reference's grouped fixture
+ * swift/Tests/MotifKitTests/Fixtures/motif_config_grouped.json:17 uses
+ * f = 2).  Each *_scaled entry point is its unscaled namesake with
+ * position_scale (> 0, finite) after theta: angle = (pos * position_scale)
+ * * theta^(-2i/D), the position scaled first as mx.fast.rope scales it.
+ * The unscaled entry points pass 1, which leaves every angle's bits
+ * unchanged. */
+int motif_rope_split4_scaled(const void* q, const void* k, const void* v, void* q1, void* q2,
+                             void* k1, void* k2, void* v1, void* v2, int dtype, int B, int S,
+                             int q_groups, int gr, int k_groups, int kr, int D, int cap,
+                             int row0, int pos0, float theta, float position_scale,
+                             int origin_first, void* stream);
+
 /* ------------------------------------------------------------------------ *
  * A GDA layer's prefill chunk from the projection outputs, in one attention
  * launch (plus the split merge when its rows are split).  Replaces, for a
@@ -235,6 +251,13 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
                            int B, int S, int q_groups, int gr, int k_groups, int D, int kv_cap,
                            int offset, float scale, float theta, int origin_first,
                            void* workspace, size_t workspace_bytes, void* stream);
+/* With RoPE scaling (see motif_rope_split4_scaled). */
+int motif_gda_prefill_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                  void* k1, void* k2, void* v1, void* v2, void* y_origin,
+                                  void* y_noise, int dtype, int B, int S, int q_groups, int gr,
+                                  int k_groups, int D, int kv_cap, int offset, float scale,
+                                  float theta, float position_scale, int origin_first,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ *
  * MLX affine quantisation (mx.quantize, mode "affine") of `rows` rows of D
@@ -372,6 +395,14 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
                           void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
                           int kv_len, float scale, float theta, int origin_first,
                           void* workspace, size_t workspace_bytes, void* stream);
+/* With RoPE scaling (see motif_rope_split4_scaled). */
+int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                 void* k1, void* k2, void* v1, void* v2, const void* subln_w,
+                                 const float* lambda_full, float one_minus_lambda_init,
+                                 float eps, void* y, int dtype, int B, int Hkv, int gr, int D,
+                                 int kv_cap, int kv_len, float scale, float theta,
+                                 float position_scale, int origin_first, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* The same from the projection outputs over the packed cache: q and the k
  * rows roped as motif_rope_split4 rounds them (fp16), the four rows
@@ -389,6 +420,18 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
                             int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
                             int group_size, float scale, float theta, int origin_first,
                             void* workspace, size_t workspace_bytes, void* stream);
+/* With RoPE scaling (see motif_rope_split4_scaled). */
+int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                   uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                                   uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                                   uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                                   uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                                   const void* subln_w, const float* lambda_full,
+                                   float one_minus_lambda_init, float eps, void* y, int dtype,
+                                   int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                                   int bits, int group_size, float scale, float theta,
+                                   float position_scale, int origin_first, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
                               const void* k2_new, const void* v1_new, const void* v2_new,

@@ -36,17 +36,18 @@ struct RopeArgs {
   int cap, row0, pos0;
   int origin_first;
   float log2_theta;
+  float pos_scale;  // RoPE position scale (1, or 1 / factor for linear scaling)
   long rows_q, rows_k, rows_v;  // B * S * heads of each projection
 };
 
 // Rotates (or, for v, copies) pairs p and p + D/2 in fp32.
 __device__ inline void rope_pair(float x1, float x2, int p, int D, int pos, bool rotate,
-                                 float log2_theta, float& y1, float& y2) {
+                                 float log2_theta, float pos_scale, float& y1, float& y2) {
   y1 = x1;
   y2 = x2;
   if (rotate) {
     float cs, sn;
-    rope_angle(p, D, pos, log2_theta, cs, sn);
+    rope_angle(p, D, pos, log2_theta, pos_scale, cs, sn);
     rope_rotate(x1, x2, cs, sn, y1, y2);
   }
 }
@@ -78,7 +79,8 @@ __device__ inline void rope_row(const RopeArgs& a, const void* src, long src_row
         for (int e = 0; e < 2; ++e) {
           const float x1 = Elem<T>::to_f32((uint16_t)(e ? in1[h] >> 16 : in1[h] & 0xFFFFu));
           const float x2 = Elem<T>::to_f32((uint16_t)(e ? in2[h] >> 16 : in2[h] & 0xFFFFu));
-          rope_pair(x1, x2, p0 + 2 * h + e, D, pos, rotate, a.log2_theta, y1[e], y2[e]);
+          rope_pair(x1, x2, p0 + 2 * h + e, D, pos, rotate, a.log2_theta, a.pos_scale, y1[e],
+                    y2[e]);
         }
         o1[h] = (uint32_t)Elem<T>::from_f32(y1[0]) | ((uint32_t)Elem<T>::from_f32(y1[1]) << 16);
         o2[h] = (uint32_t)Elem<T>::from_f32(y2[0]) | ((uint32_t)Elem<T>::from_f32(y2[1]) << 16);
@@ -94,7 +96,7 @@ __device__ inline void rope_row(const RopeArgs& a, const void* src, long src_row
     const float x1 = Elem<T>::load(src, si + p);
     const float x2 = Elem<T>::load(src, si + H + p);
     float y1, y2;
-    rope_pair(x1, x2, p, D, pos, rotate, a.log2_theta, y1, y2);
+    rope_pair(x1, x2, p, D, pos, rotate, a.log2_theta, a.pos_scale, y1, y2);
     Elem<T>::store(dst, di + p, y1);
     Elem<T>::store(dst, di + H + p, y2);
   }
@@ -188,10 +190,11 @@ using namespace motif;
 
 extern "C" {
 
-int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, void* q2, void* k1,
-                      void* k2, void* v1, void* v2, int dtype, int B, int S, int q_groups, int gr,
-                      int k_groups, int kr, int D, int cap, int row0, int pos0, float theta,
-                      int origin_first, void* stream) {
+int motif_rope_split4_scaled(const void* q, const void* k, const void* v, void* q1, void* q2,
+                             void* k1, void* k2, void* v1, void* v2, int dtype, int B, int S,
+                             int q_groups, int gr, int k_groups, int kr, int D, int cap,
+                             int row0, int pos0, float theta, float position_scale,
+                             int origin_first, void* stream) {
   CallScope scope;
   clear_error();
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
@@ -206,6 +209,8 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
                 row0 + S, cap);
   MOTIF_REQUIRE(pos0 >= 0, "rope_split4: pos0=%d must be >= 0", pos0);
   MOTIF_REQUIRE(theta > 1.f, "rope_split4: theta must be > 1");
+  MOTIF_REQUIRE(position_scale > 0.f && position_scale <= 3.4028234663852886e38f,
+                "rope_split4: position_scale must be positive and finite");
   if (B == 0 || S == 0) return MOTIF_OK;
   MOTIF_REQUIRE(q && k && v && q1 && q2 && k1 && k2 && v1 && v2, "rope_split4: null pointer");
   RopeArgs a{};
@@ -216,6 +221,7 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
   a.cap = cap; a.row0 = row0; a.pos0 = pos0;
   a.origin_first = origin_first != 0;
   a.log2_theta = log2f(theta);
+  a.pos_scale = position_scale;
   a.rows_q = (long)B * S * q_groups * (gr + 1);
   a.rows_k = (long)B * S * k_groups * (kr + 1);
   a.rows_v = (long)B * S * 2 * k_groups;
@@ -227,6 +233,15 @@ int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, voi
     case MOTIF_BF16: return vec ? launch_rope<bf16_t, true>(a, s) : launch_rope<bf16_t, false>(a, s);
     default: return launch_rope<float, false>(a, s);
   }
+}
+
+int motif_rope_split4(const void* q, const void* k, const void* v, void* q1, void* q2, void* k1,
+                      void* k2, void* v1, void* v2, int dtype, int B, int S, int q_groups, int gr,
+                      int k_groups, int kr, int D, int cap, int row0, int pos0, float theta,
+                      int origin_first, void* stream) {
+  return motif_rope_split4_scaled(q, k, v, q1, q2, k1, k2, v1, v2, dtype, B, S, q_groups, gr,
+                                  k_groups, kr, D, cap, row0, pos0, theta, 1.f, origin_first,
+                                  stream);
 }
 
 }  // extern "C"

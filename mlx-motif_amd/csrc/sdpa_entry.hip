@@ -553,12 +553,13 @@ int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
                        scale, workspace, workspace_bytes, nk, stream);
 }
 
-int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
-                          void* k2, void* v1, void* v2, const void* subln_w,
-                          const float* lambda_full, float one_minus_lambda_init, float eps,
-                          void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
-                          int kv_len, float scale, float theta, int origin_first,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                 void* k1, void* k2, void* v1, void* v2, const void* subln_w,
+                                 const float* lambda_full, float one_minus_lambda_init,
+                                 float eps, void* y, int dtype, int B, int Hkv, int gr, int D,
+                                 int kv_cap, int kv_len, float scale, float theta,
+                                 float position_scale, int origin_first, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
   CallScope scope;
   clear_error();
   const char* name = "gda_decode_proj";
@@ -571,6 +572,8 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
                 "%s: null pointer", name);
   MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the new token's row", name, kv_len);
   MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  MOTIF_REQUIRE(position_scale > 0.f && position_scale <= 3.4028234663852886e38f,
+                "%s: position_scale must be positive and finite", name);
   const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
                      tuning().mfma && gr + 1 <= 16 && kv_len <= kMfmaMaxRows &&
                      aligned(q_proj, 16) && aligned(k_proj, 16) && aligned(v_proj, 16) &&
@@ -592,6 +595,7 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
   a.from_proj = 1;
   a.q_origin_first = origin_first != 0;
   a.rope_log2_theta = log2f(theta);
+  a.rope_pos_scale = position_scale;
   const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
   rc = check_partials(name, a, true);
   if (rc != MOTIF_OK) return rc;
@@ -599,6 +603,18 @@ int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_
                                                     (hipStream_t)stream)
                             : launch_gda_decode_bf16(a, gda_columns(gr), nblocks,
                                                      (hipStream_t)stream);
+}
+
+int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                          void* k2, void* v1, void* v2, const void* subln_w,
+                          const float* lambda_full, float one_minus_lambda_init, float eps,
+                          void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
+                          int kv_len, float scale, float theta, int origin_first,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return motif_gda_decode_proj_scaled(q_proj, k_proj, v_proj, k1, k2, v1, v2, subln_w,
+                                      lambda_full, one_minus_lambda_init, eps, y, dtype, B, Hkv,
+                                      gr, D, kv_cap, kv_len, scale, theta, 1.f, origin_first,
+                                      workspace, workspace_bytes, stream);
 }
 
 int motif_sdpa_dual_v(const void* q, const void* k, const void* v1, const void* v2, void* y,
@@ -832,16 +848,17 @@ int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new
                       workspace_bytes, nk, stream);
 }
 
-int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* v_proj,
-                            uint32_t* k1_data, void* k1_scales, void* k1_biases,
-                            uint32_t* k2_data, void* k2_scales, void* k2_biases,
-                            uint32_t* v1_data, void* v1_scales, void* v1_biases,
-                            uint32_t* v2_data, void* v2_scales, void* v2_biases,
-                            const void* subln_w, const float* lambda_full,
-                            float one_minus_lambda_init, float eps, void* y, int dtype, int B,
-                            int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
-                            int group_size, float scale, float theta, int origin_first,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                   uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                                   uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                                   uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                                   uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                                   const void* subln_w, const float* lambda_full,
+                                   float one_minus_lambda_init, float eps, void* y, int dtype,
+                                   int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
+                                   int bits, int group_size, float scale, float theta,
+                                   float position_scale, int origin_first, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
   CallScope scope;
   clear_error();
   const char* name = "gda_decode_q_proj";
@@ -858,6 +875,8 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
                 "%s: null pointer", name);
   MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the new token's row", name, kv_len);
   MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  MOTIF_REQUIRE(position_scale > 0.f && position_scale <= 3.4028234663852886e38f,
+                "%s: position_scale must be positive and finite", name);
   const int gc = gda_columns(gr);
   const int ng = D > 0 ? D / group_size : 1;
   const uintptr_t data_bits = (uintptr_t)k1_data | (uintptr_t)k2_data | (uintptr_t)v1_data |
@@ -889,10 +908,28 @@ int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* 
   a.from_proj = 1;
   a.q_origin_first = origin_first != 0;
   a.rope_log2_theta = log2f(theta);
+  a.rope_pos_scale = position_scale;
   rc = check_partials(name, a, true);
   if (rc != MOTIF_OK) return rc;
   return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit),
                                  (hipStream_t)stream);
+}
+
+int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* v_proj,
+                            uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                            uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                            uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                            uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                            const void* subln_w, const float* lambda_full,
+                            float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                            int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                            int group_size, float scale, float theta, int origin_first,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return motif_gda_decode_q_proj_scaled(
+      q_proj, k_proj, v_proj, k1_data, k1_scales, k1_biases, k2_data, k2_scales, k2_biases,
+      v1_data, v1_scales, v1_biases, v2_data, v2_scales, v2_biases, subln_w, lambda_full,
+      one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D, kv_cap, kv_len, bits, group_size,
+      scale, theta, 1.f, origin_first, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"
@@ -910,11 +947,12 @@ size_t motif_gda_prefill_workspace_bytes(int B, int S, int q_groups, int gr, int
   return plan_gda_prefill(B, k_groups, G_o, G_n, S, kv_len).workspace_bytes;
 }
 
-int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
-                           void* k2, void* v1, void* v2, void* y_origin, void* y_noise, int dtype,
-                           int B, int S, int q_groups, int gr, int k_groups, int D, int kv_cap,
-                           int offset, float scale, float theta, int origin_first,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+int motif_gda_prefill_proj_scaled(const void* q_proj, const void* k_proj, const void* v_proj,
+                                  void* k1, void* k2, void* v1, void* v2, void* y_origin,
+                                  void* y_noise, int dtype, int B, int S, int q_groups, int gr,
+                                  int k_groups, int D, int kv_cap, int offset, float scale,
+                                  float theta, float position_scale, int origin_first,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   CallScope scope;
   clear_error();
   const char* name = "gda_prefill_proj";
@@ -930,6 +968,8 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
                 "%s: rows [%d, %d) must fit the cache capacity %d", name, offset, offset + S,
                 kv_cap);
   MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
+  MOTIF_REQUIRE(position_scale > 0.f && position_scale <= 3.4028234663852886e38f,
+                "%s: position_scale must be positive and finite", name);
   MOTIF_REQUIRE((long)B * k_groups * (long)kv_cap * D < (1L << 40), "%s: cache too large", name);
   MOTIF_REQUIRE(q_proj && k_proj && v_proj && k1 && k2 && v1 && v2 && y_origin && y_noise,
                 "%s: null pointer", name);
@@ -968,6 +1008,7 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
   a.qscale = scale * 1.4426950408889634f;
   a.q_groups = q_groups; a.q_gr = gr; a.q_origin_first = origin_first != 0;
   a.rope_log2_theta = log2f(theta);
+  a.rope_pos_scale = position_scale;
   a.rope_pos0 = offset;
   a.y2_row0 = (long)B * Hq_o * S;
   if (pp.nsplit > 1) {
@@ -987,6 +1028,17 @@ int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v
   SdpaArgs m = a;
   m.Hq = Hq_o + q_groups;
   return sdpa_merge(m, dtype, D, s);
+}
+
+int motif_gda_prefill_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
+                           void* k2, void* v1, void* v2, void* y_origin, void* y_noise, int dtype,
+                           int B, int S, int q_groups, int gr, int k_groups, int D, int kv_cap,
+                           int offset, float scale, float theta, int origin_first,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  return motif_gda_prefill_proj_scaled(q_proj, k_proj, v_proj, k1, k2, v1, v2, y_origin, y_noise,
+                                       dtype, B, S, q_groups, gr, k_groups, D, kv_cap, offset,
+                                       scale, theta, 1.f, origin_first, workspace,
+                                       workspace_bytes, stream);
 }
 
 // Host-only walk of every launch planner over decode, slab and prefill

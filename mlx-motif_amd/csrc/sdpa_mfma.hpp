@@ -139,7 +139,7 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
     // Lane L computes the angle of pair L (0..63) once; the lanes read the
     // eight they need with __shfl (one slow-path sincosf per lane, not eight).
     float cs0, sn0;
-    rope_angle((int)(threadIdx.x & 63u), 128, pos, a.rope_log2_theta, cs0, sn0);
+    rope_angle((int)(threadIdx.x & 63u), 128, pos, a.rope_log2_theta, a.rope_pos_scale, cs0, sn0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t r = 0;
@@ -238,7 +238,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
         // others are read from the lanes of its block.
         float cs0, sn0;
         rope_angle(32 * (col >> 3) + 8 * blk + (col & 7), 128, a.kv_len - 1, a.rope_log2_theta,
-                   cs0, sn0);
+                   a.rope_pos_scale, cs0, sn0);
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
 #pragma unroll

@@ -263,7 +263,7 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
     // eight they need with __shfl (one slow-path sincosf per lane, not eight).
     const bool first = chunk < 8;
     float cs0, sn0;
-    rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, cs0, sn0);
+    rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, a.rope_pos_scale, cs0, sn0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float other = __shfl_xor(v[e], 8);
@@ -464,7 +464,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
       // (lane L ^ 32).  Lane L computes the angle of pair L, which the
       // others read with __shfl.
       float cs0, sn0;
-      rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, cs0, sn0);
+      rope_angle(lane, D, a.kv_len - 1, a.rope_log2_theta, a.rope_pos_scale, cs0, sn0);
       const bool first = blk < 2;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {

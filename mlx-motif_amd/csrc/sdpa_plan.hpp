@@ -80,6 +80,7 @@ struct SdpaArgs {
   int from_proj;
   int q_origin_first;
   float rope_log2_theta;
+  float rope_pos_scale = 1.f;  // RoPE position scale: 1, or 1 / factor (linear scaling)
   // Prefill chunk of a GDA layer from the projection outputs
   // (gda_prefill_proj_kernel): q is q_proj (B, S_q, q_groups*(q_gr+1)*D),
   // new_k1 k_proj and new_v1 v_proj (B, S_q, 2*Hkv*D; k1[g] = head 2g,

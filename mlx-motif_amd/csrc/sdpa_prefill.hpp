@@ -611,7 +611,8 @@ __device__ inline __amdgpu_buffer_rsrc_t uniform_stream_rsrc(const void* base, u
 // half as 8-byte words.
 // (inv: the pairs' inverse frequencies, rope_inv_freq.)
 template <typename T>
-__device__ inline void rope_words_inv(uint2& lo, uint2& hi, const float (&inv)[4], int pos) {
+__device__ inline void rope_words_inv(uint2& lo, uint2& hi, const float (&inv)[4], int pos,
+                                      float pos_scale) {
   uint32_t a[2] = {lo.x, lo.y}, b[2] = {hi.x, hi.y};
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -621,7 +622,7 @@ __device__ inline void rope_words_inv(uint2& lo, uint2& hi, const float (&inv)[4
       const float x1 = Elem<T>::to_f32((uint16_t)(e ? a[h] >> 16 : a[h] & 0xFFFFu));
       const float x2 = Elem<T>::to_f32((uint16_t)(e ? b[h] >> 16 : b[h] & 0xFFFFu));
       float cs, sn;
-      rope_angle_inv(inv[2 * h + e], pos, cs, sn);
+      rope_angle_inv(inv[2 * h + e], pos, pos_scale, cs, sn);
       rope_rotate(x1, x2, cs, sn, y1[e], y2[e]);
     }
     a[h] = (uint32_t)Elem<T>::from_f32(y1[0]) | ((uint32_t)Elem<T>::from_f32(y1[1]) << 16);
@@ -631,11 +632,12 @@ __device__ inline void rope_words_inv(uint2& lo, uint2& hi, const float (&inv)[4
   hi = make_uint2(b[0], b[1]);
 }
 template <typename T>
-__device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float log2_theta) {
+__device__ inline void rope_words(uint2& lo, uint2& hi, int p0, int pos, float log2_theta,
+                                  float pos_scale) {
   const float inv[4] = {rope_inv_freq(p0, 128, log2_theta), rope_inv_freq(p0 + 1, 128, log2_theta),
                         rope_inv_freq(p0 + 2, 128, log2_theta),
                         rope_inv_freq(p0 + 3, 128, log2_theta)};
-  rope_words_inv<T>(lo, hi, inv, pos);
+  rope_words_inv<T>(lo, hi, inv, pos, pos_scale);
 }
 
 // NCB: column blocks of 16 virtual heads per wave, as in sdpa_prefill_kernel.
@@ -723,7 +725,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       const long src = ((long)b * S + (r - row0)) * pstride + (long)hk * D;
       uint2 lo = *reinterpret_cast<const uint2*>(kproj + src + p0);
       uint2 hi = *reinterpret_cast<const uint2*>(kproj + src + 64 + p0);
-      rope_words<T>(lo, hi, p0, a.rope_pos0 + (r - row0), a.rope_log2_theta);
+      rope_words<T>(lo, hi, p0, a.rope_pos0 + (r - row0), a.rope_log2_theta, a.rope_pos_scale);
       *reinterpret_cast<uint2*>(kc + (crow0 + r) * D + p0) = lo;
       *reinterpret_cast<uint2*>(kc + (crow0 + r) * D + 64 + p0) = hi;
     }
@@ -762,8 +764,8 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     for (int s = 0; s < 2; ++s) {
       uint2 l0 = make_uint2(w[s].x, w[s].y), h0 = make_uint2(w[s + 2].x, w[s + 2].y);
       uint2 l1 = make_uint2(w[s].z, w[s].w), h1 = make_uint2(w[s + 2].z, w[s + 2].w);
-      rope_words<T>(l0, h0, 32 * s + 8 * blk, pos, a.rope_log2_theta);
-      rope_words<T>(l1, h1, 32 * s + 8 * blk + 4, pos, a.rope_log2_theta);
+      rope_words<T>(l0, h0, 32 * s + 8 * blk, pos, a.rope_log2_theta, a.rope_pos_scale);
+      rope_words<T>(l1, h1, 32 * s + 8 * blk + 4, pos, a.rope_log2_theta, a.rope_pos_scale);
       w[s] = make_uint4(l0.x, l0.y, l1.x, l1.y);
       w[s + 2] = make_uint4(h0.x, h0.y, h1.x, h1.y);
     }
@@ -837,7 +839,7 @@ gda_prefill_proj_kernel(SdpaArgs a) {
         uint2* phi =
             reinterpret_cast<uint2*>(&Kt[r * 256 + (((rcp + 8) ^ (r % 16)) * 16) + 8 * rh]);
         uint2 lo = *plo, hi = *phi;
-        rope_words_inv<T>(lo, hi, rinv, a.rope_pos0 + (first_row + r - row0));
+        rope_words_inv<T>(lo, hi, rinv, a.rope_pos0 + (first_row + r - row0), a.rope_pos_scale);
         *plo = lo;
         *phi = hi;
       }

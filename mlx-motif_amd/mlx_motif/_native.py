@@ -109,16 +109,30 @@ _SIGNATURES = {
         [_vp] * 17 + [_c_f, _c_f, _vp] + [_c_int] * 9
         + [_c_f, _c_f, _c_int, _vp, _c_sz, _vp],
     ),
+    "motif_gda_decode_proj_scaled": (
+        _c_int,
+        [_vp] * 9 + [_c_f, _c_f, _vp] + [_c_int] * 7 + [_c_f, _c_f, _c_f, _c_int, _vp, _c_sz, _vp],
+    ),
+    "motif_gda_decode_q_proj_scaled": (
+        _c_int,
+        [_vp] * 17 + [_c_f, _c_f, _vp] + [_c_int] * 9
+        + [_c_f, _c_f, _c_f, _c_int, _vp, _c_sz, _vp],
+    ),
     "motif_gda_decode_q_append": (
         _c_int,
         [_vp] * 20 + [_c_f, _c_f, _vp] + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],
     ),
     "motif_polynorm": (_c_int, [_vp] * 4 + [_c_int, _c_i64, _c_int, _c_f, _vp]),
     "motif_rope_split4": (_c_int, [_vp] * 9 + [_c_int] * 11 + [_c_f, _c_int, _vp]),
+    "motif_rope_split4_scaled": (_c_int, [_vp] * 9 + [_c_int] * 11 + [_c_f, _c_f, _c_int, _vp]),
     "motif_gda_prefill_workspace_bytes": (_c_sz, [_c_int] * 7),
     "motif_gda_prefill_proj": (
         _c_int,
         [_vp] * 9 + [_c_int] * 9 + [_c_f, _c_f, _c_int, _vp, _c_sz, _vp],
+    ),
+    "motif_gda_prefill_proj_scaled": (
+        _c_int,
+        [_vp] * 9 + [_c_int] * 9 + [_c_f, _c_f, _c_f, _c_int, _vp, _c_sz, _vp],
     ),
     "motif_set_tuning": (_c_int, [ctypes.c_char_p, _c_int]),
 }

@@ -240,11 +240,11 @@ def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale
     cache ``k1, k2, v1, v2``, then the step over ``offset + 1`` rows.  On the
     fp16/bf16 cache at head_dim 128 this is ``motif_gda_decode_proj`` (the
     attention launch ropes and writes; then the merge); otherwise
-    ``rope_split4`` followed by ``gda_decode_attention``.  ``rope_scaling``
-    must be ``None``: only unscaled RoPE is built."""
-    from .rope import require_unscaled, rope_split4, rope_split4_reference
+    ``rope_split4`` followed by ``gda_decode_attention``.  ``rope_scaling``:
+    None, or a default / linear config (``rope.rope_position_scale``)."""
+    from .rope import rope_position_scale, rope_split4, rope_split4_reference
 
-    require_unscaled(rope_scaling)
+    pscale = rope_position_scale(rope_scaling)
 
     B, S, nq = q_proj.shape
     H_kv = k1.shape[1]
@@ -254,7 +254,8 @@ def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale
     kv_len = offset + 1
     if _common._DISABLE:
         q1, q2, *_ = rope_split4_reference(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset,
-                                           theta, origin_first, caches=(k1, k2, v1, v2))
+                                           theta, origin_first, caches=(k1, k2, v1, v2),
+                                           position_scale=pscale)
         return gda_decode_attention_reference(q1, q2, k1, k2, v1, v2, scale, subln_weight,
                                               lambda_full, lambda_init, gr, eps, kv_len)
     assert k_proj.shape == (B, 1, 2 * H_kv * D) and v_proj.shape == (B, 1, 2 * H_kv * D), (
@@ -274,15 +275,16 @@ def gda_decode_attention_from_proj(q_proj, k_proj, v_proj, k1, k2, v1, v2, scale
     y = torch.empty((B, H_kv * gr, 1, 2 * D), dtype=q_proj.dtype, device=dev)
     lib = _native.lib()
     ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
-    rc = lib.motif_gda_decode_proj(
+    rc = lib.motif_gda_decode_proj_scaled(
         q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(), k1.data_ptr(), k2.data_ptr(),
         v1.data_ptr(), v2.data_ptr(), w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init),
         float(eps), y.data_ptr(), _native.dtype_code(q_proj.dtype), B, H_kv, gr, D, KV_cap,
-        kv_len, float(scale), float(theta), int(bool(origin_first)), ws.data_ptr(), ws.numel(),
-        _native.stream_of(dev))
+        kv_len, float(scale), float(theta), float(pscale), int(bool(origin_first)),
+        ws.data_ptr(), ws.numel(), _native.stream_of(dev))
     if rc == _native.MOTIF_ERR_UNSUPPORTED:  # the two native calls
         q1, q2, *_ = rope_split4(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset, theta,
-                                 origin_first, caches=(k1, k2, v1, v2))
+                                 origin_first, caches=(k1, k2, v1, v2),
+                                 rope_scaling=rope_scaling)
         return gda_decode_attention(q1, q2, k1, k2, v1, v2, scale, subln_weight, lambda_full,
                                     lambda_init, gr, eps, kv_len=kv_len)
     _native.check(rc)
@@ -299,10 +301,11 @@ def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q:
     roped k rows and v rows are quantised into row ``offset`` of the packed
     slots.  ``motif_gda_decode_q_proj`` when the fused kernel takes the
     shape, else ``rope_split4`` then ``gda_decode_attention_q4(new_kv=...)``
-    (the same values bit for bit).  ``rope_scaling`` must be ``None``."""
-    from .rope import require_unscaled, rope_split4, rope_split4_reference
+    (the same values bit for bit).  ``rope_scaling``: None, or a default /
+    linear config."""
+    from .rope import rope_position_scale, rope_split4, rope_split4_reference
 
-    require_unscaled(rope_scaling)
+    pscale = rope_position_scale(rope_scaling)
 
     B, S, nq = q_proj.shape
     H_kv = k1_q[0].shape[1]
@@ -313,7 +316,7 @@ def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q:
     slots = (k1_q, k2_q, v1_q, v2_q)
     if _common._DISABLE:
         q1, q2, *rows = rope_split4_reference(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset,
-                                              theta, origin_first)
+                                              theta, origin_first, position_scale=pscale)
         return gda_decode_attention_q4(q1, q2, *slots, scale, subln_weight, lambda_full,
                                        lambda_init, gr, group_size, bits, eps, kv_len=kv_len,
                                        new_kv=rows)
@@ -333,15 +336,15 @@ def gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj, k1_q: tuple, k2_q:
     y = torch.empty((B, H_kv * gr, 1, 2 * D), dtype=q_proj.dtype, device=dev)
     lib = _native.lib()
     ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
-    rc = lib.motif_gda_decode_q_proj(
+    rc = lib.motif_gda_decode_q_proj_scaled(
         q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(),
         *(x.data_ptr() for t in slots for x in t), w.data_ptr(), lam.data_ptr(),
         float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q_proj.dtype), B,
-        H_kv, gr, D, KV_cap, kv_len, bits, group_size, float(scale), float(theta),
+        H_kv, gr, D, KV_cap, kv_len, bits, group_size, float(scale), float(theta), float(pscale),
         int(bool(origin_first)), ws.data_ptr(), ws.numel(), _native.stream_of(dev))
     if rc == _native.MOTIF_ERR_UNSUPPORTED:  # the two native calls
         q1, q2, *rows = rope_split4(q_proj, k_proj, v_proj, H_kv, gr, H_kv, 1, offset, theta,
-                                    origin_first)
+                                    origin_first, rope_scaling=rope_scaling)
         return gda_decode_attention_q4(q1, q2, *slots, scale, subln_weight, lambda_full,
                                        lambda_init, gr, group_size, bits, eps, kv_len=kv_len,
                                        new_kv=rows)

@@ -20,13 +20,14 @@ import torch
 from .. import _native
 from . import _common
 from .attention import sdpa_dual_v_rows
-from .rope import _heads, require_unscaled, rope_split4, rope_split4_reference
+from .rope import _heads, rope_position_scale, rope_split4, rope_split4_reference
 
 
 def gda_prefill_attention_from_proj_reference(q_proj, k_proj, v_proj, caches, offset: int,
                                               q_groups: int, gr: int, k_groups: int,
                                               scale: float, theta: float = 10000.0,
-                                              origin_first: bool = False):
+                                              origin_first: bool = False,
+                                              position_scale: float = 1.0):
     """Torch-op composition: ``rope_split4_reference`` into the cache, then
     the bottom-right causal dual-V attention of q1 over k1 and of q2 over k2
     (both over V1/V2)."""
@@ -34,7 +35,7 @@ def gda_prefill_attention_from_proj_reference(q_proj, k_proj, v_proj, caches, of
 
     q1, q2, k1, k2, v1, v2 = rope_split4_reference(q_proj, k_proj, v_proj, q_groups, gr,
                                                    k_groups, 1, offset, theta, origin_first,
-                                                   caches=caches)
+                                                   caches=caches, position_scale=position_scale)
     S = q_proj.shape[1]
     kv_len = offset + S
     mask = _causal_mask(S, kv_len, q_proj.device)
@@ -57,12 +58,13 @@ def gda_prefill_attention_from_proj(q_proj, k_proj, v_proj, caches, offset: int,
     query row s seeing cache rows ``[0, offset + s]``.  One launch
     (``motif_gda_prefill_proj``) where the kernel takes the shape (fp16/bf16,
     D = 128), else ``rope_split4`` and two ``sdpa_dual_v_rows`` calls.
-    ``rope_scaling`` must be ``None``."""
-    require_unscaled(rope_scaling)
+    ``rope_scaling``: None, or a default / linear config
+    (``rope.rope_position_scale``)."""
+    pscale = rope_position_scale(rope_scaling)
     if _common._DISABLE:
         return gda_prefill_attention_from_proj_reference(q_proj, k_proj, v_proj, caches, offset,
                                                          q_groups, gr, k_groups, scale, theta,
-                                                         origin_first)
+                                                         origin_first, position_scale=pscale)
     B, S, D = _heads(q_proj, k_proj, v_proj, q_groups, gr, k_groups, 1)
     assert q_groups % k_groups == 0, (
         f"q_groups={q_groups} must be a multiple of k_groups={k_groups}")
@@ -88,15 +90,15 @@ def gda_prefill_attention_from_proj(q_proj, k_proj, v_proj, caches, offset: int,
     kv_len = offset + S
     nbytes = lib.motif_gda_prefill_workspace_bytes(B, S, q_groups, gr, k_groups, D, kv_len)
     ws = _native.workspace(dev, nbytes) if nbytes else None
-    rc = lib.motif_gda_prefill_proj(
+    rc = lib.motif_gda_prefill_proj_scaled(
         q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(), *(c.data_ptr() for c in caches),
         y_o.data_ptr(), y_n.data_ptr(), _native.dtype_code(dt), B, S, q_groups, gr, k_groups, D,
-        cap, int(offset), float(scale), float(theta), int(bool(origin_first)),
+        cap, int(offset), float(scale), float(theta), float(pscale), int(bool(origin_first)),
         ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         _native.stream_of(dev))
     if rc == _native.MOTIF_ERR_UNSUPPORTED:  # the separate native calls
         q1, q2, *_ = rope_split4(q_proj, k_proj, v_proj, q_groups, gr, k_groups, 1, offset, theta,
-                                 origin_first, caches=caches)
+                                 origin_first, caches=caches, rope_scaling=rope_scaling)
         return (sdpa_dual_v_rows(q1, k1, v1, v2, scale, kv_len=kv_len, causal=True),
                 sdpa_dual_v_rows(q2, k2, v1, v2, scale, kv_len=kv_len, causal=True))
     _native.check(rc)

@@ -10,12 +10,14 @@ calls (``src/mlx_motif/model.py:590-594``; ``initialize_rope`` with
 k1/k2/v1/v2 rows are written straight into the full-capacity 4-slot fp cache
 at rows ``offset .. offset + S - 1``.
 
-Only unscaled RoPE is built: the reference model also accepts a
-``rope_scaling`` config (``initialize_rope(..., scaling_config=...)``,
-``model.py:414-419``; e.g. linear with factor 2, which divides positions by
-2).  Every wrapper here takes ``rope_scaling`` and raises
-``NotImplementedError`` for anything but ``None``, so a scaled config fails
-instead of getting unscaled positions.
+RoPE scaling: the reference builds its rope with
+``initialize_rope(..., scaling_config=args.rope_scaling)`` (``model.py:414-419``,
+mlx-lm 0.29.1).  ``None`` and the "default" type rope at positions
+``offset + s``; the "linear" type of factor f ropes at ``(offset + s) / f``
+(``nn.RoPE``'s ``scale = 1 / f``; the reference's grouped fixture uses f = 2),
+which the kernels take as a position scale.  Other types (llama3, yarn,
+longrope, ...) raise ``NotImplementedError`` rather than rope at the wrong
+positions.
 """
 
 from __future__ import annotations
@@ -38,13 +40,15 @@ def _heads(q_proj, k_proj, v_proj, q_groups, gr, k_groups, kr):
 
 def rope_split4_reference(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_groups: int,
                           kr: int, offset: int, theta: float = 10000.0,
-                          origin_first: bool = False, caches=None):
-    """Torch-op statement (fp32 angles and rotation, rounded once)."""
+                          origin_first: bool = False, caches=None, position_scale: float = 1.0):
+    """Torch-op statement (fp32 angles and rotation, rounded once); positions
+    are scaled by ``position_scale`` first."""
     B, S, D = _heads(q_proj, k_proj, v_proj, q_groups, gr, k_groups, kr)
     dev, dt = q_proj.device, q_proj.dtype
     half = D // 2
     inv = theta ** (-torch.arange(half, device=dev, dtype=torch.float32) * 2.0 / D)
-    ang = (offset + torch.arange(S, device=dev, dtype=torch.float32))[:, None] * inv[None, :]
+    pos = (offset + torch.arange(S, device=dev, dtype=torch.float32)) * float(position_scale)
+    ang = pos[:, None] * inv[None, :]
     cos, sin = torch.cos(ang)[None, :, None, :], torch.sin(ang)[None, :, None, :]
 
     def rot(x, H):
@@ -74,13 +78,25 @@ def rope_split4_reference(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_grou
     return (q1.contiguous(), q2.contiguous(), *caches)
 
 
-def require_unscaled(rope_scaling) -> None:
-    """Rejects a RoPE scaling config (``ModelArgs.rope_scaling``): the kernels
-    rope at the unscaled positions ``offset + s``."""
-    if rope_scaling is not None:
-        raise NotImplementedError(
-            f"rope_scaling={rope_scaling!r}: only unscaled RoPE (rope_scaling=None) is "
-            "supported; a scaled config would get unscaled positions")
+def rope_position_scale(rope_scaling) -> float:
+    """The position scale of a RoPE scaling config (``ModelArgs.rope_scaling``),
+    read as mlx-lm's ``initialize_rope`` reads it: the type is ``"type"`` or
+    else ``"rope_type"`` (default ``"default"``); ``None`` and "default" give
+    1, "linear" gives ``1 / factor``.  Other types raise
+    ``NotImplementedError``."""
+    if rope_scaling is None:
+        return 1.0
+    kind = rope_scaling.get("type") or rope_scaling.get("rope_type", "default")
+    if kind == "default":
+        return 1.0
+    if kind == "linear":
+        factor = float(rope_scaling["factor"])
+        if not factor > 0.0 or factor == float("inf"):
+            raise ValueError(f"rope_scaling factor must be positive and finite, got {factor}")
+        return 1.0 / factor
+    raise NotImplementedError(
+        f"rope_scaling={rope_scaling!r}: RoPE type {kind!r} is not built (default and linear "
+        "are); it would otherwise be roped at the wrong positions")
 
 
 def rope_split4(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_groups: int, kr: int,
@@ -92,12 +108,12 @@ def rope_split4(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_groups: int, k
     (B, q_groups, S, D) roped at positions ``offset + s``; k1/k2 (roped) and
     v1/v2 either new (B, H, S, D) tensors or, with ``caches=(k1, k2, v1,
     v2)`` full-capacity (B, H, cap, D) buffers, those buffers with rows
-    ``offset .. offset + S - 1`` written.  ``rope_scaling`` must be ``None``
-    (``require_unscaled``)."""
-    require_unscaled(rope_scaling)
+    ``offset .. offset + S - 1`` written.  ``rope_scaling``: None, or a
+    default / linear config (``rope_position_scale``)."""
+    pscale = rope_position_scale(rope_scaling)
     if _common._DISABLE:
         return rope_split4_reference(q_proj, k_proj, v_proj, q_groups, gr, k_groups, kr, offset,
-                                     theta, origin_first, caches)
+                                     theta, origin_first, caches, position_scale=pscale)
     B, S, D = _heads(q_proj, k_proj, v_proj, q_groups, gr, k_groups, kr)
     dev = _native.require_device(q_proj, k_proj, v_proj, *(caches or ()))
     dt = q_proj.dtype
@@ -123,10 +139,10 @@ def rope_split4(q_proj, k_proj, v_proj, q_groups: int, gr: int, k_groups: int, k
         assert 0 <= offset and offset + S <= cap, f"rows [{offset}, {offset + S}) exceed {cap}"
         outs, row0 = tuple(caches), offset
     _native.check(
-        _native.lib().motif_rope_split4(
+        _native.lib().motif_rope_split4_scaled(
             q_proj.data_ptr(), k_proj.data_ptr(), v_proj.data_ptr(), q1.data_ptr(), q2.data_ptr(),
             *(t.data_ptr() for t in outs), _native.dtype_code(dt), B, S, q_groups, gr, k_groups,
-            kr, D, cap, row0, int(offset), float(theta), int(bool(origin_first)),
+            kr, D, cap, row0, int(offset), float(theta), float(pscale), int(bool(origin_first)),
             _native.stream_of(dev),
         )
     )

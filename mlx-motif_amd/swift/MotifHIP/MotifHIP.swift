@@ -16,6 +16,7 @@ public enum MotifHIPStatus: Int32 {
     case unsupported = -2
     case workspace = -3
     case hip = -4
+    case internalError = -5
 }
 
 public enum MotifHIPDType: Int32 {
@@ -234,24 +235,44 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// The RoPE position scale of a model's rope_scaling config
+    /// (MotifTypes.swift:218, read as mlx-lm's initialize_rope reads it: the
+    /// type is `type`, else `ropeType`, else "default").  No config and
+    /// "default" give 1, "linear" gives 1 / factor; nil for a type that is
+    /// not built here or a factor that is not positive and finite, where the
+    /// caller must not use these entry points (positions would be wrong).
+    public static func ropePositionScale(type: String?, ropeType: String?,
+                                         factor: Double?) -> Float? {
+        switch type ?? ropeType ?? "default" {
+        case "default":
+            return 1
+        case "linear":
+            guard let factor, factor > 0, factor.isFinite else { return nil }
+            return Float(1 / factor)
+        default:
+            return nil
+        }
+    }
+
     /// RoPE on q and k, the q1/q2, k1/k2, v1/v2 head split and the 4-slot
     /// write in one launch: k1..v2 rows row0 ..< row0 + seqLen of buffers of
     /// `capacity` rows (the cache, or capacity = seqLen, row0 = 0 for plain
-    /// tensors), positions pos0 + s.
+    /// tensors), positions (pos0 + s) * positionScale (ropePositionScale).
     public static func ropeSplit4(
         qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
         q1: UnsafeMutableRawPointer, q2: UnsafeMutableRawPointer,
         k1: UnsafeMutableRawPointer, k2: UnsafeMutableRawPointer,
         v1: UnsafeMutableRawPointer, v2: UnsafeMutableRawPointer, dtype: MotifHIPDType,
         batch: Int, seqLen: Int, qGroups: Int, gr: Int, kGroups: Int, kRatio: Int,
-        headDim: Int, capacity: Int, row0: Int, pos0: Int, theta: Float, originFirst: Bool,
-        stream: UnsafeMutableRawPointer?
+        headDim: Int, capacity: Int, row0: Int, pos0: Int, theta: Float,
+        positionScale: Float = 1, originFirst: Bool, stream: UnsafeMutableRawPointer?
     ) -> MotifHIPStatus {
-        let rc = motif_rope_split4(qProj, kProj, vProj, q1, q2, k1, k2, v1, v2, dtype.rawValue,
-                                   Int32(batch), Int32(seqLen), Int32(qGroups), Int32(gr),
-                                   Int32(kGroups), Int32(kRatio), Int32(headDim),
-                                   Int32(capacity), Int32(row0), Int32(pos0), theta,
-                                   originFirst ? 1 : 0, stream)
+        let rc = motif_rope_split4_scaled(qProj, kProj, vProj, q1, q2, k1, k2, v1, v2,
+                                          dtype.rawValue, Int32(batch), Int32(seqLen),
+                                          Int32(qGroups), Int32(gr), Int32(kGroups),
+                                          Int32(kRatio), Int32(headDim), Int32(capacity),
+                                          Int32(row0), Int32(pos0), theta, positionScale,
+                                          originFirst ? 1 : 0, stream)
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
@@ -269,8 +290,9 @@ public enum MotifHIP {
     /// written into the 4-slot fp cache, the origin (q1 over k1) and noise
     /// (q2 over k2) dual-V passes with the bottom-right causal mask
     /// (fp16/bf16 cache, head_dim 128; other shapes return .unsupported:
-    /// compose ropeSplit4 and the multi-row sdpa calls).  Only unscaled
-    /// RoPE: check the model's rope_scaling is nil first.
+    /// compose ropeSplit4 and the multi-row sdpa calls).  positionScale: 1,
+    /// or 1 / factor for a "linear" rope_scaling config
+    /// (ropePositionScale); other scaling types are not built.
     public static func gdaPrefillFromProjections(
         qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
         keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
@@ -278,23 +300,24 @@ public enum MotifHIP {
         outputOrigin: UnsafeMutableRawPointer, outputNoise: UnsafeMutableRawPointer,
         dtype: MotifHIPDType, batch: Int, seqLen: Int, qGroups: Int, gr: Int, kGroups: Int,
         headDim: Int, kvCapacity: Int, offset: Int, scale: Float, theta: Float,
-        originFirst: Bool, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
-        stream: UnsafeMutableRawPointer?
+        positionScale: Float = 1, originFirst: Bool, workspace: UnsafeMutableRawPointer?,
+        workspaceBytes: Int, stream: UnsafeMutableRawPointer?
     ) -> MotifHIPStatus {
-        let rc = motif_gda_prefill_proj(qProj, kProj, vProj, keys1, keys2, value1, value2,
-                                        outputOrigin, outputNoise, dtype.rawValue, Int32(batch),
-                                        Int32(seqLen), Int32(qGroups), Int32(gr), Int32(kGroups),
-                                        Int32(headDim), Int32(kvCapacity), Int32(offset), scale,
-                                        theta, originFirst ? 1 : 0, workspace, workspaceBytes,
-                                        stream)
+        let rc = motif_gda_prefill_proj_scaled(qProj, kProj, vProj, keys1, keys2, value1, value2,
+                                               outputOrigin, outputNoise, dtype.rawValue,
+                                               Int32(batch), Int32(seqLen), Int32(qGroups),
+                                               Int32(gr), Int32(kGroups), Int32(headDim),
+                                               Int32(kvCapacity), Int32(offset), scale, theta,
+                                               positionScale, originFirst ? 1 : 0, workspace,
+                                               workspaceBytes, stream)
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
     /// A layer's decode attention from the projection outputs: RoPE at
     /// position kvLen - 1, the head split and the token's cache rows inside
     /// the attention launch (fp16/bf16 cache, head_dim 128; other shapes
-    /// return .unsupported: compose ropeSplit4 and gdaDecode).  Only
-    /// unscaled RoPE: check the model's rope_scaling is nil first.
+    /// return .unsupported: compose ropeSplit4 and gdaDecode).
+    /// positionScale: 1, or 1 / factor for a "linear" rope_scaling config.
     public static func gdaDecodeFromProjections(
         qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
         keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
@@ -302,16 +325,17 @@ public enum MotifHIP {
         sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
         oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
         dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int,
-        kvCapacity: Int, kvLen: Int, scale: Float, theta: Float, originFirst: Bool,
-        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        kvCapacity: Int, kvLen: Int, scale: Float, theta: Float, positionScale: Float = 1,
+        originFirst: Bool, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
         stream: UnsafeMutableRawPointer?
     ) -> MotifHIPStatus {
-        let rc = motif_gda_decode_proj(qProj, kProj, vProj, keys1, keys2, value1, value2,
-                                       sublnWeight, lambdaFull, oneMinusLambdaInit, eps, output,
-                                       dtype.rawValue, Int32(batch), Int32(kvHeads), Int32(gr),
-                                       Int32(headDim), Int32(kvCapacity), Int32(kvLen), scale,
-                                       theta, originFirst ? 1 : 0, workspace, workspaceBytes,
-                                       stream)
+        let rc = motif_gda_decode_proj_scaled(qProj, kProj, vProj, keys1, keys2, value1, value2,
+                                              sublnWeight, lambdaFull, oneMinusLambdaInit, eps,
+                                              output, dtype.rawValue, Int32(batch),
+                                              Int32(kvHeads), Int32(gr), Int32(headDim),
+                                              Int32(kvCapacity), Int32(kvLen), scale, theta,
+                                              positionScale, originFirst ? 1 : 0, workspace,
+                                              workspaceBytes, stream)
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
@@ -320,7 +344,7 @@ public enum MotifHIP {
     /// the four triples inside the attention launch (fp16 scales, head_dim
     /// 128; other shapes return .unsupported: compose ropeSplit4 and
     /// gdaDecodeQuantizedAppend, which give the same values bit for bit).
-    /// Only unscaled RoPE: check the model's rope_scaling is nil first.
+    /// positionScale: 1, or 1 / factor for a "linear" rope_scaling config.
     public static func gdaDecodeQuantizedFromProjections(
         qProj: UnsafeRawPointer, kProj: UnsafeRawPointer, vProj: UnsafeRawPointer,
         keys1: MotifHIPQuantizedTriple, keys2: MotifHIPQuantizedTriple,
@@ -329,10 +353,10 @@ public enum MotifHIP {
         oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
         dtype: MotifHIPDType, batch: Int, kvHeads: Int, gr: Int, headDim: Int,
         kvCapacity: Int, kvLen: Int, bits: Int, groupSize: Int, scale: Float, theta: Float,
-        originFirst: Bool, workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
-        stream: UnsafeMutableRawPointer?
+        positionScale: Float = 1, originFirst: Bool, workspace: UnsafeMutableRawPointer?,
+        workspaceBytes: Int, stream: UnsafeMutableRawPointer?
     ) -> MotifHIPStatus {
-        let rc = motif_gda_decode_q_proj(qProj, kProj, vProj,
+        let rc = motif_gda_decode_q_proj_scaled(qProj, kProj, vProj,
                                          keys1.data, keys1.scales, keys1.biases,
                                          keys2.data, keys2.scales, keys2.biases,
                                          value1.data, value1.scales, value1.biases,
@@ -341,8 +365,8 @@ public enum MotifHIP {
                                          output, dtype.rawValue, Int32(batch), Int32(kvHeads),
                                          Int32(gr), Int32(headDim), Int32(kvCapacity),
                                          Int32(kvLen), Int32(bits), Int32(groupSize), scale,
-                                         theta, originFirst ? 1 : 0, workspace, workspaceBytes,
-                                         stream)
+                                         theta, positionScale, originFirst ? 1 : 0, workspace,
+                                         workspaceBytes, stream)
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 

@@ -48,12 +48,15 @@ public struct MotifHIPAttentionShape {
     public var headDim: Int
     public var activations: MotifHIPDType
     public var theta: Float
+    /// RoPE position scale: 1, or MotifHIP.ropePositionScale of the model's
+    /// rope_scaling config.
+    public var positionScale: Float
     public var originFirst: Bool
     public var scale: Float
 
     public init(batch: Int, qGroups: Int, gr: Int, kGroups: Int, headDim: Int,
-                activations: MotifHIPDType, theta: Float, originFirst: Bool = false,
-                scale: Float? = nil) {
+                activations: MotifHIPDType, theta: Float, positionScale: Float = 1,
+                originFirst: Bool = false, scale: Float? = nil) {
         self.batch = batch
         self.qGroups = qGroups
         self.gr = gr
@@ -61,6 +64,7 @@ public struct MotifHIPAttentionShape {
         self.headDim = headDim
         self.activations = activations
         self.theta = theta
+        self.positionScale = positionScale
         self.originFirst = originFirst
         self.scale = scale ?? 1.0 / Float(headDim).squareRoot()
     }
@@ -243,7 +247,8 @@ public final class MotifHIPGroupedAttention {
                 oneMinusLambdaInit: oneMinusLambdaInit, eps: eps, output: output, dtype: dtype,
                 batch: shape.batch, kvHeads: shape.kGroups, gr: shape.gr,
                 headDim: shape.headDim, kvCapacity: cache.capacity, kvLen: kvLen,
-                scale: shape.scale, theta: shape.theta, originFirst: shape.originFirst,
+                scale: shape.scale, theta: shape.theta, positionScale: shape.positionScale,
+                originFirst: shape.originFirst,
                 workspace: workspace, workspaceBytes: workspaceBytes, stream: stream)
             if status == .unsupported {
                 telemetry.record("decode: rope_split4 + gda_decode")
@@ -256,7 +261,8 @@ public final class MotifHIPGroupedAttention {
                     dtype: dtype, batch: shape.batch, seqLen: 1, qGroups: shape.qGroups,
                     gr: shape.gr, kGroups: shape.kGroups, kRatio: 1, headDim: shape.headDim,
                     capacity: cache.capacity, row0: cache.offset, pos0: cache.offset,
-                    theta: shape.theta, originFirst: shape.originFirst, stream: stream)
+                    theta: shape.theta, positionScale: shape.positionScale,
+                    originFirst: shape.originFirst, stream: stream)
                 if status == .ok {
                     status = MotifHIP.gdaDecode(
                         originQueries: q1, noiseQueries: q2, keys1: cache.slot(0),
@@ -278,7 +284,8 @@ public final class MotifHIPGroupedAttention {
                 dtype: shape.activations, batch: shape.batch, kvHeads: shape.kGroups,
                 gr: shape.gr, headDim: shape.headDim, kvCapacity: cache.capacity,
                 kvLen: kvLen, bits: bits, groupSize: groupSize, scale: shape.scale,
-                theta: shape.theta, originFirst: shape.originFirst, workspace: workspace,
+                theta: shape.theta, positionScale: shape.positionScale,
+                originFirst: shape.originFirst, workspace: workspace,
                 workspaceBytes: workspaceBytes, stream: stream)
             if status == .unsupported {
                 // The token's roped rows as plain (B, H, 1, D) tensors, then
@@ -297,7 +304,8 @@ public final class MotifHIPGroupedAttention {
                     v1: v1, v2: v2, dtype: shape.activations, batch: shape.batch, seqLen: 1,
                     qGroups: shape.qGroups, gr: shape.gr, kGroups: shape.kGroups, kRatio: 1,
                     headDim: shape.headDim, capacity: 1, row0: 0, pos0: cache.offset,
-                    theta: shape.theta, originFirst: shape.originFirst, stream: stream)
+                    theta: shape.theta, positionScale: shape.positionScale,
+                    originFirst: shape.originFirst, stream: stream)
                 if status == .ok {
                     status = MotifHIP.gdaDecodeQuantizedAppend(
                         originQueries: q1, noiseQueries: q2, newKeys1: k1, newKeys2: k2,
@@ -345,7 +353,8 @@ public final class MotifHIPGroupedAttention {
             outputNoise: yNoise, dtype: dtype, batch: shape.batch, seqLen: seqLen,
             qGroups: shape.qGroups, gr: shape.gr, kGroups: shape.kGroups,
             headDim: shape.headDim, kvCapacity: cache.capacity, offset: cache.offset,
-            scale: shape.scale, theta: shape.theta, originFirst: shape.originFirst,
+            scale: shape.scale, theta: shape.theta, positionScale: shape.positionScale,
+            originFirst: shape.originFirst,
             workspace: workspace, workspaceBytes: workspaceBytes, stream: stream)
         if status == .unsupported {
             telemetry.record("prefill: no fused kernel for this shape")

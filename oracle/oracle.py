@@ -330,16 +330,19 @@ def lambda_full(lq1, lk1, lq2, lk2, lam_init: float) -> float:
 # ----------------------------------------------------------------- RoPE ---
 
 
-def rope(x, pos0: int, theta: float = 10000.0) -> np.ndarray:
+def rope(x, pos0: int, theta: float = 10000.0, scale: float = 1.0) -> np.ndarray:
     """Non-traditional RoPE (model.py:413-419: initialize_rope(head_dim,
-    traditional=False, no scaling); applied at model.py:590-594) on x
-    (B, S, H, D) in float64: channel pairs (i, i + D/2) rotated by
-    (pos0 + s) * theta^(-2i/D)."""
+    traditional=False, scaling_config=rope_scaling); applied at
+    model.py:590-594) on x (B, S, H, D) in float64: channel pairs (i, i + D/2)
+    rotated by (scale * (pos0 + s)) * theta^(-2i/D).  scale is 1 unscaled and
+    1 / factor for a "linear" scaling config (mlx-lm's initialize_rope builds
+    nn.RoPE(..., scale=1 / factor) for it)."""
     x = np.asarray(x, np.float64)
     B, S, H, D = x.shape
     half = D // 2
     inv = theta ** (-np.arange(half, dtype=np.float64) * 2.0 / D)
-    ang = (pos0 + np.arange(S, dtype=np.float64))[:, None] * inv[None, :]  # (S, half)
+    pos = (pos0 + np.arange(S, dtype=np.float64)) * float(scale)
+    ang = pos[:, None] * inv[None, :]  # (S, half)
     c = np.cos(ang)[None, :, None, :]
     s_ = np.sin(ang)[None, :, None, :]
     x1, x2 = x[..., :half], x[..., half:]
@@ -347,7 +350,7 @@ def rope(x, pos0: int, theta: float = 10000.0) -> np.ndarray:
 
 
 def rope_split4(q, k, v, q_groups: int, gr: int, k_groups: int, kr: int, pos0: int,
-                theta: float = 10000.0, origin_first: bool = False):
+                theta: float = 10000.0, origin_first: bool = False, scale: float = 1.0):
     """model.py:580-594 (reshape to heads, rope q and k), 620-629 (k1/k2 and
     v1/v2 split of the 4-slot cache write) and 669-679 (q1/q2 split).  q (B,
     S, HQ*D), k (B, S, HK*D), v (B, S, 2*k_groups*D).  Returns float64
@@ -357,8 +360,9 @@ def rope_split4(q, k, v, q_groups: int, gr: int, k_groups: int, kr: int, pos0: i
     HQ = q_groups * (gr + 1)
     HK = k_groups * (kr + 1)
     D = q.shape[-1] // HQ
-    qr = rope(q.reshape(B, S, HQ, D), pos0, theta).transpose(0, 2, 1, 3)  # (B, HQ, S, D)
-    kr_ = rope(np.asarray(k, np.float64).reshape(B, S, HK, D), pos0, theta).transpose(0, 2, 1, 3)
+    qr = rope(q.reshape(B, S, HQ, D), pos0, theta, scale).transpose(0, 2, 1, 3)  # (B, HQ, S, D)
+    kr_ = rope(np.asarray(k, np.float64).reshape(B, S, HK, D), pos0, theta,
+               scale).transpose(0, 2, 1, 3)
     vv = np.asarray(v, np.float64).reshape(B, S, 2 * k_groups, D).transpose(0, 2, 1, 3)
     if origin_first:
         q1, q2 = qr[:, : q_groups * gr], qr[:, q_groups * gr:]
@@ -375,18 +379,19 @@ def rope_split4(q, k, v, q_groups: int, gr: int, k_groups: int, kr: int, pos0: i
 
 def gda_prefill_from_proj(q, k, v, caches, offset: int, q_groups: int, gr: int, k_groups: int,
                           scale: float, theta: float = 10000.0, origin_first: bool = False,
-                          dtype: str = "f16"):
+                          dtype: str = "f16", position_scale: float = 1.0):
     """A GDA layer's prefill chunk on the k_ratio-1 fallback path: rope q and k
     at positions offset + s (model.py:590-594), split and write the 4-slot
     cache rows offset .. offset + S - 1 (model.py:620-629, update_and_fetch_4),
     split q1/q2 (model.py:669-679), then the four causal SDPA calls, concatenated
     per pass (model.py:769-797): origin = [q1 over (k1, V1) || q1 over (k1, V2)],
-    noise = the same for q2 over k2.  The roped q/k are rounded to ``dtype``
+    noise = the same for q2 over k2 (positions scaled by ``position_scale``
+    for a linear RoPE scaling config).  The roped q/k are rounded to ``dtype``
     (the reference's rope output has the activation dtype).  ``caches`` is
     (k1, k2, v1, v2), each (B, k_groups, cap, D).  Returns float64 (y_origin,
     y_noise, the four written cache slots)."""
     q1, q2, k1n, k2n, v1n, v2n = rope_split4(q, k, v, q_groups, gr, k_groups, 1, offset, theta,
-                                             origin_first)
+                                             origin_first, position_scale)
 
     def rnd(x):
         return round_to(x, dtype).astype(np.float64)

@@ -86,6 +86,18 @@ def test_quant_and_epilogue_rejections():
     assert lib.motif_polynorm(None, None, None, None, 5, 3, 16, 1e-6, None) == -1
 
 
+@pytest.mark.parametrize("pscale", [0.0, -0.5, float("inf"), float("nan")])
+def test_rope_position_scale_rejections(pscale):
+    lib = _native.lib()
+    st = lib.motif_rope_split4_scaled(*[None] * 9, 0, 1, 1, 8, 4, 8, 1, 128, 1, 0, 5, 1e4,
+                                      pscale, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "position_scale" in _err()
+    # a valid scale gets past the check to the null-pointer one
+    st = lib.motif_rope_split4_scaled(*[None] * 9, 0, 1, 1, 8, 4, 8, 1, 128, 1, 0, 5, 1e4,
+                                      0.5, 0, None)
+    assert st == _native.MOTIF_ERR_CONTRACT and "null pointer" in _err()
+
+
 def test_empty_work_is_a_no_op():
     lib = _native.lib()
     assert lib.motif_polynorm(None, None, None, None, 0, 0, 16, 1e-6, None) == 0

@@ -131,11 +131,13 @@ def test_swift_calls_match_the_c_declarations():
         assert name in decls, f"Swift calls {name}, which the header does not declare"
         assert len(args) == decls[name], (
             f"Swift call of {name} passes {len(args)} arguments, the header takes {decls[name]}")
-    # Every decode, attention and RoPE entry point has a Swift face.
+    # Every decode, attention and RoPE entry point has a Swift face (the RoPE
+    # ones through their position-scaled forms, which take scale 1 by default).
     called = {n for n, _ in calls}
     for name in ("motif_sdpa_dual_v", "motif_sdpa_dual_v_q", "motif_gda_decode",
                  "motif_gda_decode_q", "motif_gda_decode_append", "motif_gda_decode_q_append",
-                 "motif_gda_decode_proj", "motif_gda_decode_q_proj", "motif_rope_split4",
+                 "motif_gda_decode_proj_scaled", "motif_gda_decode_q_proj_scaled",
+                 "motif_rope_split4_scaled", "motif_gda_prefill_proj_scaled",
                  "motif_gda_post_split", "motif_polynorm", "motif_quant_write4"):
         assert name in called, f"no Swift wrapper calls {name}"
 

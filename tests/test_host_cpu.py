@@ -426,23 +426,47 @@ def test_decode_q_slot_contract(enabled, rng, bits):
         step(_q_trips(B, H_kv, cap, D, bits, gs))
 
 
-def test_rope_scaling_is_rejected(rng, monkeypatch):
-    """A scaled RoPE config (the reference's grouped fixture uses linear
-    scaling, factor 2) is refused by every RoPE wrapper, kernels or not,
-    instead of roping at unscaled positions."""
-    scaling = {"rope_type": "linear", "factor": 2.0, "original_max_position_embeddings": 64}
+def test_rope_scaling_configs(rng, monkeypatch):
+    """RoPE scaling configs are read as mlx-lm's initialize_rope reads them:
+    None and "default" rope at unscaled positions, "linear" (the reference's
+    grouped fixture: factor 2) at positions / factor, and every other type
+    is refused by every RoPE wrapper, kernels or not, instead of roping at
+    the wrong positions."""
+    from mlx_motif.kernels.rope import rope_position_scale
+
+    linear = {"rope_type": "linear", "factor": 2.0, "original_max_position_embeddings": 64}
+    assert rope_position_scale(None) == 1.0
+    assert rope_position_scale({"rope_type": "default"}) == 1.0
+    assert rope_position_scale(linear) == 0.5
+    assert rope_position_scale({"type": "linear", "factor": 4.0}) == 0.25
+    with pytest.raises(ValueError):
+        rope_position_scale({"type": "linear", "factor": 0.0})
+    llama3 = {"rope_type": "llama3", "factor": 8.0, "low_freq_factor": 1.0,
+              "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
     q_proj, k_proj, v_proj = _t(rng, (1, 1, 640)), _t(rng, (1, 1, 256)), _t(rng, (1, 1, 256))
     caches = [_t(rng, (1, 2, 8, 64)) for _ in range(4)]
     w, lam = _t(rng, (128,)), torch.tensor([0.5])
     for flag in (True, False):
         monkeypatch.setattr(_common, "_DISABLE", flag)
-        with pytest.raises(NotImplementedError, match="rope_scaling"):
-            K.rope_split4(q_proj, k_proj, v_proj, 2, 4, 2, 1, 3, rope_scaling=scaling)
-        with pytest.raises(NotImplementedError, match="rope_scaling"):
+        with pytest.raises(NotImplementedError, match="llama3"):
+            K.rope_split4(q_proj, k_proj, v_proj, 2, 4, 2, 1, 3, rope_scaling=llama3)
+        with pytest.raises(NotImplementedError, match="llama3"):
             K.gda_decode_attention_from_proj(q_proj, k_proj, v_proj, *caches, 0.1, w, lam, 0.2, 4,
-                                             3, rope_scaling=scaling)
-        with pytest.raises(NotImplementedError, match="rope_scaling"):
+                                             3, rope_scaling=llama3)
+        with pytest.raises(NotImplementedError, match="llama3"):
             K.gda_decode_attention_q4_from_proj(q_proj, k_proj, v_proj,
                                                 *_q_trips(1, 2, 8, 64, 4, 64), 0.1, w, lam, 0.2,
-                                                4, 3, rope_scaling=scaling)
-    K.rope_split4_reference(q_proj, k_proj, v_proj, 2, 4, 2, 1, 3)  # unscaled still runs
+                                                4, 3, rope_scaling=llama3)
+    # The torch statement under linear scaling: position p at scale 1/2 is
+    # position p / 2 unscaled (even p), and matches the float64 oracle.
+    monkeypatch.setattr(_common, "_DISABLE", True)
+    q4, k4, v4 = _t(rng, (1, 4, 640)), _t(rng, (1, 4, 256)), _t(rng, (1, 4, 256))
+    scaled = K.rope_split4(q4, k4, v4, 2, 4, 2, 1, 6, rope_scaling=linear)
+    plain = [K.rope_split4_reference(q4[:, s:s + 1], k4[:, s:s + 1], v4[:, s:s + 1], 2, 4, 2, 1,
+                                     (6 + s) // 2) for s in (0, 2)]
+    for s, ref in zip((0, 2), plain):
+        for a, b in zip(scaled[:4], ref[:4]):
+            np.testing.assert_array_equal(a[:, :, s:s + 1].float().numpy(), b.float().numpy())
+    oq1, *_ = O.rope_split4(q4.numpy(), k4.numpy(), v4.numpy(), 2, 4, 2, 1, 6, scale=0.5)
+    assert np.max(np.abs(scaled[0].double().numpy() - oq1)) <= 2 * 2.0 ** -10 * (
+        1 + np.max(np.abs(oq1)))

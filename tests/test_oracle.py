@@ -428,3 +428,16 @@ def test_vectorised_c_port_matches_scalar_build():
     a = c_oracle.sdpa_dual_v_q_f16(q, *trips, 128 ** -0.5, 64, 4, 650)
     b = c_oracle.sdpa_dual_v_q_f16(q, *trips, 128 ** -0.5, 64, 4, 650, fast=True)
     assert np.max(np.abs(a - b)) <= 1e-5
+
+
+def test_rope_linear_scaling_pins():
+    """The oracle's RoPE position scale (a "linear" scaling config of factor f
+    ropes position p at p / f): at scale 1/2 position 2p equals position p
+    unscaled, scale 1 is the unscaled RoPE, and scale 2 (the inverse, a
+    plausible mistake) differs."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((1, 1, 3, 64))
+    for p in (0, 7, 1601):
+        np.testing.assert_allclose(O.rope(x, 2 * p, scale=0.5), O.rope(x, p), rtol=0, atol=1e-12)
+        np.testing.assert_array_equal(O.rope(x, p, scale=1.0), O.rope(x, p))
+    assert np.max(np.abs(O.rope(x, 10, scale=2.0) - O.rope(x, 5))) > 1e-3
