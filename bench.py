@@ -662,7 +662,8 @@ def summarize_traffic(kind: str, fetch_dir: str, write_dir: str) -> int:
 
 def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
     """The other rows' headline shapes, timed as the decode calls are (graph
-    replay, HIP events): the fused GDA decode step at 16k, the 5-row verify
+    replay, HIP events): the fused GDA decode step at 16k and, with the
+    token's write, at 3204 over 48 layer caches, the 5-row verify
     slabs over 32768 rows (fp16 and q8), the 512-row prefill chunk over 3716
     rows and a 12.7B layer's 512-row chunk at offset 3204 from the
     projections (RoPE + 4-slot write + both passes in one launch)."""
@@ -704,6 +705,13 @@ def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
     calls, keep = make_decode_calls(torch, lib, dev, 6, fused=True)
     hbm("gda_decode_step_f16_kv16000", timed(calls), decode_bytes(KV_LEN, True))
     del calls, keep
+    # the 12.7B layer's decode step at kv 3204 with the token's row written
+    # inside the launch, over 48 distinct layer caches
+    calls, keep = make_decode_calls(torch, lib, dev, 48, kv_len=3204, cap=3328, append="fused")
+    hbm("gda_decode_step_append_f16_kv3204_x48_layers", timed(calls, 48 * 4),
+        decode_bytes(3204, True))
+    del calls, keep
+    torch.cuda.empty_cache()
     # the packed 16k decode with bf16 activations, scales and biases
     for bits, nsets in ((4, 24), (8, 16)):
         calls, keep = make_q_calls(torch, lib, dev, nsets, bits, bf16=True)

@@ -311,8 +311,11 @@ struct GdaDecodeLayout {
 static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int D) {
   GdaDecodeLayout L{};
   // One virtual head per KV head in the planner: the fused kernel runs one
-  // workgroup per (b, KV head, split), like the unfused origin pass.
-  L.plan = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, 0, 0);
+  // workgroup per (b, KV head, split), like the unfused origin pass; 4-wave
+  // workgroups, one per CU, for short contexts (kShortDecodeRows), as the
+  // single-pass call takes them.
+  const bool short4 = kv_len <= kShortDecodeRows;
+  L.plan = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, short4 ? 4 : 0, short4 ? 1 : 0);
   L.plan_q = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu);
   const int ns = L.plan.nsplit > L.plan_q.nsplit ? L.plan.nsplit : L.plan_q.nsplit;
   const size_t prow = (size_t)B * Hkv * (gr + 1);
@@ -498,8 +501,9 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
     const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
     rc = check_partials(name, a, true);
     if (rc != MOTIF_OK) return rc;
-    return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks, s)
-                              : launch_gda_decode_bf16(a, gda_columns(gr), nblocks, s);
+    const int waves = L.plan.waves;
+    return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), waves, nblocks, s)
+                              : launch_gda_decode_bf16(a, gda_columns(gr), waves, nblocks, s);
   }
   if (new_kv) {  // row kv_len - 1 of each slot: B * Hkv rows of D values
     const size_t row = (size_t)D * (dtype == MOTIF_F32 ? 4 : 2);
@@ -599,9 +603,9 @@ int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const v
   const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
   rc = check_partials(name, a, true);
   if (rc != MOTIF_OK) return rc;
-  return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), nblocks,
+  return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), L.plan.waves, nblocks,
                                                     (hipStream_t)stream)
-                            : launch_gda_decode_bf16(a, gda_columns(gr), nblocks,
+                            : launch_gda_decode_bf16(a, gda_columns(gr), L.plan.waves, nblocks,
                                                      (hipStream_t)stream);
 }
 

@@ -106,11 +106,11 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
 // passes, then the merge + gda_post_split launch.  Compiled for the fp16 and
 // bf16 caches at head_dim 128 only; the entry point composes the separate
 // calls otherwise.
-int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int nblocks,
-                                               hipStream_t s) {
+int MOTIF_CAT(launch_gda_decode_, MOTIF_SUFFIX)(const SdpaArgs& a, int gc, int waves,
+                                               int nblocks, hipStream_t s) {
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
                 std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    const int rc = launch_gda_decode_mfma_16<MOTIF_ELEM>(a, gc, nblocks, s);
+    const int rc = launch_gda_decode_mfma_16<MOTIF_ELEM>(a, gc, waves, nblocks, s);
     if (rc != MOTIF_OK) return rc;
     return launch_gda_decode_merge_d<MOTIF_ELEM, 128>(a, s);
   }

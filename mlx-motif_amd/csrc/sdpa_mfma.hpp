@@ -468,13 +468,25 @@ inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks
 }
 
 // Fused GDA decode step, 16-bit cache, head_dim 128: gc = columns (G + 1,
-// rounded up to 2, 4, 8 or 16).
+// rounded up to 2, 4, 8 or 16); waves 8, or 4 (short contexts: one
+// workgroup per CU reaches its first tile sooner).  16 columns: always 4.
 template <typename T>
-inline int launch_gda_decode_mfma_16(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
+inline int launch_gda_decode_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks,
+                                     hipStream_t st) {
+  const bool w8 = waves == 8;
   switch (gc) {
-    case 2: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a); break;
+    case 2:
+      if (w8) hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a);
+      break;
+    case 4:
+      if (w8) hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a);
+      break;
+    case 8:
+      if (w8) hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 8, 2, true>), dim3(nblocks), dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a);
+      break;
     case 16: hipLaunchKernelGGL((sdpa_mfma_kernel<T, 16, 4, 2, true>), dim3(nblocks), dim3(256), 0, st, a); break;
     default:
       set_error("gda_decode: no fused variant for %d columns", gc);

@@ -214,7 +214,9 @@ inline bool tile_softmax_scale_ok(float qscale) {
 // the smaller blocks reach their first tile sooner (32 q-heads over 8 KV
 // heads, D 128, µs per call 8 / 4 waves: 1024 rows 8.84 / 7.51, 2048 9.08 /
 // 8.07, 3204 9.59 / 9.20, 4096 9.97 / 9.69, 6144 12.19 / 12.09, 8192 13.59 /
-// 14.03).
+// 14.03).  The fused decode step (both passes over k1/k2/v1/v2, the
+// token's row written inside the launch) follows the same rule: 1024 rows
+// 12.58 / 10.25, 2048 12.74 / 11.03, 3204 13.92 / 13.47, 4096 14.32 / 13.96.
 constexpr int kShortDecodeRows = 4096;
 
 // Plan of the packed-cache matrix-core kernel (head_dim 128, fp16): 4-wave
