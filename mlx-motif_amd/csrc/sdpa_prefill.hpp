@@ -140,21 +140,29 @@ struct SwizzledTileAcc {
   // select (m_run starts at the finite sentinel and only grows).  The
   // maximum is taken over the unscaled scores (qscale > 0, so scaling it
   // gives the maximum of the scaled ones bit for bit) and each weight is
-  // exp2(fma(s, qscale, -m)).
+  // exp2(fma(s, qscale, -m)).  full (wave-uniform): every row of the tile is
+  // visible to every column of the wave, so no row is masked.
   __device__ __forceinline__ V8 softmax(const floatx4 (&sacc)[2], int row0, int r_end, int lim,
-                                        float qscale, int blk) {
+                                        float qscale, int blk, bool full) {
     float sc[8];
-    float mx = -__builtin_inff();
-    // row 16*h + 4*blk + r of the tile is visible while 16*h + r < vis
-    const int vis = min(r_end, lim) - row0 - 4 * blk;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sc[4 * h + r] = 16 * h + r < vis ? sacc[h][r] : -__builtin_inff();
-        mx = fmaxf(mx, sc[4 * h + r]);
+      for (int r = 0; r < 4; ++r) sc[4 * h + r] = sacc[h][r];
+    }
+    if (!full) {
+      asm volatile("");  // keep this a branch: only tiles at a limit take it
+      // row 16*h + 4*blk + r of the tile is visible while 16*h + r < vis
+      const int vis = min(r_end, lim) - row0 - 4 * blk;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sc[4 * h + r] = 16 * h + r < vis ? sc[4 * h + r] : -__builtin_inff();
       }
     }
+    float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                     fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
     mx = fmaxf(rows4_max(mx) * qscale, kNegSentinel);
     if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
       const float m_new = fmaxf(m_run, mx);
@@ -209,18 +217,18 @@ struct SwizzledTileAcc {
   // Mask, online softmax and both PV products of a tile with scores sacc.
   __device__ __forceinline__ void update(const floatx4 (&sacc)[2], const uint8_t* V1t,
                                          const uint8_t* V2t, int row0, int r_end, int lim,
-                                         float qscale, int col, int blk) {
-    const V8 pb = softmax(sacc, row0, r_end, lim, qscale, blk);
+                                         float qscale, int col, int blk, bool full) {
+    const V8 pb = softmax(sacc, row0, r_end, lim, qscale, blk, full);
     pv(pb, V1t, V2t, col, blk);
   }
 
   // One tile: scores() then update().
   __device__ __forceinline__ void tile(const uint8_t* Kt, const uint8_t* V1t, const uint8_t* V2t,
                                        const V8 (&qb)[4], int row0, int r_end, int lim,
-                                       float qscale, int col, int blk) {
+                                       float qscale, int col, int blk, bool full) {
     floatx4 sacc[2];
     scores(Kt, qb, sacc, col, blk);
-    update(sacc, V1t, V2t, row0, r_end, lim, qscale, col, blk);
+    update(sacc, V1t, V2t, row0, r_end, lim, qscale, col, blk, full);
   }
 
   // Column vrow's result: y (normalised, nsplit == 1) or its split partial.
@@ -419,6 +427,16 @@ sdpa_prefill_kernel(SdpaArgs a) {
     col_ok[cb] = vh[cb] < a.GV;
     lim[cb] = col_ok[cb] ? vhead_limit(a, vh[cb]) : 0;
   }
+  // Smallest limit over the wave's valid columns of each block: tiles ending
+  // at or before it (and before r_end) need no mask.
+  int lim_lo[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int v0 = wg_vh0 + (wave * NCB + cb) * 16;
+    int hi;
+    vhead_limit_range(a, v0, min(16, a.GV - v0), lim_lo[cb], hi);
+    lim_lo[cb] = __builtin_amdgcn_readfirstlane(lim_lo[cb]);
+  }
   const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16 * NCB, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
@@ -521,8 +539,9 @@ sdpa_prefill_kernel(SdpaArgs a) {
         if (wave_busy) SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb[0], s_nxt, col, blk);
       }
       if (wave_busy) {
-        st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], r_begin + i * TR, r_end,
-                         lim[0], a.qscale, col, blk);
+        const int t0 = r_begin + i * TR;
+        st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], t0, r_end, lim[0], a.qscale,
+                         col, blk, t0 + TR <= min(r_end, lim_lo[0]));
         s_cur[0] = s_nxt[0];
         s_cur[1] = s_nxt[1];
       }
@@ -534,9 +553,11 @@ sdpa_prefill_kernel(SdpaArgs a) {
       floatx4 sacc[NCB][2];
       tile_scores_n<T, NCB>(ring[i % NS][0], qb, sacc, col, blk);
       V8 pb[NCB];
+      const int t0 = r_begin + i * TR;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb)
-        pb[cb] = st_acc[cb].softmax(sacc[cb], r_begin + i * TR, r_end, lim[cb], a.qscale, blk);
+        pb[cb] = st_acc[cb].softmax(sacc[cb], t0, r_end, lim[cb], a.qscale, blk,
+                                    t0 + TR <= min(r_end, lim_lo[cb]));
       tile_pv_n<T, NCB>(st_acc, pb, ring[i % NS][1], ring[i % NS][2], col, blk);
     }
   }
@@ -672,6 +693,14 @@ gda_prefill_proj_kernel(SdpaArgs a) {
     vh[cb] = wg_vh0 + (wave * NCB + cb) * 16 + col;
     col_ok[cb] = vh[cb] < GV;
     lim[cb] = col_ok[cb] ? vhead_limit(a, vh[cb]) : 0;
+  }
+  int lim_lo[NCB];  // as in sdpa_prefill_kernel
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int v0 = wg_vh0 + (wave * NCB + cb) * 16;
+    int hi;
+    vhead_limit_range(a, v0, min(16, GV - v0), lim_lo[cb], hi);
+    lim_lo[cb] = __builtin_amdgcn_readfirstlane(lim_lo[cb]);
   }
   const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16 * NCB, GV - wg_vh0));
 
@@ -886,8 +915,10 @@ gda_prefill_proj_kernel(SdpaArgs a) {
         publish(i + 1);
         SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qbv[0], s_nxt, col, blk);
       }
-      st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], first_row(i),
-                       is_new_tile(i) ? max_lim : min(row0, max_lim), lim[0], a.qscale, col, blk);
+      const int t0 = first_row(i);
+      const int rl = is_new_tile(i) ? max_lim : min(row0, max_lim);
+      st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], t0, rl, lim[0], a.qscale, col,
+                       blk, t0 + TR <= min(rl, lim_lo[0]));
       s_cur[0] = s_nxt[0];
       s_cur[1] = s_nxt[1];
     }
@@ -898,9 +929,11 @@ gda_prefill_proj_kernel(SdpaArgs a) {
       tile_scores_n<T, NCB>(ring[i % NS][0], qbv, sacc, col, blk);
       V8 pb[NCB];
       const int rl = is_new_tile(i) ? max_lim : min(row0, max_lim);
+      const int t0 = first_row(i);
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb)
-        pb[cb] = st_acc[cb].softmax(sacc[cb], first_row(i), rl, lim[cb], a.qscale, blk);
+        pb[cb] = st_acc[cb].softmax(sacc[cb], t0, rl, lim[cb], a.qscale, blk,
+                                    t0 + TR <= min(rl, lim_lo[cb]));
       tile_pv_n<T, NCB>(st_acc, pb, ring[i % NS][1], ring[i % NS][2], col, blk);
     }
   }

@@ -37,6 +37,14 @@ constexpr int kQslabMergeFloats = 68;
 // Workgroup barrier after this wave's LDS writes completed, without the
 // vector-memory wait of __syncthreads' fence (the packed loads in flight
 // stay in flight; the compiler waits for them where they are used).
+// Smallest row limit over the valid columns of the 16-column block at
+// virtual head v0 (wave-uniform): tiles ending at or before it need no mask.
+__device__ inline int qslab_block_limit_lo(const SdpaArgs& a, int v0) {
+  int lo, hi;
+  vhead_limit_range(a, v0, min(16, a.GV - v0), lo, hi);
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
 __device__ inline void qslab_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
@@ -75,6 +83,7 @@ sdpa_qslab_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + cb * 16 + col;  // this lane's virtual head (column)
   const bool col_ok = vh < a.GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
+  const int lim_lo = qslab_block_limit_lo(a, wg_vh0 + cb * 16);
   const int max_lim = vhead_limit_max(a, wg_vh0, min(NCB * 16, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
@@ -216,8 +225,9 @@ sdpa_qslab_kernel(SdpaArgs a) {
     qslab_barrier();
     auto step = [&](int j, Packed& ld, Packed& nx) {
       load(ld, j + 2);  // ld held step j, dequantised in the step before
-      acc.tile(ring[j & 1][tp][0], ring[j & 1][tp][1], ring[j & 1][tp][2], qb,
-               r_begin + (j * NP + tp) * TR, r_end, lim, a.qscale, col, blk);
+      const int t0 = r_begin + (j * NP + tp) * TR;
+      acc.tile(ring[j & 1][tp][0], ring[j & 1][tp][1], ring[j & 1][tp][2], qb, t0, r_end, lim,
+               a.qscale, col, blk, t0 + TR <= min(r_end, lim_lo));
       dequant_store(nx, (j + 1) & 1);
       qslab_barrier();
     };
@@ -233,8 +243,9 @@ sdpa_qslab_kernel(SdpaArgs a) {
     load(P, 1);
     qslab_barrier();
     for (int j = 0; j < nsteps; ++j) {
-      acc.tile(ring[0][tp][0], ring[0][tp][1], ring[0][tp][2], qb, r_begin + (j * NP + tp) * TR,
-               r_end, lim, a.qscale, col, blk);
+      const int t0 = r_begin + (j * NP + tp) * TR;
+      acc.tile(ring[0][tp][0], ring[0][tp][1], ring[0][tp][2], qb, t0, r_end, lim, a.qscale, col,
+               blk, t0 + TR <= min(r_end, lim_lo));
       qslab_barrier();
       dequant_store(P, 0);  // step j + 1
       load(P, j + 2);
@@ -353,6 +364,7 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   const int vh = wg_vh0 + cb * 16 + col;
   const bool col_ok = !producer && vh < a.GV;
   const int lim = col_ok ? vhead_limit(a, vh) : 0;
+  const int lim_lo = qslab_block_limit_lo(a, wg_vh0 + cb * 16);
   const int max_lim = vhead_limit_max(a, wg_vh0, min(NCB * 16, a.GV - wg_vh0));
   const int r_begin = split * a.rows_per_split;
   const int r_end = min(r_begin + a.rows_per_split, max_lim);
@@ -506,8 +518,9 @@ sdpa_qslab_ws_kernel(SdpaArgs a) {
   }
   qslab_barrier();
   for (int j = 0; j < nsteps; ++j) {
-    acc.tile(ring[j & 1][tp][0], ring[j & 1][tp][1], ring[j & 1][tp][2], qb,
-             r_begin + (j * NP + tp) * TR, r_end, lim, a.qscale, col, blk);
+    const int t0 = r_begin + (j * NP + tp) * TR;
+    acc.tile(ring[j & 1][tp][0], ring[j & 1][tp][1], ring[j & 1][tp][2], qb, t0, r_end, lim,
+             a.qscale, col, blk, t0 + TR <= min(r_end, lim_lo));
     qslab_barrier();
   }
 
