@@ -294,7 +294,7 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
   // Enough for every kernel family a call may take: the fp16/bf16/fp32 and
   // VALU plans and the packed-cache matrix-core plans of each group size.
   size_t ws = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max(D), 0, 0).workspace_bytes;
-  if (D == kSdpaMfmaQD) {
+  if (D == 128 || D == 64) {  // the fp16/bf16 matrix-core kernel's plans
     const size_t w16 =
         plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 0, 0).workspace_bytes;
     if (w16 > ws) ws = w16;
@@ -303,6 +303,8 @@ size_t motif_sdpa_workspace_bytes(int B, int Hq, int Hkv, int S_q, int kv_len, i
           plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, kSdpaMfmaGcMax, 4, 1).workspace_bytes;
       if (w4 > ws) ws = w4;
     }
+  }
+  if (D == kSdpaMfmaQD) {
     for (int gs = 32; gs <= 128; gs *= 2) {
       const int nb = sdpa_q_blocks((Hkv > 0 ? Hq / Hkv : 1) * S_q, D, gs);
       const SdpaPlan p = plan_sdpa(B, Hq, Hkv, S_q, kv_len, D, sdpa_gc_max_q(D, gs),

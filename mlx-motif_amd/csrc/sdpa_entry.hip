@@ -139,7 +139,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // The matrix-core kernel takes up to 16 virtual heads per workgroup (a
   // verify slab's 5 rows x GQA 4 in two head chunks instead of three); the
   // conditions are those under which the dispatch picks that kernel.
-  const bool mfma16 = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
+  const bool mfma16 = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && mfma16_head_dim_ok(D, k) &&
                       tuning().mfma && aligned(q, 16) && kv_len <= kMfmaMaxRows;
   // Short single-row calls: 4-wave workgroups, one per CU (kShortDecodeRows).
   const bool short4 = mfma16 && S_q == 1 && kv_len <= kShortDecodeRows;

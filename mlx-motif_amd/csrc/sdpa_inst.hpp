@@ -18,9 +18,10 @@ int MOTIF_CAT(dispatch_sdpa_fp_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan
   const int nblocks = sdpa_grid_blocks(a.B * a.Hkv, p.nchunk, p.nsplit);
   if constexpr (std::is_same<MOTIF_ELEM, half_t>::value ||
                 std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    if (D == 128 && tuning().mfma && p.gc <= kSdpaMfmaGcMax && ((uintptr_t)a.q & 15u) == 0 &&
-        a.kv_len <= kMfmaMaxRows)
-      return launch_sdpa_mfma_16<MOTIF_ELEM>(a, p.gc, p.waves, nblocks, s);
+    if (mfma16_head_dim_ok(D, a.k) && tuning().mfma && p.gc <= kSdpaMfmaGcMax &&
+        ((uintptr_t)a.q & 15u) == 0 && a.kv_len <= kMfmaMaxRows)
+      return D == 128 ? launch_sdpa_mfma_16<MOTIF_ELEM, 128>(a, p.gc, p.waves, nblocks, s)
+                      : launch_sdpa_mfma_16<MOTIF_ELEM, 64>(a, p.gc, p.waves, nblocks, s);
   }
   switch (D) {
     case 32: return launch_sdpa_gc<FpFmt<MOTIF_ELEM, 32>>(a, p.gc, p.waves, nblocks, s);

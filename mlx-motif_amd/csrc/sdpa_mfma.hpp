@@ -169,13 +169,18 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
 // T: half_t (fp16 cache, v_mfma_f32_16x16x32_f16) or bf16_t (bf16 cache,
 // v_mfma_f32_16x16x32_bf16).  The 16-column single-pass variant keeps the
 // in-kernel merge's LDS (104 KB): one workgroup, one wave per SIMD, per CU.
-template <typename T, int GC, int NW, int U, bool DUAL = false>
+template <typename T, int GC, int NW, int U, bool DUAL = false, int D = 128>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(GC == 16 && !DUAL ? 1 : 2)))
 sdpa_mfma_kernel(SdpaArgs a) {
   using Op = MfmaOp<T>;
   using V8 = typename Op::V8;
-  constexpr int D = 128;
+  // head_dim 128 or 64: NQ k-steps of 32 channels for S^T, and VT dwords
+  // (2 VT channels) of each V row per lane, 2 VT MFMAs per V for O^T.
+  static_assert(D == 128 || D == 64, "head_dim 128 or 64");
+  static_assert(!DUAL || D == 128, "the fused decode step is built for head_dim 128");
+  constexpr int NQ = D / 32;
+  constexpr int VT = D / 32;
   static_assert(GC <= 16, "virtual heads ride the 16 MFMA columns");
   static_assert(U % 2 == 0, "tiles are computed in pairs");
   const int lane = threadIdx.x & 63;
@@ -211,7 +216,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds head col,
   // channels 32*s + 8*blk .. +7 for k-step s.
-  V8 qb[4];
+  V8 qb[NQ];
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
     if constexpr (DUAL) {
@@ -227,7 +232,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
       qp += 8 * blk;
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < NQ; ++s) {
       const uint4 w = col_ok ? *reinterpret_cast<const uint4*>(qp + 32 * s) : make_uint4(0, 0, 0, 0);
       qb[s] = __builtin_bit_cast(V8, w);
     }
@@ -256,9 +261,9 @@ sdpa_mfma_kernel(SdpaArgs a) {
   }
 
 
-  floatx4 acc1[8], acc2[8], accl;
+  floatx4 acc1[2 * VT], acc2[2 * VT], accl;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < 2 * VT; ++j) {
     acc1[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
@@ -295,31 +300,38 @@ sdpa_mfma_kernel(SdpaArgs a) {
         if (has) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the new rows are stored
       }
     }
-    V8 ka[U][4];
-    V8 ka2[DUAL ? U : 1][4];
-    uint32_t v1w[U][4][4], v2w[U][4][4];
+    V8 ka[U][NQ];
+    V8 ka2[DUAL ? U : 1][NQ];
+    uint32_t v1w[U][4][VT], v2w[U][4][VT];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int t0 = tile_row(k0 + u);
       // K rows for S^T: row t0 + col (A operand row = lane % 16).
       const unsigned koff = (unsigned)((t0 + col) * D * 2 + 16 * blk);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ka[u][s] = __builtin_bit_cast(V8, bload4(rk, koff + 64u * s));
+      for (int s = 0; s < NQ; ++s) ka[u][s] = __builtin_bit_cast(V8, bload4(rk, koff + 64u * s));
       if constexpr (DUAL) {
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < NQ; ++s)
           ka2[u][s] = __builtin_bit_cast(V8, bload4(rk2, koff + 64u * s));
       }
-      // V rows t0 + 4*blk + r: 16 bytes per lane, dwords 4*col .. 4*col+3
-      // (dword 4*col + t holds channels 8*col + 2t, +1); one instruction
-      // covers four whole rows.
-      const unsigned voff = (unsigned)((t0 + 4 * blk) * D * 2 + 16 * col);
+      // V rows t0 + 4*blk + r: 4 VT bytes per lane, dwords VT*col ..
+      // VT*col + VT - 1 (dword VT*col + t holds channels 2*VT*col + 2t, +1);
+      // one instruction covers four whole rows.
+      const unsigned voff = (unsigned)((t0 + 4 * blk) * D * 2 + 4 * VT * col);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint4 w1 = bload4(rv1, voff + (unsigned)(r * D * 2));
-        const uint4 w2 = bload4(rv2, voff + (unsigned)(r * D * 2));
-        v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
-        v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
+        if constexpr (VT == 4) {
+          const uint4 w1 = bload4(rv1, voff + (unsigned)(r * D * 2));
+          const uint4 w2 = bload4(rv2, voff + (unsigned)(r * D * 2));
+          v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y; v1w[u][r][2] = w1.z; v1w[u][r][3] = w1.w;
+          v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y; v2w[u][r][2] = w2.z; v2w[u][r][3] = w2.w;
+        } else {
+          const uint2 w1 = bload2(rv1, voff + (unsigned)(r * D * 2));
+          const uint2 w2 = bload2(rv2, voff + (unsigned)(r * D * 2));
+          v1w[u][r][0] = w1.x; v1w[u][r][1] = w1.y;
+          v2w[u][r][0] = w2.x; v2w[u][r][1] = w2.y;
+        }
       }
     }
 
@@ -334,12 +346,12 @@ sdpa_mfma_kernel(SdpaArgs a) {
       for (int v = 0; v < 2; ++v) {
         sacc[v] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < NQ; ++s)
           sacc[v] = Op::mma(ka[u + v][s], qb[s], sacc[v]);
         if constexpr (DUAL) {
           floatx4 s2 = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int s = 0; s < 4; ++s)
+          for (int s = 0; s < NQ; ++s)
             s2 = Op::mma(ka2[u + v][s], qb[s], s2);
           if (col == a.G) sacc[v] = s2;
         }
@@ -364,7 +376,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
         const float m_new = fmaxf(m_run, mx);
         const float fac = fast_exp2(m_run - m_new);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 2 * VT; ++j) {
           acc1[j] *= fac;
           acc2[j] *= fac;
         }
@@ -377,7 +389,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
         pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
 
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int t = 0; t < VT; ++t) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint32_t sel = h ? 0x07060302u : 0x05040100u;  // hi or lo halves, row r in half r%2
@@ -400,23 +412,23 @@ sdpa_mfma_kernel(SdpaArgs a) {
   }
 
   // O^T element (m = 4*blk + r, head col) of MFMA j = 2*t + h is channel
-  // 8*m + j.
+  // 2*VT*m + j.
   __shared__ __attribute__((aligned(16))) float lds_o[NW][GC][2 * D + kLdsPad];
   __shared__ float lds_m[NW][GC];
   __shared__ float lds_l[NW][GC];
   if (col < nvh) {
-    // acc[j][r] is channel 8*m + j with m = 4*blk + r: two float4 per row m.
+    // acc[j][r] is channel 2*VT*m + j with m = 4*blk + r: VT / 2 float4 per
+    // row m.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int ch = 8 * (4 * blk + r);
-      *reinterpret_cast<float4*>(&lds_o[wave][col][ch]) =
-          make_float4(acc1[0][r], acc1[1][r], acc1[2][r], acc1[3][r]);
-      *reinterpret_cast<float4*>(&lds_o[wave][col][ch + 4]) =
-          make_float4(acc1[4][r], acc1[5][r], acc1[6][r], acc1[7][r]);
-      *reinterpret_cast<float4*>(&lds_o[wave][col][D + ch]) =
-          make_float4(acc2[0][r], acc2[1][r], acc2[2][r], acc2[3][r]);
-      *reinterpret_cast<float4*>(&lds_o[wave][col][D + ch + 4]) =
-          make_float4(acc2[4][r], acc2[5][r], acc2[6][r], acc2[7][r]);
+      const int ch = 2 * VT * (4 * blk + r);
+#pragma unroll
+      for (int f = 0; f < VT / 2; ++f) {
+        *reinterpret_cast<float4*>(&lds_o[wave][col][ch + 4 * f]) =
+            make_float4(acc1[4 * f][r], acc1[4 * f + 1][r], acc1[4 * f + 2][r], acc1[4 * f + 3][r]);
+        *reinterpret_cast<float4*>(&lds_o[wave][col][D + ch + 4 * f]) =
+            make_float4(acc2[4 * f][r], acc2[4 * f + 1][r], acc2[4 * f + 2][r], acc2[4 * f + 3][r]);
+      }
     }
     if (blk == 0) {
       lds_m[wave][col] = m_run;
@@ -427,38 +439,38 @@ sdpa_mfma_kernel(SdpaArgs a) {
   wg_epilogue<T, D, GC, NW, DUAL>(a, lds_o, lds_m, lds_l, qrow0, nvh, split, unit);
 }
 
-// 16-bit cache (T = half_t or bf16_t), head_dim 128, <= 16 virtual heads per
-// workgroup (16: 4 waves, for the cross-wave LDS merge).
-template <typename T>
+// 16-bit cache (T = half_t or bf16_t), head_dim D (128 or 64), <= 16
+// virtual heads per workgroup (16: 4 waves, for the cross-wave LDS merge).
+template <typename T, int D = 128>
 inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks,
                                hipStream_t stream) {
   switch (gc) {
     case 1:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 8, 2, false, D>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 1, 4, 2, false, D>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 2:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 8, 2, false, D>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 2, 4, 2, false, D>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 4:
       if (waves == 8) {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 8, 2, false, D>), dim3(nblocks), dim3(8 * 64), 0, stream, a);
       } else {
-        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+        hipLaunchKernelGGL((sdpa_mfma_kernel<T, 4, 4, 2, false, D>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       }
       break;
     case 8:
-      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 8, 4, 2, false, D>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       break;
     case 16:
-      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 16, 4, 2>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
+      hipLaunchKernelGGL((sdpa_mfma_kernel<T, 16, 4, 2, false, D>), dim3(nblocks), dim3(4 * 64), 0, stream, a);
       break;
     default:
       set_error("sdpa_dual_v: no MFMA variant for %d heads per workgroup", gc);

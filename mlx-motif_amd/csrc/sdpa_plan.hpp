@@ -231,6 +231,11 @@ inline int sdpa_gc_max(int D) { return D <= 128 ? 8 : 4; }
 // Largest head chunk of the fp16/bf16 matrix-core kernel (head_dim 128):
 // the 16 MFMA columns, with 4-wave workgroups for the cross-wave LDS merge.
 constexpr int kSdpaMfmaGcMax = 16;
+// Head dims of the single-pass fp16/bf16 matrix-core decode kernel: 128, or
+// 64 with a 16-byte aligned K (its rows are read 16 bytes per lane).
+inline bool mfma16_head_dim_ok(int D, const void* k) {
+  return D == 128 || (D == 64 && ((uintptr_t)k & 15u) == 0);
+}
 
 // Largest head chunk for the packed cache's matrix-core kernel: heads times
 // scale groups share the 16 MFMA columns.
