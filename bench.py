@@ -12,14 +12,15 @@ Workload (one "step" = one call of the hot path over one layer's cache):
 Each call reads a different layer's buffers (fp16: 8 sets = 0.79 GB, q4: 24
 sets = 0.67 GB, q8: 16 sets = 0.84 GB), so the 256 MB Infinity Cache cannot
 serve them.  The K timed calls are replayed from one HIP graph (captured after
-W eager warm-up calls), bracketed by HIP events on the launch stream.
+W eager warm-up calls), bracketed by HIP events on the launch stream; the
+graph is replayed 21 times and the median replay is reported.
 
 Algorithmic bytes per call count each live K/V1/V2 row once (plus scales and
 biases for packed caches) and q and y:
   fp16 98,328,576 B, q4 27,672,576 B, q8 52,248,576 B.
 
 cpu_baseline: the oracle's C/OpenMP port (oracle/motif_oracle.c) on the host
-cores, one full fp16 call (32 heads x 16000 rows), median of 5 after 2
+cores, one full fp16 call (32 heads x 16000 rows), median of 21 runs after 3
 warm-ups.  It is a reported baseline, not the target.
 
 stdout carries exactly one JSON line.  --extra adds µs/call lines for the
@@ -65,7 +66,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-REPEATS = 7  # timed replays per workload; the median is reported
+REPEATS = 21  # timed replays per workload (at least 20); the median is reported
 
 
 def time_calls_stats(torch, calls, steps: int, warmup: int, use_graph: bool = True,
@@ -339,6 +340,9 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+CPU_REPEATS = 21  # timed runs of each CPU-baseline leg (at least 20)
+
+
 def cpu_baseline():
     """The oracle's C/OpenMP port timed on the host: one full fp16 call and
     one full q4 call, on every OpenMP thread and on one thread."""
@@ -353,13 +357,13 @@ def cpu_baseline():
     threads = c_oracle.max_threads()
     scale = 1 / np.sqrt(D)
 
-    def median_us(fn, reps):
+    def median_us(fn, reps=CPU_REPEATS, warm=3):
         times = []
-        for i in range(reps + 2):
+        for i in range(reps + warm):
             t0 = time.perf_counter()
             fn()
             t1 = time.perf_counter()
-            if i >= 2:
+            if i >= warm:
                 times.append((t1 - t0) * 1e6)
         return statistics.median(times)
 
@@ -369,13 +373,13 @@ def cpu_baseline():
     def q4(n, fast=False):
         return c_oracle.sdpa_dual_v_q_f16(q, *trips, scale, GS, 4, KV_LEN, nthreads=n, fast=fast)
 
-    us = median_us(lambda: f16(threads), 5)
-    us_q4 = median_us(lambda: q4(threads), 5)
-    us_1 = median_us(lambda: f16(1), 3)
-    us_q4_1 = median_us(lambda: q4(1), 3)
-    fus = median_us(lambda: f16(threads, True), 5)
-    fus_q4 = median_us(lambda: q4(threads, True), 5)
-    fus_1 = median_us(lambda: f16(1, True), 3)
+    us = median_us(lambda: f16(threads))
+    us_q4 = median_us(lambda: q4(threads))
+    us_1 = median_us(lambda: f16(1))
+    us_q4_1 = median_us(lambda: q4(1))
+    fus = median_us(lambda: f16(threads, True))
+    fus_q4 = median_us(lambda: q4(threads, True))
+    fus_1 = median_us(lambda: f16(1, True))
     try:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -387,8 +391,9 @@ def cpu_baseline():
         "kind": "port",
         "sample": "one full sdpa_dual_v call (32 heads x 16000 rows, D 128) of the C/OpenMP "
                   "port oracle/motif_oracle.c, fp16 cache (value) and q4 cache, on `cores` "
-                  "OpenMP threads (median of 5 after 2 warm-ups) and on one thread (median of "
-                  "3); value: gcc -O2 -mf16c -ffp-contract=off (scalar, the checker's build); "
+                  f"OpenMP threads and on one thread (each the median of {CPU_REPEATS} runs "
+                  "after 3 warm-ups); value: gcc -O2 -mf16c -ffp-contract=off (scalar, the "
+                  "checker's build); "
                   "`vectorised`: the same source built gcc -O3 -march=x86-64-v3 -ffast-math",
         "gbps": round(alg_bytes("f16") / us / 1e3, 2),
         "one_thread_us": round(us_1, 1),
