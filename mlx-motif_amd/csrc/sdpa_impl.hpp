@@ -472,54 +472,85 @@ struct MergeShape {
 
 // Unnormalised merged accumulator of float4 column col of partial row vrow
 // (every lane of the column gets it) and the row's total L.
+// Loads of one partial row for merge_row_column, issued before any is
+// consumed (merge_row_column_issue), so that a caller merging several rows
+// issues all of their loads in one round trip.  They go through buffer
+// resources over the row's ns splits: loads past them return 0 with no
+// branch (a branch per load made the compiler wait on loads in flight), and
+// merge_row_column_finish masks those splits.
 template <int D>
-__device__ inline float4 merge_row_column(const SdpaArgs& a, long vrow, int col, int lane,
-                                          float& L_out) {
+struct MergeColumnLoads {
+  float4 v[MergeShape<D>::UNR];
+  float mj[MergeShape<D>::UNR];
+  float2 ml[kMaxSplits / 64];
+};
+
+template <int D>
+__device__ inline void merge_load_batch(const SdpaArgs& a, long vrow, int col, int lane, int s0,
+                                        MergeColumnLoads<D>& ld) {
   using S = MergeShape<D>;
   const int grp = lane / S::CW;
   const int ns = a.nsplit;
-  const float* po = a.part_o + vrow * ns * 2 * D + col * 4;
-  const float* pml = a.part_ml + vrow * ns * 2;
-
-  float4 v[S::UNR];
-  float mj[S::UNR];
-  auto load_batch = [&](int s0) {
+  const auto ro = part_rsrc(a.part_o + vrow * ns * 2 * D, (unsigned)(ns * 2 * D * 4));
+  const auto rml = part_rsrc(a.part_ml + vrow * ns * 2, (unsigned)(ns * 2 * 4));
 #pragma unroll
-    for (int j = 0; j < S::UNR; ++j) {
-      const int s = s0 + grp + j * S::NGR;
-      v[j] = s < ns ? *reinterpret_cast<const float4*>(po + (long)s * 2 * D)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-      mj[j] = s < ns ? pml[2 * s] : kNegSentinel;
-    }
-  };
-  // (m, l) of splits lane, lane + 64, ... and the first batch together.
-  float2 ml[kMaxSplits / 64];
-#pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) {
-    const int s = lane + 64 * i;
-    ml[i] = s < ns ? *reinterpret_cast<const float2*>(pml + 2 * s) : make_float2(kNegSentinel, 0.f);
+  for (int j = 0; j < S::UNR; ++j) {
+    const unsigned s = (unsigned)(s0 + grp + j * S::NGR);
+    ld.v[j] = __builtin_bit_cast(
+        float4, __builtin_amdgcn_raw_buffer_load_b128(ro, (s * 2 * D + col * 4) * 4u, 0, 0));
+    ld.mj[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rml, s * 8u, 0, 0));
   }
-  load_batch(0);
+}
 
+// (m, l) of splits lane, lane + 64, ... and the first batch together.
+template <int D>
+__device__ inline void merge_row_column_issue(const SdpaArgs& a, long vrow, int col, int lane,
+                                              MergeColumnLoads<D>& ld) {
+  const int ns = a.nsplit;
+  const auto rml = part_rsrc(a.part_ml + vrow * ns * 2, (unsigned)(ns * 2 * 4));
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / 64; ++i)
+    ld.ml[i] = __builtin_bit_cast(
+        float2, __builtin_amdgcn_raw_buffer_load_b64(rml, (unsigned)(lane + 64 * i) * 8u, 0, 0));
+  merge_load_batch<D>(a, vrow, col, lane, 0, ld);
+  // Keep the loads here: the scheduler would otherwise sink the batch below
+  // the wait for the (m, l) pairs, a second round trip.
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Unnormalised merged accumulator of float4 column col of partial row vrow
+// (every lane of the column gets it) and the row's total L, from the loads
+// merge_row_column_issue started.
+template <int D>
+__device__ inline float4 merge_row_column_finish(const SdpaArgs& a, long vrow, int col, int lane,
+                                                 MergeColumnLoads<D>& ld, float& L_out) {
+  using S = MergeShape<D>;
+  const int ns = a.nsplit;
+  const int grp = lane / S::CW;
+  float mi[kMaxSplits / 64];  // m of split lane + 64 i, the sentinel past ns
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / 64; ++i) mi[i] = lane + 64 * i < ns ? ld.ml[i].x : kNegSentinel;
   float M = kNegSentinel;
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, ml[i].x);
+  for (int i = 0; i < kMaxSplits / 64; ++i) M = fmaxf(M, mi[i]);
   M = group_max<64>(M);
-  float L = 0.f;
+  float L = 0.f;  // (l past ns reads 0)
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / 64; ++i) L = fmaf(ml[i].y, fast_exp2(ml[i].x - M), L);
+  for (int i = 0; i < kMaxSplits / 64; ++i) L = fmaf(ld.ml[i].y, fast_exp2(mi[i] - M), L);
   L_out = group_sum<64>(L);
 
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < ns; s0 += S::NGR * S::UNR) {
-    if (s0 > 0) load_batch(s0);
+    if (s0 > 0) merge_load_batch<D>(a, vrow, col, lane, s0, ld);
 #pragma unroll
     for (int j = 0; j < S::UNR; ++j) {
-      const float f = fast_exp2(mj[j] - M);  // 0 for splits past ns (sentinel m)
-      acc.x = fmaf(v[j].x, f, acc.x);
-      acc.y = fmaf(v[j].y, f, acc.y);
-      acc.z = fmaf(v[j].z, f, acc.z);
-      acc.w = fmaf(v[j].w, f, acc.w);
+      // 0 for splits past ns (their m is replaced by the sentinel; o reads 0)
+      const float mjv = s0 + grp + j * S::NGR < ns ? ld.mj[j] : kNegSentinel;
+      const float f = fast_exp2(mjv - M);
+      acc.x = fmaf(ld.v[j].x, f, acc.x);
+      acc.y = fmaf(ld.v[j].y, f, acc.y);
+      acc.z = fmaf(ld.v[j].z, f, acc.z);
+      acc.w = fmaf(ld.v[j].w, f, acc.w);
     }
   }
   // Sum the NGR split groups of each column (lanes col, col + CW, ...).
@@ -531,6 +562,16 @@ __device__ inline float4 merge_row_column(const SdpaArgs& a, long vrow, int col,
     acc.w += __shfl_xor(acc.w, off);
   }
   return acc;
+}
+
+// Unnormalised merged accumulator of float4 column col of partial row vrow
+// (every lane of the column gets it) and the row's total L.
+template <int D>
+__device__ inline float4 merge_row_column(const SdpaArgs& a, long vrow, int col, int lane,
+                                          float& L_out) {
+  MergeColumnLoads<D> ld;
+  merge_row_column_issue<D>(a, vrow, col, lane, ld);
+  return merge_row_column_finish<D>(a, vrow, col, lane, ld, L_out);
 }
 
 // Merge block -> (virtual row, slice of NSL).  With one head chunk per KV
@@ -796,10 +837,17 @@ __global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kern
   const int col = wave * S::CW + lane % S::CW;
   const bool head_lane = lane < S::CW;  // one lane per column stores
 
-  float Lo, Ln;
-  const float4 ao = merge_row_column<D>(a, prow0 + (h - j * a.G), col, lane, Lo);
-  const float4 an = merge_row_column<D>(a, prow0 + a.G, col, lane, Ln);
+  // Both rows' loads (and lambda's) are in flight before either is consumed.
+  MergeColumnLoads<D> lo, ln;
+  merge_row_column_issue<D>(a, prow0 + (h - j * a.G), col, lane, lo);
+  merge_row_column_issue<D>(a, prow0 + a.G, col, lane, ln);
   const float lam = *a.gda_lambda;
+  float wv[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wv[e] = Elem<T>::load(a.gda_w, col * 4 + e);
+  float Lo, Ln;
+  const float4 ao = merge_row_column_finish<D>(a, prow0 + (h - j * a.G), col, lane, lo, Lo);
+  const float4 an = merge_row_column_finish<D>(a, prow0 + a.G, col, lane, ln, Ln);
   auto out_t = [](float v, float L) {  // o / l rounded to T (o when l == 0)
     const float x = L == 0.f ? v : v / L;
     if constexpr (Elem<T>::kBytes == 2) return Elem<T>::to_f32(Elem<T>::from_f32(x));
@@ -826,7 +874,7 @@ __global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kern
   float y[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
-    y[e] = d[e] * rms_inv * Elem<T>::load(a.gda_w, col * 4 + e) * a.gda_scale;
+    y[e] = d[e] * rms_inv * wv[e] * a.gda_scale;
   const long off = orow * 2 * D + col * 4;
   if constexpr (Elem<T>::kBytes == 2) {
     *reinterpret_cast<uint2*>((uint16_t*)a.y + off) = make_uint2(
