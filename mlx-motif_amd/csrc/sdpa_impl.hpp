@@ -645,20 +645,40 @@ __device__ inline void merge_rows(const SdpaArgs& a, long vrow, int lane) {
   for (int k = 0; k < CPL; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
   float M = kNegSentinel, L = 0.f;
   for (int s0 = 0; s0 < ns; s0 += NB) {
+    // Every load of the batch is issued before any is consumed: the split
+    // and column indices are clamped to valid ones (no branch per load, at
+    // which the compiler would wait on loads in flight) and the splits past
+    // ns and columns past C4 are masked afterwards.
+    float2 mlr[NB];
+    float4 vr[NB][CPL];
+    uint2 hr[NB][CPL];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int sc = min(s0 + j, ns - 1);
+      mlr[j] = pml[sc];
+#pragma unroll
+      for (int k = 0; k < CPL; ++k) {
+        const int cc = min(lane + 64 * k, C4 - 1);
+        if constexpr (F16)
+          hr[j][k] = ph[(long)sc * C4 + cc];
+        else
+          vr[j][k] = po[(long)sc * C4 + cc];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float2 ml[NB];
     float4 v[NB][CPL];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       const int s = s0 + j;
-      ml[j] = s < ns ? pml[s] : make_float2(kNegSentinel, 0.f);
+      ml[j] = s < ns ? mlr[j] : make_float2(kNegSentinel, 0.f);
 #pragma unroll
       for (int k = 0; k < CPL; ++k) {
-        const int c = lane + 64 * k;
-        const bool in = s < ns && c < C4;
+        const bool in = s < ns && lane + 64 * k < C4;
         if constexpr (F16)
-          v[j][k] = in ? half4_floats(ph[(long)s * C4 + c]) : make_float4(0.f, 0.f, 0.f, 0.f);
+          v[j][k] = in ? half4_floats(hr[j][k]) : make_float4(0.f, 0.f, 0.f, 0.f);
         else
-          v[j][k] = in ? po[(long)s * C4 + c] : make_float4(0.f, 0.f, 0.f, 0.f);
+          v[j][k] = in ? vr[j][k] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
     float Mb = M;
@@ -733,13 +753,24 @@ __global__ void __launch_bounds__(256) sdpa_merge_rows16_kernel(SdpaArgs a, long
   float4 acc[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
   float M = kNegSentinel, L = 0.f;
   for (int s0 = 0; s0 < ns; s0 += NB) {
+    // All loads first, at clamped split indices, then the masks (as in
+    // merge_rows).
+    float2 mlr[NB];
+    uint4 wr[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int sc = min(s0 + j, ns - 1);
+      mlr[j] = pml[sc];
+      wr[j] = ph[(long)sc * C8 + c];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float2 ml[NB];
     float4 v[NB][2];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const int s = s0 + j;
-      ml[j] = s < ns ? pml[s] : make_float2(kNegSentinel, 0.f);
-      const uint4 w = s < ns ? ph[(long)s * C8 + c] : make_uint4(0, 0, 0, 0);
+      const bool in = s0 + j < ns;
+      ml[j] = in ? mlr[j] : make_float2(kNegSentinel, 0.f);
+      const uint4 w = in ? wr[j] : make_uint4(0, 0, 0, 0);
       v[j][0] = half4_floats(make_uint2(w.x, w.y));
       v[j][1] = half4_floats(make_uint2(w.z, w.w));
     }
