@@ -665,16 +665,21 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   };
 
   // Two register sets in turn: the loads of the next U tiles are in flight
-  // while the current ones are computed.  (A third set, with two sets'
-  // loads in flight, measured slower for q4.)
-  while (tile_row(k0) < max_lim) {
-    load_tiles(tb, k0 + U);
-    compute_tiles(ta, k0);
-    k0 += U;
-    if (tile_row(k0) >= max_lim) break;
-    load_tiles(ta, k0 + U);
-    compute_tiles(tb, k0);
-    k0 += U;
+  // while the current ones are computed, and each set is reloaded as soon as
+  // it has been consumed.  (Loading the next set at the top of each
+  // iteration instead made the compiler wait there on the set in flight:
+  // q8 at 16k 15.05 against 14.85 us per call.  A third set, with two sets'
+  // loads in flight, measured slower for q4.)  Sets past the wave's last
+  // tile read zeros and cost no traffic.
+  int nset = 0;  // tile sets of U tiles this wave visits
+  while (tile_row(nset * U) < max_lim) ++nset;
+  load_tiles(tb, U);
+  for (int n = 0; n < nset; n += 2) {
+    compute_tiles(ta, n * U);
+    load_tiles(ta, (n + 2) * U);
+    if (n + 1 >= nset) break;
+    compute_tiles(tb, (n + 1) * U);
+    load_tiles(tb, (n + 3) * U);
   }
 
   // acc[i][r] of lane (col, blk) is channel 8*(4*blk + r) + i for head h; it
