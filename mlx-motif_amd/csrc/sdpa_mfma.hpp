@@ -335,6 +335,10 @@ sdpa_mfma_kernel(SdpaArgs a) {
       }
     }
 
+    // Every load of the U tiles is issued before the first product (the
+    // scheduler would otherwise hold some back until the first K rows land).
+    __builtin_amdgcn_sched_barrier(0);
+
     // Tiles in pairs: the PV products take both tiles' 32 rows in one
     // 16x16x32 MFMA (k = 8*blk + j is row 4*blk + j of the pair's first
     // tile for j < 4, row 4*blk + j - 4 of its second for j >= 4), with one
