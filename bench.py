@@ -246,10 +246,12 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     return [(mk_q if bits else mk)(*t) for t in sets], (q1, q2, w, lam, sets, y, o, n, ws)
 
 
-def make_small_step_calls(torch, lib, dev, nsets, kv_len=1024):
+def make_small_step_calls(torch, lib, dev, nsets, kv_len=1024, fused=True):
     """The small GDA decode step: q1, q2 (1, 8, 1, D) over k1/k2/v1/v2 (1, 4,
-    kv_len, D) fp16, two motif_sdpa_dual_v calls (GQA 2) then
-    motif_gda_post_split with gr 1 into y (1, 8, 1, 2D)."""
+    kv_len, D) fp16 into y (1, 8, 1, 2D): one motif_gda_decode_heads call
+    (attention launch + merge with the epilogue), or (fused=False) the
+    reference's three calls, two motif_sdpa_dual_v (GQA 2) then
+    motif_gda_post_split with gr 1."""
     from mlx_motif import _native
 
     g = torch.Generator(device=dev)
@@ -260,13 +262,21 @@ def make_small_step_calls(torch, lib, dev, nsets, kv_len=1024):
     sets = [tuple(torch.randn((1, 4, kv_len, D), generator=g, device=dev).half()
                   for _ in range(4)) for _ in range(nsets)]
     o, n, y = (torch.empty((1, 8, 1, 2 * D), dtype=torch.float16, device=dev) for _ in range(3))
-    nbytes = lib.motif_sdpa_workspace_bytes(1, 8, 4, 1, kv_len, D)
+    nbytes = max(lib.motif_sdpa_workspace_bytes(1, 8, 4, 1, kv_len, D),
+                 lib.motif_gda_decode_heads_workspace_bytes(1, 8, 8, 4, kv_len, D))
     ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
     scale = 1.0 / D ** 0.5
 
     def mk(k1, k2, v1, v2):
         def call():
             st = torch.cuda.current_stream().cuda_stream
+            if fused:
+                _native.check(lib.motif_gda_decode_heads(
+                    q1.data_ptr(), q2.data_ptr(), None, None, None, None, k1.data_ptr(),
+                    k2.data_ptr(), v1.data_ptr(), v2.data_ptr(), w.data_ptr(), lam.data_ptr(),
+                    0.8, 1e-5, y.data_ptr(), 0, 1, 8, 8, 4, D, kv_len, kv_len, scale,
+                    ws.data_ptr(), ws.numel(), st))
+                return
             for q, k, out in ((q1, k1, o), (q2, k2, n)):
                 _native.check(lib.motif_sdpa_dual_v(
                     q.data_ptr(), k.data_ptr(), v1.data_ptr(), v2.data_ptr(), out.data_ptr(), 0,
@@ -667,7 +677,9 @@ def summarize_traffic(kind: str, fetch_dir: str, write_dir: str) -> int:
 
 def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
     """The other rows' headline shapes, timed as the decode calls are (graph
-    replay, HIP events): the fused GDA decode step at 16k and, with the
+    replay, HIP events): the small GDA step (8 signal/noise pairs over 4 KV
+    heads at 1024 rows, fused and as three calls), the fused GDA decode step
+    at 16k and, with the
     token's write, at 3204 over 48 layer caches, the 5-row verify
     slabs over 32768 rows (fp16 and q8), the 512-row prefill chunk over 3716
     rows and a 12.7B layer's 512-row chunk at offset 3204 from the
@@ -696,10 +708,16 @@ def secondary(torch, lib, dev, steps: int = 50, warm: int = 5) -> dict:
 
     # one GDA decode step of the small layer the CPU reference runs: 8
     # signal/noise head pairs over 4 KV heads (GQA 2), fp16 cache of 1024
-    # rows; two sdpa_dual_v calls + gda_post_split (gr 1)
+    # rows: the fused step (bytes: 4 cache streams, q1, q2, y) and the
+    # reference's three calls (two sdpa_dual_v + gda_post_split, gr 1: 6
+    # streams, and o, n written and read back)
     calls, keep = make_small_step_calls(torch, lib, dev, 16)
-    hbm("gda_step_f16_8pairs_4kv_kv1024", timed(calls), 6 * 4 * 1024 * D * 2 + 16 * D * 2 +
-        3 * 8 * 2 * D * 2)
+    hbm("gda_step_f16_8pairs_4kv_kv1024", timed(calls), 4 * 4 * 1024 * D * 2 + 16 * D * 2 +
+        8 * 2 * D * 2)
+    del calls, keep
+    calls, keep = make_small_step_calls(torch, lib, dev, 16, fused=False)
+    hbm("gda_step_f16_8pairs_4kv_kv1024_three_calls", timed(calls),
+        6 * 4 * 1024 * D * 2 + 16 * D * 2 + 3 * 8 * 2 * D * 2)
     del calls, keep
     # the 12.7B layer call at kv 3204, 48 back-to-back calls over 48
     # distinct layer buffers

@@ -355,6 +355,44 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                        int bits, int group_size, float scale, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* The same step for any noise-head count: q1 (B, Hq1, 1, D) origin queries
+ * and q2 (B, Hq2, 1, D) noise queries over Hkv KV heads, each pass a GQA
+ * sdpa_dual_v call (attention.py:190-260, native GQA, so Hkv divides Hq2)
+ * and gda_post_split pairing origin head h with noise head h / gr,
+ * gr = Hq1 / Hq2 (gda.py:223-282, q_origin == q_groups * gr at gda.py:248).
+ * motif_gda_decode / motif_gda_decode_append are the case Hq2 == Hkv (the
+ * 12.7B layout, model.py:749-768); Hq2 > Hkv is e.g. 8 origin and 8 noise
+ * heads over 4 KV heads.  k1_new .. v2_new: all four null (no cache write)
+ * or all four set (the token's rows, written at row kv_len - 1 first, as
+ * the _append entry points do).  The fused launch takes the G1 = Hq1 / Hkv
+ * origin and G2 = Hq2 / Hkv noise heads of a KV head as G1 + G2 <= 16
+ * columns (packed cache: that sum rounded up to a power of two, times
+ * D / group_size, <= 16); other shapes compose the separate calls on the
+ * device.  Workspace: motif_gda_decode_heads_workspace_bytes(B, Hq1, Hq2,
+ * Hkv, kv_len, D) bytes (0 when Hkv does not divide Hq2 or Hq2 does not
+ * divide Hq1), 256-byte aligned, zeroed before its first use.  Contract
+ * otherwise as motif_gda_decode / motif_gda_decode_q. */
+size_t motif_gda_decode_heads_workspace_bytes(int B, int Hq1, int Hq2, int Hkv, int kv_len,
+                                              int D);
+int motif_gda_decode_heads(const void* q1, const void* q2, const void* k1_new,
+                           const void* k2_new, const void* v1_new, const void* v2_new, void* k1,
+                           void* k2, void* v1, void* v2, const void* subln_w,
+                           const float* lambda_full, float one_minus_lambda_init, float eps,
+                           void* y, int dtype, int B, int Hq1, int Hq2, int Hkv, int D,
+                           int kv_cap, int kv_len, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int motif_gda_decode_q_heads(const void* q1, const void* q2, const void* k1_new,
+                             const void* k2_new, const void* v1_new, const void* v2_new,
+                             uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                             uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                             uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                             uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                             const void* subln_w, const float* lambda_full,
+                             float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                             int Hq1, int Hq2, int Hkv, int D, int kv_cap, int kv_len, int bits,
+                             int group_size, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* Decode step with append: one call per layer for a decode token (no single
  * counterpart in the reference, whose step is the cache write
  * MotifGroupedKVCache.update_and_fetch_4 / the quantized cache's

@@ -300,7 +300,8 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
 }
 
 // ------------------------------------------------ fused GDA decode step ---
-// Partial rows of the fused path: (b, KV head, column), G + 1 columns.
+// Partial rows of the fused path: (b, KV head, column), G1 + G2 columns (G1
+// origin and G2 noise heads per KV head; G2 = 1 in the 12.7B layout).
 struct GdaDecodeLayout {
   SdpaPlan plan;    // fp16-cache kernel (8-wave workgroups)
   SdpaPlan plan_q;  // packed-cache kernel (4-wave workgroups, one per CU)
@@ -308,7 +309,7 @@ struct GdaDecodeLayout {
   size_t sdpa_bytes, yo_bytes, yn_bytes, composed_bytes;
 };
 
-static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int D) {
+static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int G1, int G2, int kv_len, int D) {
   GdaDecodeLayout L{};
   // One virtual head per KV head in the planner: the fused kernel runs one
   // workgroup per (b, KV head, split), like the unfused origin pass; 4-wave
@@ -318,18 +319,18 @@ static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int
   L.plan = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, short4 ? 4 : 0, short4 ? 1 : 0);
   L.plan_q = plan_sdpa(B, Hkv, Hkv, 1, kv_len, D, 1, kSdpaMfmaQWaves, kSdpaMfmaQWgsPerCu);
   const int ns = L.plan.nsplit > L.plan_q.nsplit ? L.plan.nsplit : L.plan_q.nsplit;
-  const size_t prow = (size_t)B * Hkv * (gr + 1);
+  const size_t prow = (size_t)B * Hkv * (G1 + G2);
   L.counter_bytes = round256(prow * sizeof(unsigned));
   L.o_bytes = round256(prow * ns * 2 * D * sizeof(float));
   L.ml_bytes = round256(prow * ns * 2 * sizeof(float));
   L.fused_bytes = L.counter_bytes + L.o_bytes + L.ml_bytes;
   // Composed path: both attention calls' workspace (any cache format), then
   // o and n (fp32 bound).
-  const size_t w1 = motif_sdpa_workspace_bytes(B, Hkv * gr, Hkv, 1, kv_len, D);
-  const size_t w2 = motif_sdpa_workspace_bytes(B, Hkv, Hkv, 1, kv_len, D);
+  const size_t w1 = motif_sdpa_workspace_bytes(B, Hkv * G1, Hkv, 1, kv_len, D);
+  const size_t w2 = motif_sdpa_workspace_bytes(B, Hkv * G2, Hkv, 1, kv_len, D);
   L.sdpa_bytes = round256(w1 > w2 ? w1 : w2);
-  L.yo_bytes = round256((size_t)B * Hkv * gr * 2 * D * sizeof(float));
-  L.yn_bytes = round256((size_t)B * Hkv * 2 * D * sizeof(float));
+  L.yo_bytes = round256((size_t)B * Hkv * G1 * 2 * D * sizeof(float));
+  L.yn_bytes = round256((size_t)B * Hkv * G2 * 2 * D * sizeof(float));
   L.composed_bytes = L.sdpa_bytes + L.yo_bytes + L.yn_bytes;
   return L;
 }
@@ -337,11 +338,12 @@ static GdaDecodeLayout gda_decode_layout(int B, int Hkv, int gr, int kv_len, int
 // Checks shared by both fused-decode entry points; the workspace check
 // covers the larger of the fused and composed layouts.
 static int gda_decode_common(const char* name, const GdaDecodeLayout& L, int dtype, int B,
-                             int Hkv, int gr, int D, int kv_cap, int kv_len, void* ws,
+                             int Hkv, int G1, int G2, int D, int kv_cap, int kv_len, void* ws,
                              size_t ws_bytes) {
   MOTIF_REQUIRE(dtype == MOTIF_F16 || dtype == MOTIF_BF16 || dtype == MOTIF_F32,
                 "%s: unknown dtype code %d", name, dtype);
-  MOTIF_REQUIRE(B >= 1 && Hkv >= 1 && gr >= 1, "%s: B, H_kv, gr must be >= 1", name);
+  MOTIF_REQUIRE(B >= 1 && Hkv >= 1 && G1 >= 1 && G2 >= 1 && G1 % G2 == 0,
+                "%s: B, H_kv, gr must be >= 1", name);
   MOTIF_REQUIRE(D > 0 && D % 32 == 0, "%s: D=%d must be a multiple of 32", name, D);
   MOTIF_REQUIRE(kv_cap >= 0 && 0 <= kv_len && kv_len <= kv_cap,
                 "%s: kv_len=%d must be in [0, %d]", name, kv_len, kv_cap);
@@ -358,8 +360,8 @@ static int gda_decode_common(const char* name, const GdaDecodeLayout& L, int dty
 // Arguments of a fused launch: partial rows (b, KV head, column) after the
 // (unused) counter block.
 static SdpaArgs gda_decode_args(const GdaDecodeLayout& L, const SdpaPlan& p, const void* q1,
-                                const void* q2, void* y, int B, int Hkv, int gr, int kv_cap,
-                                int kv_len, float scale, const void* subln_w,
+                                const void* q2, void* y, int B, int Hkv, int G1, int G2,
+                                int kv_cap, int kv_len, float scale, const void* subln_w,
                                 const float* lambda_full, float one_minus_lambda_init,
                                 float eps, void* ws) {
   SdpaArgs a{};
@@ -368,10 +370,11 @@ static SdpaArgs gda_decode_args(const GdaDecodeLayout& L, const SdpaPlan& p, con
   a.y = y;
   a.B = B;
   a.Hkv = Hkv;
-  a.Hq = Hkv * gr;
+  a.Hq = Hkv * G1;
   a.S_q = 1;
-  a.G = gr;
-  a.GV = gr + 1;
+  a.G = G1;
+  a.G2 = G2;
+  a.GV = G1 + G2;
   a.nchunk = 1;
   a.kv_cap = kv_cap;
   a.kv_len = kv_len;
@@ -440,7 +443,23 @@ static int scratch_for_device(void** out, hipStream_t s) {
   return MOTIF_OK;
 }
 
-static int gda_columns(int gr) { return gr + 1 <= 2 ? 2 : gr + 1 <= 4 ? 4 : gr + 1 <= 8 ? 8 : 16; }
+// Columns of a fused launch: the n = G1 + G2 heads of a KV head, rounded up
+// to a compiled width.
+static int gda_columns(int n) { return n <= 2 ? 2 : n <= 4 ? 4 : n <= 8 ? 8 : 16; }
+
+// Origin / noise heads per KV head of a step whose q1 has Hq1 and q2 Hq2
+// heads over Hkv KV heads: both passes are GQA calls of sdpa_dual_v
+// (attention.py:237-243: heads a multiple of Hkv), and gda_post_split pairs
+// origin head h with noise head h / gr, gr = Hq1 / Hq2 (gda.py:248).
+static int gda_heads(const char* name, int Hq1, int Hq2, int Hkv, int& G1, int& G2) {
+  MOTIF_REQUIRE(Hkv >= 1 && Hq2 >= 1 && Hq1 >= 1, "%s: H_q1, H_q2, H_kv must be >= 1", name);
+  MOTIF_REQUIRE(Hq2 % Hkv == 0, "%s: H_q2=%d must be a multiple of H_kv=%d", name, Hq2, Hkv);
+  MOTIF_REQUIRE(Hq1 % Hq2 == 0, "%s: H_q1=%d must be a multiple of H_q2=%d (q_origin == "
+                "q_groups * gr)", name, Hq1, Hq2);
+  G1 = Hq1 / Hkv;
+  G2 = Hq2 / Hkv;
+  return MOTIF_OK;
+}
 
 }  // namespace motif
 
@@ -451,7 +470,17 @@ extern "C" {
 size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int D) {
   if (B <= 0 || Hkv <= 0 || gr <= 0 || D <= 0 || kv_len < 0) return 0;
   CallScope scope;
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, 1, kv_len, D);
+  return L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
+}
+
+size_t motif_gda_decode_heads_workspace_bytes(int B, int Hq1, int Hq2, int Hkv, int kv_len,
+                                              int D) {
+  if (B <= 0 || Hkv <= 0 || Hq1 <= 0 || Hq2 <= 0 || D <= 0 || kv_len < 0 || Hq2 % Hkv != 0 ||
+      Hq1 % Hq2 != 0)
+    return 0;
+  CallScope scope;
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, Hq1 / Hkv, Hq2 / Hkv, kv_len, D);
   return L.fused_bytes > L.composed_bytes ? L.fused_bytes : L.composed_bytes;
 }
 
@@ -463,13 +492,13 @@ size_t motif_gda_decode_workspace_bytes(int B, int Hkv, int gr, int kv_len, int 
 static int gda_decode_fp(const char* name, const void* q1, const void* q2, const void* k1,
                          const void* k2, const void* v1, const void* v2, const void* subln_w,
                          const float* lambda_full, float one_minus_lambda_init, float eps,
-                         void* y, int dtype, int B, int Hkv, int gr, int D, int kv_cap,
-                         int kv_len, float scale, void* workspace, size_t workspace_bytes,
-                         const void* const* new_kv, void* stream) {
+                         void* y, int dtype, int B, int Hkv, int G1, int G2, int D,
+                         int kv_cap, int kv_len, float scale, void* workspace,
+                         size_t workspace_bytes, const void* const* new_kv, void* stream) {
   CallScope scope;
   clear_error();
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
-  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, G1, G2, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, G1, G2, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q1 && q2 && y && subln_w && lambda_full &&
@@ -481,14 +510,14 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
   }
   hipStream_t s = (hipStream_t)stream;
   const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 &&
-                     tuning().mfma && gr + 1 <= 16 &&
+                     tuning().mfma && G1 + G2 <= 16 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
                      aligned(k1, 16) && aligned(k2, 16) &&
                      aligned(v1, 16) && aligned(v2, 16) && aligned(y, 8) &&
                      (!new_kv || ((uintptr_t)new_kv[0] | (uintptr_t)new_kv[1] |
                                   (uintptr_t)new_kv[2] | (uintptr_t)new_kv[3]) % 16 == 0);
   if (fused) {
-    SdpaArgs a = gda_decode_args(L, L.plan, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
+    SdpaArgs a = gda_decode_args(L, L.plan, q1, q2, y, B, Hkv, G1, G2, kv_cap, kv_len, scale,
                                  subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
     a.k = k1;
     a.k2 = k2;
@@ -502,8 +531,9 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
     rc = check_partials(name, a, true);
     if (rc != MOTIF_OK) return rc;
     const int waves = L.plan.waves;
-    return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), waves, nblocks, s)
-                              : launch_gda_decode_bf16(a, gda_columns(gr), waves, nblocks, s);
+    const int gc = gda_columns(G1 + G2);
+    return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gc, waves, nblocks, s)
+                              : launch_gda_decode_bf16(a, gc, waves, nblocks, s);
   }
   if (new_kv) {  // row kv_len - 1 of each slot: B * Hkv rows of D values
     const size_t row = (size_t)D * (dtype == MOTIF_F32 ? 4 : 2);
@@ -522,14 +552,14 @@ static int gda_decode_fp(const char* name, const void* q1, const void* q2, const
   char* w = (char*)workspace;
   void* yo = w + L.sdpa_bytes;
   void* yn = w + L.sdpa_bytes + L.yo_bytes;
-  rc = motif_sdpa_dual_v(q1, k1, v1, v2, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap, kv_len, scale,
+  rc = motif_sdpa_dual_v(q1, k1, v1, v2, yo, dtype, B, Hkv * G1, Hkv, D, kv_cap, kv_len, scale,
                          workspace, L.sdpa_bytes, stream);
   if (rc != MOTIF_OK) return rc;
-  rc = motif_sdpa_dual_v(q2, k2, v1, v2, yn, dtype, B, Hkv, Hkv, D, kv_cap, kv_len, scale,
+  rc = motif_sdpa_dual_v(q2, k2, v1, v2, yn, dtype, B, Hkv * G2, Hkv, D, kv_cap, kv_len, scale,
                          workspace, L.sdpa_bytes, stream);
   if (rc != MOTIF_OK) return rc;
-  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
-                              lambda_full, one_minus_lambda_init, eps, stream);
+  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * G1, Hkv * G2, G1 / G2, 1,
+                              2 * D, lambda_full, one_minus_lambda_init, eps, stream);
 }
 
 extern "C" {
@@ -540,8 +570,40 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
                      int dtype, int B, int Hkv, int gr, int D, int kv_cap, int kv_len,
                      float scale, void* workspace, size_t workspace_bytes, void* stream) {
   return gda_decode_fp("gda_decode", q1, q2, k1, k2, v1, v2, subln_w, lambda_full,
-                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D, kv_cap, kv_len,
+                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, 1, D, kv_cap, kv_len,
                        scale, workspace, workspace_bytes, nullptr, stream);
+}
+
+// New rows: all four null (no write) or all four set (the token's rows,
+// written at row kv_len - 1 first, as motif_gda_decode_append does).
+static int gda_new_rows(const char* name, const void* k1_new, const void* k2_new,
+                        const void* v1_new, const void* v2_new, bool& append) {
+  const int n = (k1_new != nullptr) + (k2_new != nullptr) + (v1_new != nullptr) +
+                (v2_new != nullptr);
+  MOTIF_REQUIRE(n == 0 || n == 4, "%s: new rows must be all null or all set", name);
+  append = n == 4;
+  return MOTIF_OK;
+}
+
+int motif_gda_decode_heads(const void* q1, const void* q2, const void* k1_new,
+                           const void* k2_new, const void* v1_new, const void* v2_new, void* k1,
+                           void* k2, void* v1, void* v2, const void* subln_w,
+                           const float* lambda_full, float one_minus_lambda_init, float eps,
+                           void* y, int dtype, int B, int Hq1, int Hq2, int Hkv, int D,
+                           int kv_cap, int kv_len, float scale, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  CallScope scope;  // one tuning snapshot for the whole call
+  clear_error();
+  const char* name = "gda_decode_heads";
+  int G1 = 0, G2 = 0;
+  bool append = false;
+  int rc = gda_heads(name, Hq1, Hq2, Hkv, G1, G2);
+  if (rc == MOTIF_OK) rc = gda_new_rows(name, k1_new, k2_new, v1_new, v2_new, append);
+  if (rc != MOTIF_OK) return rc;
+  const void* const nk[4] = {k1_new, k2_new, v1_new, v2_new};
+  return gda_decode_fp(name, q1, q2, k1, k2, v1, v2, subln_w, lambda_full,
+                       one_minus_lambda_init, eps, y, dtype, B, Hkv, G1, G2, D, kv_cap, kv_len,
+                       scale, workspace, workspace_bytes, append ? nk : nullptr, stream);
 }
 
 int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
@@ -553,7 +615,7 @@ int motif_gda_decode_append(const void* q1, const void* q2, const void* k1_new,
                             void* stream) {
   const void* const nk[4] = {k1_new, k2_new, v1_new, v2_new};
   return gda_decode_fp("gda_decode_append", q1, q2, k1, k2, v1, v2, subln_w, lambda_full,
-                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D, kv_cap, kv_len,
+                       one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, 1, D, kv_cap, kv_len,
                        scale, workspace, workspace_bytes, nk, stream);
 }
 
@@ -567,8 +629,8 @@ int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const v
   CallScope scope;
   clear_error();
   const char* name = "gda_decode_proj";
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
-  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, 1, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, 1, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(q_proj && k_proj && v_proj && k1 && k2 && v1 && v2 && y && subln_w &&
@@ -588,8 +650,9 @@ int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const v
               "motif_rope_split4 and motif_gda_decode", name, dtype, D, gr);
     return MOTIF_ERR_UNSUPPORTED;
   }
-  SdpaArgs a = gda_decode_args(L, L.plan, q_proj, q_proj, y, B, Hkv, gr, kv_cap, kv_len, scale,
-                               subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
+  SdpaArgs a = gda_decode_args(L, L.plan, q_proj, q_proj, y, B, Hkv, gr, 1, kv_cap, kv_len,
+                               scale, subln_w, lambda_full, one_minus_lambda_init, eps,
+                               workspace);
   a.k = k1;
   a.k2 = k2;
   a.v1 = v1;
@@ -603,10 +666,10 @@ int motif_gda_decode_proj_scaled(const void* q_proj, const void* k_proj, const v
   const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
   rc = check_partials(name, a, true);
   if (rc != MOTIF_OK) return rc;
-  return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr), L.plan.waves, nblocks,
-                                                    (hipStream_t)stream)
-                            : launch_gda_decode_bf16(a, gda_columns(gr), L.plan.waves, nblocks,
-                                                     (hipStream_t)stream);
+  return dtype == MOTIF_F16 ? launch_gda_decode_f16(a, gda_columns(gr + 1), L.plan.waves,
+                                                    nblocks, (hipStream_t)stream)
+                            : launch_gda_decode_bf16(a, gda_columns(gr + 1), L.plan.waves,
+                                                     nblocks, (hipStream_t)stream);
 }
 
 int motif_gda_decode_proj(const void* q_proj, const void* k_proj, const void* v_proj, void* k1,
@@ -734,13 +797,13 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
                         const uint32_t* v2_data, const void* v2_scales, const void* v2_biases,
                         const void* subln_w, const float* lambda_full,
                         float one_minus_lambda_init, float eps, void* y, int dtype, int B,
-                        int Hkv, int gr, int D, int kv_cap, int kv_len, int bits,
+                        int Hkv, int G1, int G2, int D, int kv_cap, int kv_len, int bits,
                         int group_size, float scale, void* workspace, size_t workspace_bytes,
                         const void* const* new_kv, void* stream) {
   CallScope scope;
   clear_error();
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
-  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, G1, G2, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, G1, G2, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
@@ -758,7 +821,7 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
     MOTIF_REQUIRE(kv_len >= 1, "%s: kv_len=%d must count the appended row", name, kv_len);
   }
   hipStream_t s = (hipStream_t)stream;
-  const int gc = gda_columns(gr);
+  const int gc = gda_columns(G1 + G2);
   const int ng = D / group_size;
   const uintptr_t data_bits = (uintptr_t)k1_data | (uintptr_t)k2_data | (uintptr_t)v1_data |
                               (uintptr_t)v2_data;
@@ -766,7 +829,7 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
                                (uintptr_t)k2_scales | (uintptr_t)k2_biases |
                                (uintptr_t)v1_scales | (uintptr_t)v1_biases |
                                (uintptr_t)v2_scales | (uintptr_t)v2_biases;
-  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && G1 + G2 <= 16 &&
                      gc * ng <= 16 && (data_bits & 15u) == 0 &&
                      (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
@@ -774,8 +837,9 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
                      (!new_kv || ((uintptr_t)new_kv[0] | (uintptr_t)new_kv[1] |
                                   (uintptr_t)new_kv[2] | (uintptr_t)new_kv[3]) % 16 == 0);
   if (fused) {
-    SdpaArgs a = gda_decode_args(L, L.plan_q, q1, q2, y, B, Hkv, gr, kv_cap, kv_len, scale,
-                                 subln_w, lambda_full, one_minus_lambda_init, eps, workspace);
+    SdpaArgs a = gda_decode_args(L, L.plan_q, q1, q2, y, B, Hkv, G1, G2, kv_cap, kv_len,
+                                 scale, subln_w, lambda_full, one_minus_lambda_init, eps,
+                                 workspace);
     a.kd = k1_data; a.ks = k1_scales; a.kb = k1_biases;
     a.k2d = k2_data; a.k2s = k2_scales; a.k2b = k2_biases;
     a.v1d = v1_data; a.v1s = v1_scales; a.v1b = v1_biases;
@@ -804,15 +868,15 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
   void* yo = w + L.sdpa_bytes;
   void* yn = w + L.sdpa_bytes + L.yo_bytes;
   rc = motif_sdpa_dual_v_q(q1, k1_data, k1_scales, k1_biases, v1_data, v1_scales, v1_biases,
-                           v2_data, v2_scales, v2_biases, yo, dtype, B, Hkv * gr, Hkv, D, kv_cap,
+                           v2_data, v2_scales, v2_biases, yo, dtype, B, Hkv * G1, Hkv, D, kv_cap,
                            kv_len, bits, group_size, scale, workspace, L.sdpa_bytes, stream);
   if (rc != MOTIF_OK) return rc;
   rc = motif_sdpa_dual_v_q(q2, k2_data, k2_scales, k2_biases, v1_data, v1_scales, v1_biases,
-                           v2_data, v2_scales, v2_biases, yn, dtype, B, Hkv, Hkv, D, kv_cap,
+                           v2_data, v2_scales, v2_biases, yn, dtype, B, Hkv * G2, Hkv, D, kv_cap,
                            kv_len, bits, group_size, scale, workspace, L.sdpa_bytes, stream);
   if (rc != MOTIF_OK) return rc;
-  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * gr, Hkv, gr, 1, 2 * D,
-                              lambda_full, one_minus_lambda_init, eps, stream);
+  return motif_gda_post_split(yo, yn, subln_w, y, dtype, B, Hkv * G1, Hkv * G2, G1 / G2, 1,
+                              2 * D, lambda_full, one_minus_lambda_init, eps, stream);
 }
 
 extern "C" {
@@ -828,9 +892,36 @@ int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                        size_t workspace_bytes, void* stream) {
   return gda_decode_q("gda_decode_q", q1, q2, k1_data, k1_scales, k1_biases, k2_data, k2_scales,
                       k2_biases, v1_data, v1_scales, v1_biases, v2_data, v2_scales, v2_biases,
-                      subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, D,
-                      kv_cap, kv_len, bits, group_size, scale, workspace, workspace_bytes,
+                      subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B, Hkv, gr, 1,
+                      D, kv_cap, kv_len, bits, group_size, scale, workspace, workspace_bytes,
                       nullptr, stream);
+}
+
+int motif_gda_decode_q_heads(const void* q1, const void* q2, const void* k1_new,
+                             const void* k2_new, const void* v1_new, const void* v2_new,
+                             uint32_t* k1_data, void* k1_scales, void* k1_biases,
+                             uint32_t* k2_data, void* k2_scales, void* k2_biases,
+                             uint32_t* v1_data, void* v1_scales, void* v1_biases,
+                             uint32_t* v2_data, void* v2_scales, void* v2_biases,
+                             const void* subln_w, const float* lambda_full,
+                             float one_minus_lambda_init, float eps, void* y, int dtype, int B,
+                             int Hq1, int Hq2, int Hkv, int D, int kv_cap, int kv_len, int bits,
+                             int group_size, float scale, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  CallScope scope;  // one tuning snapshot for the whole call
+  clear_error();
+  const char* name = "gda_decode_q_heads";
+  int G1 = 0, G2 = 0;
+  bool append = false;
+  int rc = gda_heads(name, Hq1, Hq2, Hkv, G1, G2);
+  if (rc == MOTIF_OK) rc = gda_new_rows(name, k1_new, k2_new, v1_new, v2_new, append);
+  if (rc != MOTIF_OK) return rc;
+  const void* const nk[4] = {k1_new, k2_new, v1_new, v2_new};
+  return gda_decode_q(name, q1, q2, k1_data, k1_scales, k1_biases, k2_data, k2_scales,
+                      k2_biases, v1_data, v1_scales, v1_biases, v2_data, v2_scales, v2_biases,
+                      subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B, Hkv, G1, G2,
+                      D, kv_cap, kv_len, bits, group_size, scale, workspace, workspace_bytes,
+                      append ? nk : nullptr, stream);
 }
 
 int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new,
@@ -848,7 +939,7 @@ int motif_gda_decode_q_append(const void* q1, const void* q2, const void* k1_new
   return gda_decode_q("gda_decode_q_append", q1, q2, k1_data, k1_scales, k1_biases, k2_data,
                       k2_scales, k2_biases, v1_data, v1_scales, v1_biases, v2_data, v2_scales,
                       v2_biases, subln_w, lambda_full, one_minus_lambda_init, eps, y, dtype, B,
-                      Hkv, gr, D, kv_cap, kv_len, bits, group_size, scale, workspace,
+                      Hkv, gr, 1, D, kv_cap, kv_len, bits, group_size, scale, workspace,
                       workspace_bytes, nk, stream);
 }
 
@@ -866,8 +957,8 @@ int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const
   CallScope scope;
   clear_error();
   const char* name = "gda_decode_q_proj";
-  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
-  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, D, kv_cap, kv_len, workspace,
+  const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, 1, kv_len, D);
+  int rc = gda_decode_common(name, L, dtype, B, Hkv, gr, 1, D, kv_cap, kv_len, workspace,
                              workspace_bytes);
   if (rc != MOTIF_OK) return rc;
   MOTIF_REQUIRE(bits == 4 || bits == 8, "%s: bits=%d must be 4 or 8", name, bits);
@@ -881,7 +972,7 @@ int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const
   MOTIF_REQUIRE(theta > 1.f, "%s: theta must be > 1", name);
   MOTIF_REQUIRE(position_scale > 0.f && position_scale <= 3.4028234663852886e38f,
                 "%s: position_scale must be positive and finite", name);
-  const int gc = gda_columns(gr);
+  const int gc = gda_columns(gr + 1);
   const int ng = D > 0 ? D / group_size : 1;
   const uintptr_t data_bits = (uintptr_t)k1_data | (uintptr_t)k2_data | (uintptr_t)v1_data |
                               (uintptr_t)v2_data;
@@ -899,7 +990,7 @@ int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const
               "motif_rope_split4 and motif_gda_decode_q_append", name, dtype, D, gr, group_size);
     return MOTIF_ERR_UNSUPPORTED;
   }
-  SdpaArgs a = gda_decode_args(L, L.plan_q, q_proj, q_proj, y, B, Hkv, gr, kv_cap, kv_len,
+  SdpaArgs a = gda_decode_args(L, L.plan_q, q_proj, q_proj, y, B, Hkv, gr, 1, kv_cap, kv_len,
                                scale, subln_w, lambda_full, one_minus_lambda_init, eps,
                                workspace);
   a.kd = k1_data; a.ks = k1_scales; a.kb = k1_biases;
@@ -1173,7 +1264,7 @@ int motif_plan_selfcheck(void) {
           // the fused decode step: partials are always published
           if (S_q == 1 && Hq / Hkv >= 2) {
             const int gr = Hq / Hkv - 1 > 0 ? Hq / Hkv - 1 : 1;
-            const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, kv_len, D);
+            const GdaDecodeLayout L = gda_decode_layout(B, Hkv, gr, 1, kv_len, D);
             const size_t prow = (size_t)B * Hkv * (gr + 1);
             for (const SdpaPlan* p : {&L.plan, &L.plan_q}) {
               if (p->nsplit < 1 || p->nsplit > kMaxSplits ||

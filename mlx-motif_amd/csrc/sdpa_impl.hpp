@@ -847,7 +847,7 @@ int launch_sdpa_merge_d(const SdpaArgs& a, hipStream_t s) {
 // --------------------------------------------- fused GDA decode merge ---
 // Second launch of a fused GDA decode step (origin and noise passes share
 // one attention launch): one workgroup per origin row (b, h) merges the
-// splits of that row and of its noise head h / G, rounds both to T (the
+// splits of that row and of its noise head h / gr, rounds both to T (the
 // reference's attention outputs are T tensors), and applies gda_post_split
 // (src/mlx_motif/kernels/gda.py:131-192):
 //   d = o - lambda * n,  y = T(d * rsqrt(mean(d^2) + eps) * w * (1 - lambda_init)).
@@ -863,22 +863,28 @@ __global__ void __launch_bounds__(MergeShape<D>::NSL * 64) gda_decode_merge_kern
   if (!merge_block_coords(a, blockIdx.x, 1, a.G, orow, unused_slice)) return;
   const long b = orow / a.Hq;
   const int h = (int)(orow - b * a.Hq);
-  const int j = h / a.G;
-  const long prow0 = (b * a.Hkv + j) * (a.G + 1);
+  const int j = h / a.G;  // KV head
+  const int i = h - j * a.G;  // origin column within it
+  // Partial rows of KV head j: G origin columns, then G2 noise columns;
+  // origin head h pairs with noise head h / gr (gr = G / G2), column
+  // G + i / gr of the same KV head.
+  const long prow0 = (b * a.Hkv + j) * (a.G + a.G2);
+  const long orow_p = prow0 + i;
+  const long nrow_p = prow0 + a.G + i / (a.G / a.G2);
   const int col = wave * S::CW + lane % S::CW;
   const bool head_lane = lane < S::CW;  // one lane per column stores
 
   // Both rows' loads (and lambda's) are in flight before either is consumed.
   MergeColumnLoads<D> lo, ln;
-  merge_row_column_issue<D>(a, prow0 + (h - j * a.G), col, lane, lo);
-  merge_row_column_issue<D>(a, prow0 + a.G, col, lane, ln);
+  merge_row_column_issue<D>(a, orow_p, col, lane, lo);
+  merge_row_column_issue<D>(a, nrow_p, col, lane, ln);
   const float lam = *a.gda_lambda;
   float wv[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) wv[e] = Elem<T>::load(a.gda_w, col * 4 + e);
   float Lo, Ln;
-  const float4 ao = merge_row_column_finish<D>(a, prow0 + (h - j * a.G), col, lane, lo, Lo);
-  const float4 an = merge_row_column_finish<D>(a, prow0 + a.G, col, lane, ln, Ln);
+  const float4 ao = merge_row_column_finish<D>(a, orow_p, col, lane, lo, Lo);
+  const float4 an = merge_row_column_finish<D>(a, nrow_p, col, lane, ln, Ln);
   auto out_t = [](float v, float L) {  // o / l rounded to T (o when l == 0)
     const float x = L == 0.f ? v : v / L;
     if constexpr (Elem<T>::kBytes == 2) return Elem<T>::to_f32(Elem<T>::from_f32(x));

@@ -164,8 +164,9 @@ __device__ inline void append_rows_16bit(const SdpaArgs& a, long bk, int lane) {
 }
 
 // DUAL: fused GDA decode step.  Columns 0..G-1 are the origin heads of the
-// KV head (scores from k), column G its noise head (scores from k2); both
-// share the V1/V2 rows, and the partials go to the fused merge launch.
+// KV head (scores from k), columns G..G+G2-1 its noise heads (scores from
+// k2; G2 = a.G2, one in the 12.7B layout); all share the V1/V2 rows, and
+// the partials go to the fused merge launch.
 // T: half_t (fp16 cache, v_mfma_f32_16x16x32_f16) or bf16_t (bf16 cache,
 // v_mfma_f32_16x16x32_bf16).  The 16-column single-pass variant keeps the
 // in-kernel merge's LDS (104 KB): one workgroup, one wave per SIMD, per CU.
@@ -199,7 +200,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
   const int vh0 = chunk * GC;
   const int nvh = min(GC, a.GV - vh0);
   // First output row: y row (non-DUAL) or partial row (DUAL) of column 0.
-  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
+  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + a.G2)
                           : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
   const int max_lim = vhead_limit_max(a, vh0, nvh);
@@ -220,14 +221,15 @@ sdpa_mfma_kernel(SdpaArgs a) {
   {
     const uint16_t* qp = (const uint16_t*)a.q + (qrow0 + (col_ok ? col : 0)) * D + 8 * blk;
     if constexpr (DUAL) {
-      if (a.from_proj) {  // q_proj heads: stripe g*(G+1)+j, or origin-first
+      if (a.from_proj) {  // q_proj heads (G2 == 1): stripe g*(G+1)+j, or origin-first
         const int head = a.q_origin_first
                              ? (col < a.G ? kvh * a.G + col : a.Hkv * a.G + kvh)
                              : kvh * (a.G + 1) + (col < a.G ? col : a.G);
         qp = (const uint16_t*)a.q + ((long)b * a.Hkv * (a.G + 1) + head) * D;
-      } else {
-        qp = col < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + col) * D
-                       : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      } else {  // noise column G + i: q2 head kvh * G2 + i
+        qp = col < a.G
+                 ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + col) * D
+                 : (const uint16_t*)a.q2 + (((long)b * a.Hkv + kvh) * a.G2 + (col - a.G)) * D;
       }
       qp += 8 * blk;
     }
@@ -357,7 +359,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
 #pragma unroll
           for (int s = 0; s < NQ; ++s)
             s2 = Op::mma(ka2[u + v][s], qb[s], s2);
-          if (col == a.G) sacc[v] = s2;
+          if (col >= a.G) sacc[v] = s2;
         }
       }
 
@@ -483,7 +485,7 @@ inline int launch_sdpa_mfma_16(const SdpaArgs& a, int gc, int waves, int nblocks
   return check_launch("sdpa_dual_v (mfma)");
 }
 
-// Fused GDA decode step, 16-bit cache, head_dim 128: gc = columns (G + 1,
+// Fused GDA decode step, 16-bit cache, head_dim 128: gc = columns (G + G2,
 // rounded up to 2, 4, 8 or 16); waves 8, or 4 (short contexts: one
 // workgroup per CU reaches its first tile sooner).  16 columns: always 4.
 template <typename T>

@@ -291,7 +291,7 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
 // verify slab) read each row in several workgroups and use cached loads, so
 // all but the first find the rows in L2 or the Infinity Cache.
 // DUAL: fused GDA decode step, as in sdpa_mfma_kernel: head h < G of a
-// column scores against k, head G (the noise head) against k2.
+// column scores against k, heads G..G+G2-1 (the noise heads) against k2.
 // NB: column blocks per wave.  Block bb holds heads bb*GC .. bb*GC+GC-1 of
 // the workgroup's NB*GC; the K and V codes of a tile are unpacked once and
 // feed every block's MFMAs, so a verify slab (e.g. 5 rows x GQA 4 = 20
@@ -332,7 +332,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int vh0 = chunk * GCW;
   const int nvh = min(GCW, a.GV - vh0);
   // First output row: y row (non-DUAL) or partial row (DUAL) of head 0.
-  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + 1)
+  const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + a.G2)
                           : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
   const int grp = col / GC;  // scale group of this column
@@ -439,13 +439,15 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     const uint16_t* qp =
         (const uint16_t*)a.q + (qrow0 + (hb[bb] < nvh ? hb[bb] : 0)) * D + 32 * blk;
     if constexpr (DUAL) {
-      if (a.from_proj) {  // q_proj heads: stripe g*(G+1)+j, or origin-first
-        const int head = a.q_origin_first ? (h < a.G ? kvh * a.G + h : a.Hkv * a.G + kvh)
-                                          : kvh * (a.G + 1) + (h < a.G ? h : a.G);
+      const int hq = h < nvh ? h : 0;  // unused columns load head 0 (in bounds)
+      if (a.from_proj) {  // q_proj heads (G2 == 1): stripe g*(G+1)+j, or origin-first
+        const int head = a.q_origin_first ? (hq < a.G ? kvh * a.G + hq : a.Hkv * a.G + kvh)
+                                          : kvh * (a.G + 1) + (hq < a.G ? hq : a.G);
         qp = (const uint16_t*)a.q + ((long)b * a.Hkv * (a.G + 1) + head) * D;
-      } else {
-        qp = h < a.G ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + h) * D
-                     : (const uint16_t*)a.q2 + ((long)b * a.Hkv + kvh) * D;
+      } else {  // noise column G + i: q2 head kvh * G2 + i
+        qp = hq < a.G
+                 ? (const uint16_t*)a.q + ((long)b * a.Hq + (long)kvh * a.G + hq) * D
+                 : (const uint16_t*)a.q2 + (((long)b * a.Hkv + kvh) * a.G2 + (hq - a.G)) * D;
       }
       qp += 32 * blk;
     }
@@ -580,7 +582,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           }
           s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[0][s], s2, 0, 0, 0);
         }
-        const bool noise = h == a.G;
+        const bool noise = h >= a.G;
 #pragma unroll
         for (int r = 0; r < 4; ++r) sacc[0][r] = noise ? s2[r] : sacc[0][r];
 #pragma unroll
@@ -767,7 +769,7 @@ int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hip
 }
 
 // Fused GDA decode step over the packed cache: gc columns per scale group
-// (G + 1 rounded up to a power of two, gc * 128 / gs <= 16), 4 waves.
+// (G + G2 rounded up to a power of two, gc * 128 / gs <= 16), 4 waves.
 template <int BITS, int GS>
 int launch_gda_decode_mfma_q_gs(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;

@@ -50,9 +50,10 @@ struct SdpaArgs {
   float qscale;     // softmax scale * log2(e)
   // Fused GDA decode step (origin and noise passes in one launch, then the
   // merge applies gda_post_split): q holds the origin queries (B, Hq, 1, D)
-  // with Hq = Hkv * G, q2 the noise queries (B, Hkv, 1, D), k the origin
-  // keys, k2 the noise keys; partial rows are (b, KV head, column) with
-  // columns 0..G-1 the origin heads and G the noise head.
+  // with Hq = Hkv * G, q2 the noise queries (B, Hkv * G2, 1, D), k the
+  // origin keys, k2 the noise keys; partial rows are (b, KV head, column)
+  // with columns 0..G-1 the origin heads and G..G+G2-1 the noise heads
+  // (G2 below; one in the 12.7B layout, G / G2 origin heads per noise head).
   const void* q2;
   const void* k2;
   const uint32_t* k2d;  // packed noise keys (data, scales, biases)
@@ -92,7 +93,7 @@ struct SdpaArgs {
   void* y2;
   long y2_row0;
   int nqb_origin;
-  int G2;
+  int G2;  // noise heads per KV head (the prefill chunk and the fused decode step)
   int q_groups, q_gr;
   int rope_pos0;
 };

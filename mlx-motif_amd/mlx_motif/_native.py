@@ -118,6 +118,15 @@ _SIGNATURES = {
         [_vp] * 17 + [_c_f, _c_f, _vp] + [_c_int] * 9
         + [_c_f, _c_f, _c_f, _c_int, _vp, _c_sz, _vp],
     ),
+    "motif_gda_decode_heads_workspace_bytes": (_c_sz, [_c_int] * 6),
+    "motif_gda_decode_heads": (
+        _c_int,
+        [_vp] * 12 + [_c_f, _c_f, _vp] + [_c_int] * 8 + [_c_f, _vp, _c_sz, _vp],
+    ),
+    "motif_gda_decode_q_heads": (
+        _c_int,
+        [_vp] * 20 + [_c_f, _c_f, _vp] + [_c_int] * 10 + [_c_f, _vp, _c_sz, _vp],
+    ),
     "motif_gda_decode_q_append": (
         _c_int,
         [_vp] * 20 + [_c_f, _c_f, _vp] + [_c_int] * 9 + [_c_f, _vp, _c_sz, _vp],

@@ -12,6 +12,11 @@ The reference runs this as three kernel calls (DUAL_V path of
 at head_dim 128, ``motif_gda_decode`` serves both passes from one attention
 launch that reads each KV head's k1, k2, v1 and v2 rows once (the separate
 calls read v1 and v2 twice), and applies the epilogue in the split merge.
+``q2`` may hold any multiple of H_kv noise heads (the reference's calls are
+GQA calls, and ``gda_post_split`` pairs origin head h with noise head
+h // gr): one per KV head is the 12.7B layout (``motif_gda_decode``), more
+take ``motif_gda_decode_heads`` (e.g. 8 origin and 8 noise heads over 4 KV
+heads, gr = 1).
 Other shapes compose the separate native calls inside the library.
 ``gda_decode_attention_q4`` is the same step over the packed q4/q8 cache
 (QUANT_SDPA path, ``model.py:717-748``: two ``sdpa_dual_v_q4`` calls).
@@ -101,6 +106,19 @@ def _check_q_slots(slots, B, H_kv, KV_cap, D, bits, group_size, dtype):
                 raise TypeError(f"scales/biases dtype {x.dtype} must match q dtype {dtype}")
 
 
+def _noise_heads(q1, q2, H_kv, gr, name):
+    """Noise heads of the step (q2's head count): the reference's contract
+    q_origin == q_groups * gr (gda.py:248), with q_groups a multiple of H_kv
+    since the noise pass is a GQA call (attention.py:237-243)."""
+    B, H_o, S_q, D = q1.shape
+    assert S_q == 1 and q2.shape[2] == 1, f"{name} is decode-only"
+    H_n = q2.shape[1]
+    assert q2.shape == (B, H_n, 1, D), "q2 must be (B, q_groups, 1, D)"
+    assert H_o == H_n * gr, f"q_origin={H_o} != q_groups({H_n}) * gr({gr})"
+    assert H_n % H_kv == 0, f"q_groups={H_n} must be a multiple of H_kv={H_kv}"
+    return H_n
+
+
 def _require_in_place(tensors):
     for t in tensors:
         if not t.is_contiguous():
@@ -111,11 +129,12 @@ def _require_in_place(tensors):
 def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lambda_full,
                          lambda_init: float, gr: int, eps: float = 1e-5,
                          kv_len: int | None = None, new_kv=None):
-    """``q1`` (B, H_kv*gr, 1, D) origin queries, ``q2`` (B, H_kv, 1, D) noise
-    queries; ``k1, k2, v1, v2`` (B, H_kv, KV_cap, D) full-capacity 4-slot
+    """``q1`` (B, q_groups*gr, 1, D) origin queries, ``q2`` (B, q_groups, 1, D)
+    noise queries with q_groups a multiple of H_kv (H_kv in the 12.7B
+    layout); ``k1, k2, v1, v2`` (B, H_kv, KV_cap, D) full-capacity 4-slot
     cache buffers with ``kv_len`` live rows (default ``KV_cap``).  With
     ``new_kv`` the token's rows are first written at row ``kv_len - 1``.
-    Returns (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
+    Returns (B, q_groups*gr, 1, 2D) in ``q1.dtype``."""
     if kv_len is None:
         kv_len = k1.shape[2]
     if new_kv is not None:
@@ -129,10 +148,8 @@ def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lam
                                               lambda_full, lambda_init, gr, eps, kv_len)
     B, H_o, S_q, D = q1.shape
     _, H_kv, KV_cap, _ = k1.shape
-    assert S_q == 1 and q2.shape[2] == 1, "gda_decode_attention is decode-only"
+    H_n = _noise_heads(q1, q2, H_kv, gr, "gda_decode_attention")
     assert D % 32 == 0, f"D={D} must be a multiple of 32"
-    assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
-    assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
     for t in (k2, v1, v2):
         assert t.shape == (B, H_kv, KV_cap, D), "k2,v1,v2 must match (B, H_kv, KV_cap, D)"
     assert 0 <= kv_len <= KV_cap, f"kv_len={kv_len} must be in [0, {KV_cap}]"
@@ -145,12 +162,22 @@ def gda_decode_attention(q1, q2, k1, k2, v1, v2, scale: float, subln_weight, lam
     lam = _common.f32_scalar_tensor(lambda_full, dev)
     y = torch.empty((B, H_o, 1, 2 * D), dtype=q1.dtype, device=dev)
     lib = _native.lib()
+    caches = (k1.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr())
+    if H_n != H_kv:  # several noise heads per KV head
+        ws = _native.workspace(dev, lib.motif_gda_decode_heads_workspace_bytes(
+            B, H_o, H_n, H_kv, kv_len, D))
+        rows = tuple(t.data_ptr() for t in new_kv) if new_kv is not None else (None,) * 4
+        _native.check(lib.motif_gda_decode_heads(
+            q1.data_ptr(), q2.data_ptr(), *rows, *caches, w.data_ptr(), lam.data_ptr(),
+            float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q1.dtype), B,
+            H_o, H_n, H_kv, D, KV_cap, kv_len, float(scale), ws.data_ptr(), ws.numel(),
+            _native.stream_of(dev)))
+        return y
     n = lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D)
     ws = _native.workspace(dev, n)
     tail = (w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps), y.data_ptr(),
             _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len, float(scale),
             ws.data_ptr(), ws.numel(), _native.stream_of(dev))
-    caches = (k1.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr())
     if new_kv is None:
         rc = lib.motif_gda_decode(q1.data_ptr(), q2.data_ptr(), *caches, *tail)
     else:
@@ -181,8 +208,9 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     """The decode step over the packed cache: each ``*_q`` is a ``(data
     uint32, scales, biases)`` triple of (B, H_kv, KV_cap, ...) tensors as
     ``sdpa_dual_v_q4`` takes them.  With ``new_kv`` the token's rows (in
-    ``q1.dtype``) are first quantised into row ``kv_len - 1``.  Returns
-    (B, H_kv*gr, 1, 2D) in ``q1.dtype``."""
+    ``q1.dtype``) are first quantised into row ``kv_len - 1``.  ``q2`` as
+    for ``gda_decode_attention``.  Returns (B, q_groups*gr, 1, 2D) in
+    ``q1.dtype``."""
     B, H_o, S_q, D = q1.shape
     _, H_kv, KV_cap, n_uint = k1_q[0].shape
     if kv_len is None:
@@ -201,9 +229,7 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     assert n_uint * (32 // bits) == D, (
         f"k_data last axis = {n_uint} ⇒ packed D = {n_uint * (32 // bits)}, expected {D}"
     )
-    assert S_q == 1 and q2.shape[2] == 1, "gda_decode_attention_q4 is decode-only"
-    assert H_o == H_kv * gr, f"q_origin={H_o} != q_groups({H_kv}) * gr({gr})"
-    assert q2.shape == (B, H_kv, 1, D), "q2 must be (B, H_kv, 1, D)"
+    H_n = _noise_heads(q1, q2, H_kv, gr, "gda_decode_attention_q4")
     _q_contract(D, H_o, H_kv, group_size, bits, kv_len, KV_cap)
     _check_q_slots(slots, B, H_kv, KV_cap, D, bits, group_size, q1.dtype)
     dev = _native.require_device(q1, q2, *(x for t in slots for x in t), *(new_kv or ()))
@@ -215,8 +241,18 @@ def gda_decode_attention_q4(q1, q2, k1_q: tuple, k2_q: tuple, v1_q: tuple, v2_q:
     lam = _common.f32_scalar_tensor(lambda_full, dev)
     y = torch.empty((B, H_o, 1, 2 * D), dtype=q1.dtype, device=dev)
     lib = _native.lib()
-    ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
     ptrs = [x.data_ptr() for t in slots for x in t]
+    if H_n != H_kv:  # several noise heads per KV head
+        ws = _native.workspace(dev, lib.motif_gda_decode_heads_workspace_bytes(
+            B, H_o, H_n, H_kv, kv_len, D))
+        rows = tuple(t.data_ptr() for t in new_kv) if new_kv is not None else (None,) * 4
+        _native.check(lib.motif_gda_decode_q_heads(
+            q1.data_ptr(), q2.data_ptr(), *rows, *ptrs, w.data_ptr(), lam.data_ptr(),
+            float(1.0 - lambda_init), float(eps), y.data_ptr(), _native.dtype_code(q1.dtype), B,
+            H_o, H_n, H_kv, D, KV_cap, kv_len, bits, group_size, float(scale), ws.data_ptr(),
+            ws.numel(), _native.stream_of(dev)))
+        return y
+    ws = _native.workspace(dev, lib.motif_gda_decode_workspace_bytes(B, H_kv, gr, kv_len, D))
     tail = (w.data_ptr(), lam.data_ptr(), float(1.0 - lambda_init), float(eps), y.data_ptr(),
             _native.dtype_code(q1.dtype), B, H_kv, gr, D, KV_cap, kv_len, bits, group_size,
             float(scale), ws.data_ptr(), ws.numel(), _native.stream_of(dev))

@@ -235,6 +235,73 @@ public enum MotifHIP {
         return MotifHIPStatus(rawValue: rc) ?? .hip
     }
 
+    /// Workspace bytes of a decode step with any noise-head count (0 when
+    /// kvHeads does not divide noiseHeads or noiseHeads does not divide
+    /// originHeads).
+    public static func gdaDecodeHeadsWorkspaceBytes(batch: Int, originHeads: Int,
+                                                   noiseHeads: Int, kvHeads: Int, kvLen: Int,
+                                                   headDim: Int) -> Int {
+        Int(motif_gda_decode_heads_workspace_bytes(Int32(batch), Int32(originHeads),
+                                                   Int32(noiseHeads), Int32(kvHeads),
+                                                   Int32(kvLen), Int32(headDim)))
+    }
+
+    /// The decode step for any noise-head count: originHeads queries over k1
+    /// and noiseHeads over k2 (both multiples of kvHeads), origin head h paired
+    /// with noise head h / (originHeads / noiseHeads) in gda_post_split.
+    /// gdaDecode is the case noiseHeads == kvHeads.  newRows: nil, or the
+    /// token's (k1, k2, v1, v2) rows, written at row kvLen - 1 first.
+    public static func gdaDecodeHeads(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        newRows: (UnsafeRawPointer, UnsafeRawPointer, UnsafeRawPointer, UnsafeRawPointer)?,
+        keys1: UnsafeMutableRawPointer, keys2: UnsafeMutableRawPointer,
+        value1: UnsafeMutableRawPointer, value2: UnsafeMutableRawPointer,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, originHeads: Int, noiseHeads: Int, kvHeads: Int,
+        headDim: Int, kvCapacity: Int, kvLen: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_heads(originQueries, noiseQueries, newRows?.0, newRows?.1,
+                                        newRows?.2, newRows?.3, keys1, keys2, value1, value2,
+                                        sublnWeight, lambdaFull, oneMinusLambdaInit, eps, output,
+                                        dtype.rawValue, Int32(batch), Int32(originHeads),
+                                        Int32(noiseHeads), Int32(kvHeads), Int32(headDim),
+                                        Int32(kvCapacity), Int32(kvLen), scale, workspace,
+                                        workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
+    /// Same over the packed q4/q8 cache (new rows quantised as quantWrite4
+    /// stores them).
+    public static func gdaDecodeQuantizedHeads(
+        originQueries: UnsafeRawPointer, noiseQueries: UnsafeRawPointer,
+        newRows: (UnsafeRawPointer, UnsafeRawPointer, UnsafeRawPointer, UnsafeRawPointer)?,
+        keys1: MotifHIPQuantizedTriple, keys2: MotifHIPQuantizedTriple,
+        value1: MotifHIPQuantizedTriple, value2: MotifHIPQuantizedTriple,
+        sublnWeight: UnsafeRawPointer, lambdaFull: UnsafePointer<Float>,
+        oneMinusLambdaInit: Float, eps: Float, output: UnsafeMutableRawPointer,
+        dtype: MotifHIPDType, batch: Int, originHeads: Int, noiseHeads: Int, kvHeads: Int,
+        headDim: Int, kvCapacity: Int, kvLen: Int, bits: Int, groupSize: Int, scale: Float,
+        workspace: UnsafeMutableRawPointer?, workspaceBytes: Int,
+        stream: UnsafeMutableRawPointer?
+    ) -> MotifHIPStatus {
+        let rc = motif_gda_decode_q_heads(originQueries, noiseQueries, newRows?.0, newRows?.1,
+                                          newRows?.2, newRows?.3,
+                                          keys1.data, keys1.scales, keys1.biases,
+                                          keys2.data, keys2.scales, keys2.biases,
+                                          value1.data, value1.scales, value1.biases,
+                                          value2.data, value2.scales, value2.biases,
+                                          sublnWeight, lambdaFull, oneMinusLambdaInit, eps,
+                                          output, dtype.rawValue, Int32(batch),
+                                          Int32(originHeads), Int32(noiseHeads),
+                                          Int32(kvHeads), Int32(headDim), Int32(kvCapacity),
+                                          Int32(kvLen), Int32(bits), Int32(groupSize), scale,
+                                          workspace, workspaceBytes, stream)
+        return MotifHIPStatus(rawValue: rc) ?? .hip
+    }
+
     /// The RoPE position scale of a model's rope_scaling config
     /// (MotifTypes.swift:218, read as mlx-lm's initialize_rope reads it: the
     /// type is `type`, else `ropeType`, else "default").  No config and

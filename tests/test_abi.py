@@ -164,6 +164,43 @@ def test_gda_decode_rejections_and_workspace():
     assert lib.motif_gda_decode_workspace_bytes(0, 8, 4, 16, 128) == 0
 
 
+def test_gda_decode_heads_rejections_and_workspace():
+    """The step for any noise-head count: q2's heads must be a multiple of
+    H_kv and divide q1's (q_origin == q_groups * gr), and the new-row
+    pointers come all null or all set; all refused before any HIP call."""
+    lib = _native.lib()
+
+    def args(Hq1, Hq2, Hkv, rows=(None,) * 4, dtype=0, kv_cap=1024, kv_len=1024, ws=None, n=0):
+        return ((1, 1) + tuple(rows) + (1,) * 5 + (1, 0.8, 1e-5, 1, dtype, 1, Hq1, Hq2, Hkv, 128,
+                kv_cap, kv_len, 0.1, ws, n, None))
+
+    st = lib.motif_gda_decode_heads(*args(8, 6, 4))
+    assert st == _native.MOTIF_ERR_CONTRACT and "H_q2=6 must be a multiple of H_kv=4" in _err()
+    st = lib.motif_gda_decode_heads(*args(12, 8, 4))
+    assert st == _native.MOTIF_ERR_CONTRACT and "H_q1=12 must be a multiple of H_q2=8" in _err()
+    st = lib.motif_gda_decode_heads(*args(8, 8, 4, rows=(1, 1, None, 1)))
+    assert st == _native.MOTIF_ERR_CONTRACT and "all null or all set" in _err()
+    st = lib.motif_gda_decode_heads(*args(8, 8, 4, dtype=7))
+    assert st == _native.MOTIF_ERR_CONTRACT and "dtype" in _err()
+    st = lib.motif_gda_decode_heads(*args(8, 8, 4))
+    assert st == _native.MOTIF_ERR_WORKSPACE and "workspace" in _err()
+    qargs = ((1, 1) + (None,) * 4 + (1,) * 14 + (0.8, 1e-5, 1, 0, 1, 8, 6, 4, 128, 1024, 1024,
+             4, 64, 0.1, None, 0, None))
+    st = lib.motif_gda_decode_q_heads(*qargs)
+    assert st == _native.MOTIF_ERR_CONTRACT and "multiple of H_kv" in _err()
+
+    ws = lib.motif_gda_decode_heads_workspace_bytes
+    assert ws(1, 8, 6, 4, 1024, 128) == 0 and ws(1, 12, 8, 4, 1024, 128) == 0
+    assert ws(0, 8, 8, 4, 1024, 128) == 0
+    # one noise head per KV head: the same layout as motif_gda_decode
+    assert ws(1, 32, 8, 8, 16000, 128) == lib.motif_gda_decode_workspace_bytes(1, 8, 4, 16000, 128)
+    # 8 origin + 8 noise heads over 4 KV heads: partial rows of 4 columns
+    # per KV head, and the composed path's two (B, 8, 1, 2D) fp32 outputs
+    n = ws(1, 8, 8, 4, 1024, 128)
+    assert n >= 4 * 4 * (2 * 128 + 2) * 4 and n >= 2 * 8 * 2 * 128 * 4
+    assert ws(1, 8, 8, 4, 16000, 128) >= n
+
+
 def test_tuning_changes_while_other_threads_size_calls():
     """motif_set_tuning from one thread while others size calls: each call
     reads one snapshot of the knobs, so every size is the one of either

@@ -136,6 +136,7 @@ def test_swift_calls_match_the_c_declarations():
     called = {n for n, _ in calls}
     for name in ("motif_sdpa_dual_v", "motif_sdpa_dual_v_q", "motif_gda_decode",
                  "motif_gda_decode_q", "motif_gda_decode_append", "motif_gda_decode_q_append",
+                 "motif_gda_decode_heads", "motif_gda_decode_q_heads",
                  "motif_gda_decode_proj_scaled", "motif_gda_decode_q_proj_scaled",
                  "motif_rope_split4_scaled", "motif_gda_prefill_proj_scaled",
                  "motif_gda_post_split", "motif_polynorm", "motif_quant_write4"):
