@@ -161,13 +161,20 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
   // the kernel with LDS-shared K/V tiles reads the cache once per block of
   // up to 128 heads instead of once per 8.
   if ((dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
-      use_shared_tiles(a.GV, kv_len) && tile_softmax_scale_ok(a.qscale) &&
+      use_shared_tiles(a.GV, kv_len) && kv_len <= kMfmaMaxRows &&
+      tile_softmax_scale_ok(a.qscale) &&
       aligned(q, 16) && aligned(y, 16) && aligned(k, 16) && aligned(v1, 16) &&
       aligned(v2, 16)) {
     const PrefillPlan pp = plan_prefill(B, Hq, Hkv, S_q, kv_len, D);
     a.nchunk = pp.nqb;
     a.nsplit = pp.nsplit;
     a.rows_per_split = pp.rows_per_split;
+    // Chunks (64+ virtual heads per KV head) deal their tiles to the splits
+    // round robin: the causal limit then costs every split alike (512 rows
+    // over 3716: 69.9 -> 67.6-68.1 us; 2048 over 4228 201.7 -> 191.8).  Long
+    // slabs keep contiguous ranges (5 rows over 32768: 37.4 against 37.9
+    // round robin).
+    a.tiles_rr = a.GV >= kPrefillMinHeads ? 1 : 0;
     a.fused_merge = 0;
     a.counters = nullptr;
     a.part_o = a.part_ml = nullptr;

@@ -41,6 +41,10 @@ struct SdpaArgs {
   // the matrix-core decode kernels deal blocks of (waves x 16) rows to the
   // splits round robin and ignore rows_per_split.
   int nsplit, rows_per_split;
+  // Shared-tile multi-row kernel: its 32-row tiles dealt to the splits round
+  // robin (1: tile i of split s is tile i * nsplit + s) or in contiguous
+  // ranges of rows_per_split rows (0).
+  int tiles_rr;
   int group_size;
   int fused_merge;  // 1: last-arriving workgroup merges; 0: sdpa_merge_kernel does
   // Split partial outputs stored as fp16 o / l (the shared-tile kernels of

@@ -438,8 +438,17 @@ sdpa_prefill_kernel(SdpaArgs a) {
     lim_lo[cb] = __builtin_amdgcn_readfirstlane(lim_lo[cb]);
   }
   const int max_lim = vhead_limit_max(a, wg_vh0, min(NW * 16 * NCB, a.GV - wg_vh0));
-  const int r_begin = split * a.rows_per_split;
-  const int r_end = min(r_begin + a.rows_per_split, max_lim);
+  // The block's visible rows [0, max_lim) in 32-row tiles, dealt to the
+  // splits round robin (a.tiles_rr: tile i of split s is tile i * nsplit +
+  // s, so every split of a block gets the same tile count, +-1, whatever the
+  // causal limit) or in contiguous ranges of rows_per_split rows (tile
+  // i of split s is tile s * tps + i).  Rows at or past r_end = max_lim are
+  // masked.
+  const int ns = a.nsplit;
+  const int r_end = max_lim;
+  const int tps = a.rows_per_split / TR;  // tiles per contiguous range
+  const int tstride = a.tiles_rr ? ns : 1;
+  const int tbase = a.tiles_rr ? split : split * tps;
   const long qrow0 = ((long)b * a.Hq + (long)kvh * a.G) * a.S_q;  // row of virtual head 0
 
   // Q^T, B operand of the 16x16x32 MFMA: lane (col, blk) holds its column's
@@ -461,9 +470,10 @@ sdpa_prefill_kernel(SdpaArgs a) {
     asm volatile("" ::"v"(qb[cb][0]), "v"(qb[cb][1]), "v"(qb[cb][2]), "v"(qb[cb][3]));
   }
 
-  // Rows [r_begin, r_end) of this KV head through range-checked resources.
-  const long hrow0 = (long)unit * a.kv_cap + r_begin;
-  const unsigned nbytes = (unsigned)(max(r_end - r_begin, 0) * D * 2);
+  // Rows [0, r_end) of this KV head through range-checked resources (byte
+  // offsets stay 32-bit: kv_len <= kMfmaMaxRows, checked on the host).
+  const long hrow0 = (long)unit * a.kv_cap;
+  const unsigned nbytes = (unsigned)(max(r_end, 0) * D * 2);
   const __amdgpu_buffer_rsrc_t rsrc[3] = {
       stream_rsrc((const uint16_t*)a.k + hrow0 * D, nbytes),
       stream_rsrc((const uint16_t*)a.v1 + hrow0 * D, nbytes),
@@ -486,7 +496,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
       const int g = (wave + c * NW) % 8;
       const int r = 4 * g + lane / 16;
       const int chunk = (lane % 16) ^ (r % 16);
-      const unsigned voff = (unsigned)((tile * TR + r) * D * 2 + chunk * 16);
+      const unsigned voff = (unsigned)(((tile * tstride + tbase) * TR + r) * D * 2 + chunk * 16);
       lds_copy16_rsrc(rsrc[t], voff, lds_byte_addr(&ring[st][t][g * 1024]));
     }
   };
@@ -494,8 +504,9 @@ sdpa_prefill_kernel(SdpaArgs a) {
   SwizzledTileAcc<T> st_acc[NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) st_acc[cb].init();
-  const int nrows = max(r_end - r_begin, 0);
-  const int ntiles = (nrows + TR - 1) / TR;
+  const int n_vis = (max(r_end, 0) + TR - 1) / TR;  // the block's tiles
+  const int ntiles = a.tiles_rr ? (n_vis > split ? (n_vis - split + ns - 1) / ns : 0)
+                                : max(0, min(tps, n_vis - tbase));
 
   // Every workgroup's tile count is uniform, so every barrier is reached by
   // all of its threads.  Software-pipelined over tiles: the S^T products of
@@ -539,7 +550,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
         if (wave_busy) SwizzledTileAcc<T>::scores(ring[(i + 1) % NS][0], qb[0], s_nxt, col, blk);
       }
       if (wave_busy) {
-        const int t0 = r_begin + i * TR;
+        const int t0 = (i * tstride + tbase) * TR;
         st_acc[0].update(s_cur, ring[i % NS][1], ring[i % NS][2], t0, r_end, lim[0], a.qscale,
                          col, blk, t0 + TR <= min(r_end, lim_lo[0]));
         s_cur[0] = s_nxt[0];
@@ -553,7 +564,7 @@ sdpa_prefill_kernel(SdpaArgs a) {
       floatx4 sacc[NCB][2];
       tile_scores_n<T, NCB>(ring[i % NS][0], qb, sacc, col, blk);
       V8 pb[NCB];
-      const int t0 = r_begin + i * TR;
+      const int t0 = (i * tstride + tbase) * TR;
 #pragma unroll
       for (int cb = 0; cb < NCB; ++cb)
         pb[cb] = st_acc[cb].softmax(sacc[cb], t0, r_end, lim[cb], a.qscale, blk,
