@@ -223,6 +223,13 @@ __device__ inline float group_sum(float x) {
   return x;
 }
 
+// Maximum of two floats as v_maximum(3)_f32 (the IEEE 754-2019 maximum):
+// fmaxf (maxnum) first canonicalises each operand the compiler cannot prove
+// canonical -- MFMA results, cross-lane moves -- with a v_max_f32 x, x of
+// its own, tripling a max tree over scores.  For non-NaN operands the value
+// is fmaxf's (a NaN operand gives NaN instead of the other operand).
+__device__ inline float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 template <int W>
 __device__ inline float group_max(float x) {
   if constexpr (W >= 2) x = fmaxf(x, dpp<kDppQuadXor1>(x));

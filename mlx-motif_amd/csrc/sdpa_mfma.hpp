@@ -373,11 +373,11 @@ sdpa_mfma_kernel(SdpaArgs a) {
           const int row = tile_row(k0 + u + v) + 4 * blk + r;
           const bool ok = row < lim;
           sc[4 * v + r] = ok ? sacc[v][r] * a.qscale : kNegSentinel;
-          mx = fmaxf(mx, sc[4 * v + r]);
+          mx = vmax(mx, sc[4 * v + r]);
         }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = vmax(mx, __shfl_xor(mx, 16));
+      mx = vmax(mx, __shfl_xor(mx, 32));
       if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
         const float m_new = fmaxf(m_run, mx);
         const float fac = fast_exp2(m_run - m_new);

@@ -56,8 +56,8 @@ __device__ inline void swap32(float x, float& a, float& b) {
 __device__ inline float rows4_max(float x) {
   float a, b;
   swap16(x, a, b);
-  swap32(fmaxf(a, b), a, b);
-  return fmaxf(a, b);
+  swap32(vmax(a, b), a, b);
+  return vmax(a, b);
 }
 // Sum over the four 16-lane rows; every lane receives the same bits (the
 // operands of each add are the same pair, in the same order, on both
@@ -609,10 +609,10 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           const int row = row0 + r;
           const bool ok = row < lim[bb];  // lim <= max_lim
           sc[r] = ok ? t * a.qscale : kNegSentinel;
-          mx = fmaxf(mx, sc[r]);
+          mx = vmax(mx, sc[r]);
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = vmax(mx, __shfl_xor(mx, 16));
+        mx = vmax(mx, __shfl_xor(mx, 32));
         if (__ballot(mx > m_run[bb] + kSlack) != 0) {
           const float m_new = fmaxf(m_run[bb], mx);
           const float fac = fast_exp2(m_run[bb] - m_new);

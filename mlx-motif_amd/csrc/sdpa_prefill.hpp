@@ -161,8 +161,8 @@ struct SwizzledTileAcc {
           sc[4 * h + r] = 16 * h + r < vis ? sc[4 * h + r] : -__builtin_inff();
       }
     }
-    float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
-                     fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    float mx = vmax(vmax(vmax(sc[0], sc[1]), vmax(sc[2], sc[3])),
+                    vmax(vmax(sc[4], sc[5]), vmax(sc[6], sc[7])));
     mx = fmaxf(rows4_max(mx) * qscale, kNegSentinel);
     if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
       const float m_new = fmaxf(m_run, mx);

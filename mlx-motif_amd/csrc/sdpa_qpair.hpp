@@ -380,8 +380,8 @@ sdpa_qpair_kernel(SdpaArgs a) {
         x[i] = row < lim ? x[i] : -__builtin_inff();
       }
     }
-    float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
-                     fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    float mx = vmax(vmax(vmax(x[0], x[1]), vmax(x[2], x[3])),
+                    vmax(vmax(x[4], x[5]), vmax(x[6], x[7])));
     mx = rows4_max(mx) * qscale;
     if (__ballot(mx > m_run + kSlack) != 0) {
       const float m_new = fmaxf(m_run, mx);
