@@ -23,7 +23,12 @@
 //     which is where the C layout of the two score tiles leaves each lane's
 //     softmax weights, so P never moves between lanes.  The V^T operand of
 //     channel 8*col + i takes code i of the lane's row words, paired across
-//     rows with one v_perm_b32 and masked (q4: nibble i as u or 16u).
+//     rows with one v_perm_b32 (a byte per half).  q4: channel 2b (the low
+//     nibble of byte b) masks it to u; channel 2b + 1 takes the whole byte
+//     u + 16u' unmasked, and the epilogue recovers the high nibble's sum as
+//     the difference of the two accumulators (one AND fewer per operand
+//     dword; every product stays exact and the difference carries one fp32
+//     rounding of a sum of similar size).
 //
 // Softmax: log2 units, one running-max update per pair (lazy rescaling with
 // the packed kernel's slack), cross-row maxima with v_permlane16/32_swap,
@@ -443,10 +448,9 @@ sdpa_qpair_kernel(SdpaArgs a) {
           const int by = BITS == 4 ? i / 2 : i % 4;
           const uint32_t x1 = pair_bytes(P.v1[T][2 * h][wi], P.v1[T][2 * h + 1][wi], by);
           const uint32_t x2 = pair_bytes(P.v2[T][2 * h][wi], P.v2[T][2 * h + 1][wi], by);
-          if constexpr (BITS == 4) {
-            const uint32_t m = (i & 1) ? 0x00F000F0u : 0x000F000Fu;
-            a1[2 * T + h] = x1 & m;
-            a2[2 * T + h] = x2 & m;
+          if constexpr (BITS == 4) {  // even i: low nibbles; odd i: whole bytes
+            a1[2 * T + h] = (i & 1) ? x1 : x1 & 0x000F000Fu;
+            a2[2 * T + h] = (i & 1) ? x2 : x2 & 0x000F000Fu;
           } else {
             a1[2 * T + h] = x1;
             a2[2 * T + h] = x2;
@@ -482,7 +486,8 @@ sdpa_qpair_kernel(SdpaArgs a) {
 
   // acc[i][r] of lane (col, blk) is channel 8*(4*blk + r) + i of head hh,
   // valid where that channel's group is g.  Codes were u * 2^-24 (q8, q4 low
-  // nibbles: even i) or 16u * 2^-24 (q4 high nibbles: odd i).
+  // nibbles: even i) or, for q4's odd i, whole bytes (u_lo + 16 u_hi) * 2^-24,
+  // so acc[i] - acc[i - 1] is the high nibbles' 16 u_hi * 2^-24 sum.
   __shared__ __attribute__((aligned(16))) float lds_o[NW][GC][2 * D + kLdsPad];
   __shared__ float lds_m[NW][GC];
   __shared__ float lds_l[NW][GC];
@@ -497,8 +502,9 @@ sdpa_qpair_kernel(SdpaArgs a) {
       float o1[8], o2[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        o1[i] = fmaf(acc1[i][r], f[i], be1);
-        o2[i] = fmaf(acc2[i][r], f[i], be2);
+        const bool odd4 = BITS == 4 && (i & 1);
+        o1[i] = fmaf(odd4 ? acc1[i][r] - acc1[i - 1][r] : acc1[i][r], f[i], be1);
+        o2[i] = fmaf(odd4 ? acc2[i][r] - acc2[i - 1][r] : acc2[i][r], f[i], be2);
       }
       *reinterpret_cast<float4*>(&lds_o[wave][hh][ch]) = make_float4(o1[0], o1[1], o1[2], o1[3]);
       *reinterpret_cast<float4*>(&lds_o[wave][hh][ch + 4]) = make_float4(o1[4], o1[5], o1[6], o1[7]);
