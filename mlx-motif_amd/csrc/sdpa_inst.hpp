@@ -69,9 +69,9 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
     const bool aligned = (data_bits & 15u) == 0 && (scale_bits & (ng == 1 ? 7u : 15u)) == 0 &&
                          a.kv_cap % 4 == 0 && a.kv_len <= kMfmaMaxRows;
     if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16) {
-      // Paired-tile kernel: 4-bit by default (qpair 1); 8-bit too with
-      // qpair 2 (slower than the per-tile kernel there).
-      if (tuning().qpair >= (bits == 4 ? 1 : 2) && ng <= 2 && ((uintptr_t)a.q & 15u) == 0 &&
+      // Paired-tile kernel with qpair 2 only: for fp16 activations the
+      // per-tile kernel is faster at both code widths.
+      if (tuning().qpair >= 2 && ng <= 2 && ((uintptr_t)a.q & 15u) == 0 &&
           tile_softmax_scale_ok(a.qscale))
         return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);

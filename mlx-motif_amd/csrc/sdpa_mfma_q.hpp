@@ -17,13 +17,24 @@
 //     h + GC*g carries p * s_V of group g); the bias term is a per-lane fp32
 //     sum folded in at the end.
 //
-// Codes become fp16 with the exponent trick: a code placed in the mantissa
-// of 1024.0 (0x6400) reads as 1024 + u (or 1024 + 16u for the high nibble of
-// a byte), and one packed fp16 add or fma recovers u exactly.  V^T fragments
-// (4 rows x 1 channel per lane) come from one code word per row, paired
-// across rows with v_perm_b32.  Everything else (split plan, online softmax
-// in log2 units with lazy rescaling, workgroup epilogue) matches the
-// fp16-cache kernel.
+// Codes enter the MFMAs as fp16 subnormals: a code u in the low mantissa
+// bits of a zero-exponent half is the value u * 2^-24 (16u * 2^-24 for the
+// high nibble of a byte), and the matrix cores multiply subnormal fp16
+// inputs exactly, so a v_perm_b32 (q8: a byte per half) or one AND (q4: a
+// nibble per half) makes an operand, with no bias to add or subtract.
+//   K: q8 k-step s holds words 2s, 2s+1 in channel order.  q4 k-steps 0/1
+//     hold the low nibbles of words 0-1 / 2-3 and steps 2/3 their high
+//     nibbles (channel order qtile_k_channel), summed in two chains
+//     t_lo = sum q u 2^-24 and t_hi = sum q 16u 2^-24; sum q u is
+//     2^24 (t_lo + t_hi / 16).  The 2^24 rides on the softmax scale and
+//     the bias term's qsum carries 2^-24 (powers of two: exact).
+//   V^T fragments (4 rows x 1 channel per lane) take code i of one word per
+//     row, paired across rows with v_perm_b32.  q4: channel 2b (the low
+//     nibble of byte b) masks it to u; channel 2b + 1 takes the whole byte
+//     u + 16u' and the epilogue recovers the high nibble's sum as the
+//     difference of the two accumulators, times 2^20 (2^24 for the others).
+// Everything else (split plan, online softmax in log2 units with lazy
+// rescaling, workgroup epilogue) matches the fp16-cache kernel.
 #pragma once
 
 #include "quant_impl.hpp"
@@ -71,48 +82,48 @@ __device__ inline float rows4_sum(float x) {
 
 
 __device__ inline half2_t as_h2(uint32_t x) { return __builtin_bit_cast(half2_t, x); }
-
-// 1024 + u  ->  u
-__device__ inline half2_t sub1024(uint32_t x) {
-  return as_h2(x) - half2_t{(_Float16)1024.f, (_Float16)1024.f};
-}
-// 1024 + 16u  ->  u
-__device__ inline half2_t sub1024_hi(uint32_t x) {
-  return as_h2(x) * half2_t{(_Float16)0.0625f, (_Float16)0.0625f} -
-         half2_t{(_Float16)64.f, (_Float16)64.f};
-}
 __device__ inline uint32_t h2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
-// The fp16 exponent pattern 0x6400 in both halves, held in a VGPR: with the
-// mask as the one scalar operand, (x & mask) | magic is a single v_and_or_b32
-// (gfx9 VOP3 instructions take at most one scalar or literal operand, so
-// with both constants as literals the compiler emits an and plus an or).
-__device__ inline uint32_t magic_vgpr() {
-  uint32_t v;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "s"(0x64006400u));
-  return v;
+// Value of code 1 as an fp16 subnormal, and its inverse.
+constexpr float kCodeUnit = 0x1p-24f;
+constexpr float kCodeScale = 0x1p24f;
+
+// Channel (within the lane's 32-channel block) of element j of k-step s of
+// the K operand.  q4: steps 0/1 hold the low nibbles of words 0-1 / 2-3,
+// steps 2/3 their high nibbles; a word w gives (w & 0x000F000F) = nibbles 0
+// and 4, ((w >> 8) & 0x000F000F) = nibbles 2 and 6.  q8: step s holds words
+// 2s, 2s+1, bytes in order.
+template <int BITS>
+__host__ __device__ constexpr int qtile_k_channel(int s, int j) {
+  if constexpr (BITS == 4) {
+    constexpr int lo[4] = {0, 4, 2, 6};
+    return 16 * (s & 1) + 8 * (j / 4) + lo[j % 4] + (s >> 1);
+  } else {
+    return 8 * s + j;
+  }
 }
 
-// 8 channels of one q4 word as exact fp16 codes, in the order
-// [0, 4, 1, 5, 2, 6, 3, 7] (q4_order): k-operand order of the K fragments.
-__device__ inline half8_t q4_word_codes(uint32_t w, uint32_t magic) {
-  const uint32_t w8 = w >> 8;
-  const half2_t y0 = sub1024((w & 0x000F000Fu) | magic);
-  const half2_t y1 = sub1024_hi((w & 0x00F000F0u) | magic);
-  const half2_t y2 = sub1024((w8 & 0x000F000Fu) | magic);
-  const half2_t y3 = sub1024_hi((w8 & 0x00F000F0u) | magic);
-  return half8_t{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
-}
-__host__ __device__ constexpr int q4_order(int j) { return (j & 1) ? 4 + (j >> 1) : (j >> 1); }
-
-// 8 channels of two q8 words (4 each) as exact fp16 codes, natural order.
-__device__ inline half8_t q8_words_codes(uint32_t w0, uint32_t w1) {
-  const uint32_t magic = 0x64646464u;  // byte 0x64: high byte of 1024.0
-  const half2_t y0 = sub1024(__builtin_amdgcn_perm(magic, w0, 0x04010400u));
-  const half2_t y1 = sub1024(__builtin_amdgcn_perm(magic, w0, 0x04030402u));
-  const half2_t y2 = sub1024(__builtin_amdgcn_perm(magic, w1, 0x04010400u));
-  const half2_t y3 = sub1024(__builtin_amdgcn_perm(magic, w1, 0x04030402u));
-  return half8_t{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
+// K operand of k-step s from the lane's K words (order qtile_k_channel).
+template <int BITS, int KW>
+__device__ inline half8_t k_codes(const uint32_t (&k)[KW], int s) {
+  uint32_t e[4];
+  if constexpr (BITS == 4) {
+    const uint32_t m = s < 2 ? 0x000F000Fu : 0x00F000F0u;
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t x = k[2 * (s & 1) + w];
+      e[2 * w] = x & m;
+      e[2 * w + 1] = (x >> 8) & m;
+    }
+  } else {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t x = k[2 * s + w];
+      e[2 * w] = __builtin_amdgcn_perm(x, x, 0x0C010C00u);
+      e[2 * w + 1] = __builtin_amdgcn_perm(x, x, 0x0C030C02u);
+    }
+  }
+  return __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
 }
 
 // Byte k of words a (low half) and b (high half), zero-extended to 16 bits.
@@ -121,27 +132,18 @@ __device__ inline uint32_t pair_bytes(uint32_t a, uint32_t b, int k) {
   return __builtin_amdgcn_perm(b, a, sel);
 }
 
-// V^T fragment: code i of the lane's word in rows r0..r3, as exact fp16.
+// V^T fragment: code i of the lane's word in rows r0..r3 as fp16 subnormals
+// (q4, odd i: the whole byte, u_lo + 16 u_hi).
 template <int BITS>
-__device__ inline half4_t v_codes(const uint32_t (&w)[4], int i, uint32_t magic) {
-  if constexpr (BITS == 4) {
-    const int k = i >> 1;
-    const uint32_t x01 = pair_bytes(w[0], w[1], k);
-    const uint32_t x23 = pair_bytes(w[2], w[3], k);
-    half2_t lo, hi;
-    if (i & 1) {
-      lo = sub1024_hi((x01 & 0x00F000F0u) | magic);
-      hi = sub1024_hi((x23 & 0x00F000F0u) | magic);
-    } else {
-      lo = sub1024((x01 & 0x000F000Fu) | magic);
-      hi = sub1024((x23 & 0x000F000Fu) | magic);
-    }
-    return half4_t{lo.x, lo.y, hi.x, hi.y};
-  } else {
-    const half2_t lo = sub1024(pair_bytes(w[0], w[1], i) | magic);
-    const half2_t hi = sub1024(pair_bytes(w[2], w[3], i) | magic);
-    return half4_t{lo.x, lo.y, hi.x, hi.y};
+__device__ inline half4_t v_codes(const uint32_t (&w)[4], int i) {
+  const int k = BITS == 4 ? i >> 1 : i;
+  uint32_t lo = pair_bytes(w[0], w[1], k);
+  uint32_t hi = pair_bytes(w[2], w[3], k);
+  if (BITS == 4 && !(i & 1)) {
+    lo &= 0x000F000Fu;
+    hi &= 0x000F000Fu;
   }
+  return __builtin_bit_cast(half4_t, make_uint2(lo, hi));
 }
 
 // Rotate within 16-lane DPP rows.
@@ -497,28 +499,34 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
   }
 
-  // Q^T (B of the K MFMA): lane (col, blk), k-step s covers channels
-  // 32*blk + 8*s + order[j]; nonzero only where the channel's group is the
-  // column's group.  qsum: sum of q_h over the column's group.
+  // Q^T (B of the K MFMA): lane (col, blk), element j of k-step s is channel
+  // 32*blk + qtile_k_channel(s, j); nonzero only where the channel's group is
+  // the column's group.  qsum: sum of q_h over the column's group, times
+  // 2^-24 (the unit of the code sums it is added to).
   half8_t qb[NB][4];
   float qsum[NB];
 #pragma unroll
   for (int bb = 0; bb < NB; ++bb) {
     const bool mine = used[bb] && (32 * blk) / GS == grp;
+    half8_t raw[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) raw[s] = __builtin_bit_cast(half8_t, qraw[bb][s]);
     qsum[bb] = 0.f;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const half8_t raw = __builtin_bit_cast(half8_t, qraw[bb][s]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const _Float16 v = mine ? raw[BITS == 4 ? q4_order(j) : j] : (_Float16)0.f;
+        const int c = qtile_k_channel<BITS>(s, j);
+        const _Float16 v = mine ? raw[c / 8][c % 8] : (_Float16)0.f;
         qb[bb][s][j] = v;
         qsum[bb] += (float)v;
       }
     }
     qsum[bb] += __shfl_xor(qsum[bb], 16);
     qsum[bb] += __shfl_xor(qsum[bb], 32);
+    qsum[bb] *= kCodeUnit;
   }
+  const float qscale = a.qscale * kCodeScale;  // scores are sums in units of 2^-24
 
   floatx4 acc1[NB][8], acc2[NB][8], accl[NB];
   float beta1[NB], beta2[NB];  // sum_r p * b_V over this lane's rows
@@ -535,7 +543,6 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     m_run[bb] = kNegSentinel;
   }
   const half4_t ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
-  const uint32_t magic = magic_vgpr();
 
   // Scores, online softmax and both V products of this wave's loaded tiles
   // k0 .. k0 + U - 1.
@@ -554,33 +561,46 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
         for (int t = 0; t < NS; ++t) drop_rows_past(sw[t], (unsigned)row0, (unsigned)max_lim);
       }
-      floatx4 sacc[NB];
+      // Code sums in units of 2^-24: q4 in two chains (low nibbles, high
+      // nibbles at 16x), q8 in one.
+      floatx4 sacc[NB], shi[NB];
 #pragma unroll
-      for (int bb = 0; bb < NB; ++bb) sacc[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int bb = 0; bb < NB; ++bb) {
+        sacc[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        shi[bb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        half8_t ka;
-        if constexpr (BITS == 4) {
-          ka = q4_word_codes(T[u].k[s], magic);
-        } else {
-          ka = q8_words_codes(T[u].k[2 * s], T[u].k[2 * s + 1]);
+        const half8_t ka = k_codes<BITS>(T[u].k, s);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          if (BITS == 4 && s >= 2)
+            shi[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[bb][s], shi[bb], 0, 0, 0);
+          else
+            sacc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[bb][s], sacc[bb], 0, 0, 0);
         }
+      }
+      if constexpr (BITS == 4) {
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb)
-          sacc[bb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[bb][s], sacc[bb], 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sacc[bb][r] = fmaf(shi[bb][r], 0.0625f, sacc[bb][r]);
       }
       uint32_t skw[2] = {sw[0][0], sw[0][1]}, bkw[2] = {sw[1][0], sw[1][1]};
       if constexpr (DUAL) {  // the noise head's column: k2 codes and scales
         floatx4 s2 = floatx4{0.f, 0.f, 0.f, 0.f};
+        floatx4 s2hi = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
-          half8_t ka;
-          if constexpr (BITS == 4) {
-            ka = q4_word_codes(T[u].k2[s], magic);
-          } else {
-            ka = q8_words_codes(T[u].k2[2 * s], T[u].k2[2 * s + 1]);
-          }
-          s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[0][s], s2, 0, 0, 0);
+          const half8_t ka = k_codes<BITS>(T[u].k2, s);
+          if (BITS == 4 && s >= 2)
+            s2hi = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[0][s], s2hi, 0, 0, 0);
+          else
+            s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[0][s], s2, 0, 0, 0);
+        }
+        if constexpr (BITS == 4) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s2[r] = fmaf(s2hi[r], 0.0625f, s2[r]);
         }
         const bool noise = h >= a.G;
 #pragma unroll
@@ -608,7 +628,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           t = sum_group_columns<GC>(t);
           const int row = row0 + r;
           const bool ok = row < lim[bb];  // lim <= max_lim
-          sc[r] = ok ? t * a.qscale : kNegSentinel;
+          sc[r] = ok ? t * qscale : kNegSentinel;
           mx = vmax(mx, sc[r]);
         }
         mx = vmax(mx, __shfl_xor(mx, 16));
@@ -652,8 +672,8 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           x1[r] = T[u].v1[r][BITS == 4 ? 0 : (i >> 2)];
           x2[r] = T[u].v2[r][BITS == 4 ? 0 : (i >> 2)];
         }
-        const half4_t a1 = v_codes<BITS>(x1, BITS == 4 ? i : (i & 3), magic);
-        const half4_t a2 = v_codes<BITS>(x2, BITS == 4 ? i : (i & 3), magic);
+        const half4_t a1 = v_codes<BITS>(x1, BITS == 4 ? i : (i & 3));
+        const half4_t a2 = v_codes<BITS>(x2, BITS == 4 ? i : (i & 3));
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
           acc1[bb][i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, w1[bb], acc1[bb][i], 0, 0, 0);
@@ -702,19 +722,24 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     if (used[bb] && (32 * blk) / GS == grp) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        // Code sums to values: 2^24, or for a q4 high nibble (odd channel)
+        // (whole-byte sum - low-nibble sum) * 2^20.
+        float o1[8], o2[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const bool odd4 = BITS == 4 && (i & 1);
+          const float f = odd4 ? 0x1p20f : kCodeScale;
+          o1[i] = fmaf(odd4 ? acc1[bb][i][r] - acc1[bb][i & ~1][r] : acc1[bb][i][r], f, be1);
+          o2[i] = fmaf(odd4 ? acc2[bb][i][r] - acc2[bb][i & ~1][r] : acc2[bb][i][r], f, be2);
+        }
         const int ch = 8 * (4 * blk + r);
-        *reinterpret_cast<float4*>(&lds_o[wave][hh][ch]) =
-            make_float4(acc1[bb][0][r] + be1, acc1[bb][1][r] + be1, acc1[bb][2][r] + be1,
-                        acc1[bb][3][r] + be1);
+        *reinterpret_cast<float4*>(&lds_o[wave][hh][ch]) = make_float4(o1[0], o1[1], o1[2], o1[3]);
         *reinterpret_cast<float4*>(&lds_o[wave][hh][ch + 4]) =
-            make_float4(acc1[bb][4][r] + be1, acc1[bb][5][r] + be1, acc1[bb][6][r] + be1,
-                        acc1[bb][7][r] + be1);
+            make_float4(o1[4], o1[5], o1[6], o1[7]);
         *reinterpret_cast<float4*>(&lds_o[wave][hh][D + ch]) =
-            make_float4(acc2[bb][0][r] + be2, acc2[bb][1][r] + be2, acc2[bb][2][r] + be2,
-                        acc2[bb][3][r] + be2);
+            make_float4(o2[0], o2[1], o2[2], o2[3]);
         *reinterpret_cast<float4*>(&lds_o[wave][hh][D + ch + 4]) =
-            make_float4(acc2[bb][4][r] + be2, acc2[bb][5][r] + be2, acc2[bb][6][r] + be2,
-                        acc2[bb][7][r] + be2);
+            make_float4(o2[4], o2[5], o2[6], o2[7]);
       }
     }
     if (col < GC && hh < nvh && blk == 0) {

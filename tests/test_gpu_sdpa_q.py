@@ -258,8 +258,8 @@ def test_full_size_16k_valu(gpu, rng, valu_only, bits):
     assert err <= 2e-3, f"bits={bits}: {err:.3e}"
 
 
-# Paired-tile kernel (group sizes 64 and 128; qpair 2 runs it for 8-bit
-# caches too) against the per-tile kernel on the same inputs: both inside the oracle bar and within
+# Paired-tile kernel (group sizes 64 and 128; qpair 2 runs it for fp16
+# activations) against the per-tile kernel on the same inputs: both inside the oracle bar and within
 # 2e-3 of each other.  Lengths cover the first row, both sides of 16- and
 # 32-row boundaries, partial pairs and the 16k workload; poisoned padding.
 @pytest.mark.parametrize("Hq,Hkv,cap,kv_len", [
