@@ -71,6 +71,41 @@ struct MfmaOp<bf16_t> {
 // the matrix cores take as fp16 or bf16: 2^8 leaves p a wide margin.
 constexpr float kRescaleSlackF16 = 8.f;
 
+// Lane l receives its own value and lane l ^ 16's (in row order: rows 0/1
+// hold (row 0, row 1) of the pair, rows 2/3 (row 2, row 3)); likewise l ^ 32
+// for the 32-lane swap.  Issued as asm: at -O3 the compiler folds the second
+// result of __builtin_amdgcn_permlane16_swap into the first, which breaks a
+// swap of one value against itself.  The s_nops cover the VALU-write ->
+// permlane-read and permlane-write -> VALU-read hazards.
+__device__ inline void swap16(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ inline void swap32(float x, float& a, float& b) {
+  a = x;
+  b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// Max over the four 16-lane rows (lanes l, l^16, l^32, l^48): every lane
+// receives the same value.
+__device__ inline float rows4_max(float x) {
+  float a, b;
+  swap16(x, a, b);
+  swap32(vmax(a, b), a, b);
+  return vmax(a, b);
+}
+// Sum over the four 16-lane rows; every lane receives the same bits (the
+// operands of each add are the same pair, in the same order, on both
+// partners).
+__device__ inline float rows4_sum(float x) {
+  float a, b;
+  swap16(x, a, b);
+  swap32(a + b, a, b);
+  return a + b;
+}
+
 // Causal row limit of query row s (see sdpa_dual_v_kernel).
 __device__ inline int row_limit(const SdpaArgs& a, int s) {
   int L = a.causal ? a.kv_len - a.S_q + s + 1 : a.kv_len;
@@ -203,7 +238,9 @@ sdpa_mfma_kernel(SdpaArgs a) {
   const long qrow0 = DUAL ? ((long)b * a.Hkv + kvh) * (a.G + a.G2)
                           : ((long)b * a.Hq + (long)kvh * a.G) * a.S_q + vh0;
 
-  const int max_lim = vhead_limit_max(a, vh0, nvh);
+  // Rows below min_lim are visible to every column of the workgroup.
+  int min_lim, max_lim;
+  vhead_limit_range(a, vh0, nvh, min_lim, max_lim);
   const bool col_ok = col < nvh;
   const int lim = col_ok ? vhead_limit(a, vh0 + col) : 0;  // <= max_lim
 
@@ -363,21 +400,32 @@ sdpa_mfma_kernel(SdpaArgs a) {
         }
       }
 
-      // Scores of rows t_v + 4*blk + r for head col, log2 units.
+      // Scores of rows t_v + 4*blk + r for head col, log2 units.  Rows at or
+      // past the column's limit score -inf, so their weight exp2(-inf - m)
+      // is 0 with no select (m_run starts at the finite sentinel and only
+      // grows); only a pair reaching min_lim holds such rows (a wave-uniform
+      // test).
       float sc[8];
-      float mx = kNegSentinel;
 #pragma unroll
       for (int v = 0; v < 2; ++v) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = tile_row(k0 + u + v) + 4 * blk + r;
-          const bool ok = row < lim;
-          sc[4 * v + r] = ok ? sacc[v][r] * a.qscale : kNegSentinel;
-          mx = vmax(mx, sc[4 * v + r]);
+        for (int r = 0; r < 4; ++r) sc[4 * v + r] = sacc[v][r] * a.qscale;
+      }
+      if (tile_row(k0 + u + 1) + 16 > min_lim) {
+        asm volatile("");  // keep this a branch: only pairs at a limit take it
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = tile_row(k0 + u + v) + 4 * blk + r;
+            sc[4 * v + r] = row < lim ? sc[4 * v + r] : -__builtin_inff();
+          }
         }
       }
-      mx = vmax(mx, __shfl_xor(mx, 16));
-      mx = vmax(mx, __shfl_xor(mx, 32));
+      float mx = kNegSentinel;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = vmax(mx, sc[j]);
+      mx = rows4_max(mx);
       if (__ballot(mx > m_run + kRescaleSlackF16) != 0) {
         const float m_new = fmaxf(m_run, mx);
         const float fac = fast_exp2(m_run - m_new);
@@ -392,7 +440,7 @@ sdpa_mfma_kernel(SdpaArgs a) {
       V8 pb;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        pb[j] = Op::from_f32(sc[j] > kNegSentinel ? fast_exp2(sc[j] - m_run) : 0.f);
+        pb[j] = Op::from_f32(fast_exp2(sc[j] - m_run));
 
 #pragma unroll
       for (int t = 0; t < VT; ++t) {

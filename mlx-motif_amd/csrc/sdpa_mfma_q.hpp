@@ -45,42 +45,6 @@ namespace motif {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-// Lane l receives its own value and lane l ^ 16's (in row order: rows 0/1
-// hold (row 0, row 1) of the pair, rows 2/3 (row 2, row 3)); likewise l ^ 32
-// for the 32-lane swap.  Issued as asm: at -O3 the compiler folds the second
-// result of __builtin_amdgcn_permlane16_swap into the first, which breaks a
-// swap of one value against itself.  The s_nops cover the VALU-write ->
-// permlane-read and permlane-write -> VALU-read hazards.
-__device__ inline void swap16(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-__device__ inline void swap32(float x, float& a, float& b) {
-  a = x;
-  b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-}
-
-// Max over the four 16-lane rows (lanes l, l^16, l^32, l^48): every lane
-// receives the same value.
-__device__ inline float rows4_max(float x) {
-  float a, b;
-  swap16(x, a, b);
-  swap32(vmax(a, b), a, b);
-  return vmax(a, b);
-}
-// Sum over the four 16-lane rows; every lane receives the same bits (the
-// operands of each add are the same pair, in the same order, on both
-// partners).
-__device__ inline float rows4_sum(float x) {
-  float a, b;
-  swap16(x, a, b);
-  swap32(a + b, a, b);
-  return a + b;
-}
-
-
 __device__ inline half2_t as_h2(uint32_t x) { return __builtin_bit_cast(half2_t, x); }
 __device__ inline uint32_t h2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
@@ -351,7 +315,9 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   const int gsel = grp < NG ? grp : 0;  // group whose scales this lane reads
   // v_perm selector keeping half (gsel & 1) of two words: low word = row r.
   const uint32_t sel = (gsel & 1) ? 0x07060302u : 0x05040100u;
-  const int max_lim = vhead_limit_max(a, vh0, nvh);
+  // Rows below min_lim are visible to every column of the workgroup.
+  int min_lim, max_lim;
+  vhead_limit_range(a, vh0, nvh, min_lim, max_lim);
   // Rows are dealt to the splits in blocks of NW 16-row tiles, round robin,
   // as in sdpa_mfma_kernel: tile k of wave w in split s is tile
   // (k * nsplit + s) * NW + w of the KV head.  The resources cover rows
@@ -619,20 +585,26 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
 #pragma unroll
       for (int bb = 0; bb < NB; ++bb) {
         float sc[4];
-        float mx = kNegSentinel;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // Unused columns have Q^T = 0 and qsum = 0, so t = 0 there without
           // a select (their scale words are finite cache values or 0).
-          float t = fmaf(skr[r], sacc[bb][r], bkr[r] * qsum[bb]);
-          t = sum_group_columns<GC>(t);
-          const int row = row0 + r;
-          const bool ok = row < lim[bb];  // lim <= max_lim
-          sc[r] = ok ? t * qscale : kNegSentinel;
-          mx = vmax(mx, sc[r]);
+          const float t = fmaf(skr[r], sacc[bb][r], bkr[r] * qsum[bb]);
+          sc[r] = sum_group_columns<GC>(t) * qscale;
         }
-        mx = vmax(mx, __shfl_xor(mx, 16));
-        mx = vmax(mx, __shfl_xor(mx, 32));
+        // Rows at or past the column's limit score -inf, so their weight
+        // exp2(-inf - m) is 0 with no select (m_run starts at the finite
+        // sentinel and only grows); only a tile reaching min_lim holds such
+        // rows (a wave-uniform test).
+        if (tr + 16 > min_lim) {
+          asm volatile("");  // keep this a branch: only tiles at a limit take it
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[r] = row0 + r < lim[bb] ? sc[r] : -__builtin_inff();
+        }
+        float mx = kNegSentinel;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = vmax(mx, sc[r]);
+        mx = rows4_max(mx);
         if (__ballot(mx > m_run[bb] + kSlack) != 0) {
           const float m_new = fmaxf(m_run[bb], mx);
           const float fac = fast_exp2(m_run[bb] - m_new);
@@ -649,7 +621,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         float p[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          p[r] = sc[r] > kNegSentinel ? fast_exp2(sc[r] - m_run[bb]) : 0.f;
+          p[r] = fast_exp2(sc[r] - m_run[bb]);
         // p rounded to fp16 once; the V weights, the bias terms and l all
         // use these same values.
         const half2_t p01 = half2_t{(_Float16)p[0], (_Float16)p[1]};
