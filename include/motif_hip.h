@@ -502,9 +502,9 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * "fused_merge" (0, the default: a second launch combines the splits; 1: the
  * last workgroup to finish combines them inside the attention launch),
  * "qpair" (packed caches at head_dim 128, group size 64/128: 1, the
- * default, runs bf16 activations on the paired-tile kernel and fp16 ones
- * on the per-tile kernel; 2 runs fp16 activations on the paired-tile
- * kernel too; 0 neither: bf16 activations take the VALU kernel), "qslab" (packed-cache
+ * default, runs bf16 activations over 4-bit caches on the paired-tile
+ * kernel and every other call on the per-tile kernel; 2 runs every such
+ * call on the paired-tile kernel; 0 none), "qslab" (packed-cache
  * verify slabs of 17..64 virtual heads per KV head: 2, the default, runs 8-
  * and 4-bit slabs on the kernel that dequantises each tile once into LDS;
  * 1 only 8-bit slabs; 0 neither), "waves_per_wg" 4 also selects that

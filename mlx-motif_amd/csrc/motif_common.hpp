@@ -38,7 +38,7 @@ struct Tuning {
   int mfma = 1;            // 1 = matrix-core kernels where compiled, 0 = VALU kernels
   int fused_merge = 0;     // 1 = last-arriving workgroup merges splits, 0 = merge kernel
   int poly_rows = 0;       // persistent PolyNorm workgroups per CU (0 = by register use)
-  int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 bf16 activations, 2 also fp16
+  int qpair = 1;           // paired-tile packed-cache kernel (group size 64/128): 0 off, 1 bf16 q4, 2 every call
   int qslab = 2;           // slabs of 17..64 virtual heads, tiles dequantised into LDS: 0 off, 1 q8, 2 q4+q8
   int qslab_ws = 1;        // slab kernel with producer / consumer waves (8 waves): 1 on, 0 off
   int merge_rows = 1;      // row-per-wave merge launch from 2048 partial rows: 1 on, 0 off

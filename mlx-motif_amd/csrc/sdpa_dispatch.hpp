@@ -26,10 +26,12 @@ int dispatch_sdpa_q_f32(const SdpaArgs& a, const SdpaPlan& p, int D, int bits, h
 int launch_sdpa_qpair(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
                       hipStream_t s, bool bf16 = false);
 
-// The paired-tile kernel takes this bf16 call: head_dim 128, group size 64
-// or 128, the pointer alignment and row bounds of the matrix-core kernels,
-// and a scale its tile softmax handles.
-bool qpair_bf16_ok(const SdpaArgs& a, int D, int gs);
+// A bf16 call the matrix-core kernels take: head_dim 128, the pointer
+// alignment and row bounds of those kernels.
+bool mfma_q_bf16_ok(const SdpaArgs& a, int D, int gs);
+// ... on the paired-tile kernel: group size 64 or 128, a scale its tile
+// softmax handles, and qpair 1 (4-bit caches; the default) or 2 (both).
+bool qpair_bf16_ok(const SdpaArgs& a, int D, int gs, int bits);
 
 // Packed cache (fp16 scales, head dim 128), a verify slab of 17..64 virtual
 // heads per KV head: tiles dequantised once per workgroup into LDS

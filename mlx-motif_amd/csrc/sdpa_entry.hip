@@ -67,16 +67,20 @@ static int check_partials(const char* name, const SdpaArgs& a, bool always) {
   return MOTIF_ERR_INTERNAL;
 }
 
-bool qpair_bf16_ok(const SdpaArgs& a, int D, int gs) {
-  if (D != kSdpaMfmaQD || (gs != 64 && gs != 128) || !tuning().mfma || tuning().qpair < 1)
-    return false;
+bool mfma_q_bf16_ok(const SdpaArgs& a, int D, int gs) {
+  if (D != kSdpaMfmaQD || (gs != 32 && gs != 64 && gs != 128) || !tuning().mfma) return false;
   const int ng = D / gs;
   const uintptr_t scale_bits = (uintptr_t)a.ks | (uintptr_t)a.kb | (uintptr_t)a.v1s |
                                (uintptr_t)a.v1b | (uintptr_t)a.v2s | (uintptr_t)a.v2b;
   const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;
   return ((data_bits | (uintptr_t)a.q) & 15u) == 0 &&
          (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && a.kv_cap % 4 == 0 &&
-         a.kv_len <= kMfmaMaxRows && tile_softmax_scale_ok(a.qscale);
+         a.kv_len <= kMfmaMaxRows;
+}
+
+bool qpair_bf16_ok(const SdpaArgs& a, int D, int gs, int bits) {
+  return tuning().qpair >= (bits == 4 ? 1 : 2) && (gs == 64 || gs == 128) &&
+         mfma_q_bf16_ok(a, D, gs) && tile_softmax_scale_ok(a.qscale);
 }
 
 // Shared shape checks (the reference asserts of attention.py:237-243, 556-564)
@@ -228,8 +232,9 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   // fill 2-3 blocks of columns (a verify slab), one workgroup carries all of
   // them (NB column blocks), provided the pointers suit that kernel; its plan
   // has one head chunk of NB blocks.
-  // bf16 activations (q4 / q8, group size 64 or 128): the paired-tile
-  // matrix-core kernel with its plan (4-wave workgroups, one per CU).
+  // bf16 activations (q4 / q8): the per-tile or the paired-tile matrix-core
+  // kernel and the same plan (4-wave workgroups, one per CU), in one column
+  // block.
   SdpaArgs probe{};
   probe.q = q;
   probe.kd = kd; probe.ks = ks; probe.kb = kb;
@@ -238,10 +243,10 @@ static int sdpa_q_run(const char* name, const void* q, const uint32_t* kd, const
   probe.kv_cap = kv_cap;
   probe.kv_len = kv_len;
   probe.qscale = scale * 1.4426950408889634f;
-  const bool pair_bf16 = dtype == MOTIF_BF16 && qpair_bf16_ok(probe, D, gs);
-  const bool mfma_q = D == kSdpaMfmaQD && tuning().mfma && (dtype == MOTIF_F16 || pair_bf16);
+  const bool q_bf16 = dtype == MOTIF_BF16 && mfma_q_bf16_ok(probe, D, gs);
+  const bool mfma_q = D == kSdpaMfmaQD && tuning().mfma && (dtype == MOTIF_F16 || q_bf16);
   int nb = 1;
-  if (mfma_q && !pair_bf16 && Hkv >= 1 && Hq % Hkv == 0) {
+  if (mfma_q && dtype == MOTIF_F16 && Hkv >= 1 && Hq % Hkv == 0) {
     const int ng = D / gs;
     const uintptr_t scale_bits = (uintptr_t)ks | (uintptr_t)kb | (uintptr_t)v1s |
                                  (uintptr_t)v1b | (uintptr_t)v2s | (uintptr_t)v2b;

@@ -66,22 +66,26 @@ int MOTIF_CAT(dispatch_sdpa_q_, MOTIF_SUFFIX)(const SdpaArgs& a, const SdpaPlan&
     const uintptr_t scale_bits = (uintptr_t)a.ks | (uintptr_t)a.kb | (uintptr_t)a.v1s |
                                  (uintptr_t)a.v1b | (uintptr_t)a.v2s | (uintptr_t)a.v2b;
     const uintptr_t data_bits = (uintptr_t)a.kd | (uintptr_t)a.v1d | (uintptr_t)a.v2d;
-    const bool aligned = (data_bits & 15u) == 0 && (scale_bits & (ng == 1 ? 7u : 15u)) == 0 &&
-                         a.kv_cap % 4 == 0 && a.kv_len <= kMfmaMaxRows;
+    const bool aligned = ((data_bits | (uintptr_t)a.q) & 15u) == 0 &&
+                         (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && a.kv_cap % 4 == 0 &&
+                         a.kv_len <= kMfmaMaxRows;
     if (D == 128 && tuning().mfma && aligned && p.gc * ng <= 16) {
       // Paired-tile kernel with qpair 2 only: for fp16 activations the
       // per-tile kernel is faster at both code widths.
-      if (tuning().qpair >= 2 && ng <= 2 && ((uintptr_t)a.q & 15u) == 0 &&
-          tile_softmax_scale_ok(a.qscale))
+      if (tuning().qpair >= 2 && ng <= 2 && tile_softmax_scale_ok(a.qscale))
         return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
       return launch_sdpa_mfma_q(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
     }
   }
   if constexpr (std::is_same<MOTIF_ELEM, bf16_t>::value) {
-    // bf16 activations: the paired-tile kernel for 4- and 8-bit caches
-    // (sdpa_q_run planned it: 4-wave workgroups, one per CU).
-    if (qpair_bf16_ok(a, D, a.group_size) && p.gc * (D / a.group_size) <= 16)
-      return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s, true);
+    // bf16 activations on the matrix cores (sdpa_q_run planned it: 4-wave
+    // workgroups, one per CU): 4-bit caches at group size 64/128 on the
+    // paired-tile kernel (faster there), the others on the per-tile kernel.
+    if (mfma_q_bf16_ok(a, D, a.group_size) && p.gc * (D / a.group_size) <= 16) {
+      if (qpair_bf16_ok(a, D, a.group_size, bits))
+        return launch_sdpa_qpair(a, bits, a.group_size, p.gc, p.waves, nblocks, s, true);
+      return launch_sdpa_mfma_q<bf16_t>(a, bits, a.group_size, p.gc, p.waves, nblocks, s);
+    }
   }
   if (bits == 4) {
     switch (D) {

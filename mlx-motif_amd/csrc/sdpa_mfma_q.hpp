@@ -48,6 +48,21 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 __device__ inline half2_t as_h2(uint32_t x) { return __builtin_bit_cast(half2_t, x); }
 __device__ inline uint32_t h2_bits(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
+// Low / high 16-bit element of a packed pair as fp32 (fp16 or bf16).
+template <typename T>
+__device__ inline float pair_lo_f32(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w << 16);
+  return (float)as_h2(w).x;
+}
+template <typename T>
+__device__ inline float pair_hi_f32(uint32_t w) {
+  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w & 0xFFFF0000u);
+  return (float)as_h2(w).y;
+}
+// Two floats as an fp16 pair (round to nearest even).
+__device__ inline uint32_t f16_pair(float lo, float hi) {
+  return h2_bits(half2_t{(_Float16)lo, (_Float16)hi});
+}
 // Value of code 1 as an fp16 subnormal, and its inverse.
 constexpr float kCodeUnit = 0x1p-24f;
 constexpr float kCodeScale = 0x1p24f;
@@ -263,9 +278,16 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
 // feed every block's MFMAs, so a verify slab (e.g. 5 rows x GQA 4 = 20
 // virtual heads) runs as one pass instead of one workgroup per 8 heads.
 // The accumulators of NB > 1 blocks live in AGPRs at one wave per SIMD.
+// E: element type of q, the scales and biases and y (fp16 or bf16).  bf16
+// heads are scaled by a power of two and rounded to fp16 once (below); the
+// products stay fp16 MFMAs over the codes, and the K scales and the bias
+// terms are taken in fp32.  Those fp32 operands need more registers than two
+// waves per SIMD leave, so bf16 variants run one wave per SIMD (4-wave
+// workgroups, the planner's default).
 template <int BITS, int GS, int GC, int NW, int U, int POL = kCachePolicyStream,
-          bool DUAL = false, int NB = 1>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NB > 1 ? 1 : 2)))
+          bool DUAL = false, int NB = 1, typename E = half_t>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(NB > 1 || std::is_same<E, bf16_t>::value ? 1 : 2)))
 sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int D = 128;
   constexpr int NG = D / GS;  // scale groups per row
@@ -277,6 +299,8 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   constexpr int VW = Tile::VW;
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
   static_assert(!DUAL || NB == 1, "the fused decode step uses one column block");
+  constexpr bool kBf16 = std::is_same<E, bf16_t>::value;
+  static_assert(!(DUAL && kBf16), "the fused packed decode step takes fp16 activations");
   // Lazy-rescale slack (see kRescaleSlackF16): here p also multiplies the V
   // scale in fp16, so p * s must stay finite.  An fp16 cache row spans at
   // most 2 * 65504, so s <= 131008 / 15 (q4) or / 255 (q8), and 2^slack * s
@@ -465,6 +489,37 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
   }
 
+  // bf16 activations: each head's q is scaled by 2^-e, e the smallest >= 0
+  // that brings the head's largest |q| below 2^15 (the four lanes of a
+  // column hold the head's 128 channels), and rounded to fp16; 2^e goes
+  // into that head's softmax scale.
+  int q_exp[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    q_exp[bb] = 0;
+    if constexpr (kBf16) {
+      uint32_t w[16];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        w[4 * s] = qraw[bb][s].x; w[4 * s + 1] = qraw[bb][s].y;
+        w[4 * s + 2] = qraw[bb][s].z; w[4 * s + 3] = qraw[bb][s].w;
+      }
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        mx = fmaxf(mx, fmaxf(fabsf(pair_lo_f32<E>(w[i])), fabsf(pair_hi_f32<E>(w[i]))));
+      mx = rows4_max(mx);
+      const int ex = (int)((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFFu) - 127;
+      q_exp[bb] = ex > 14 ? ex - 14 : 0;  // 0 for zero, subnormal and small heads
+      const float f = __builtin_bit_cast(float, (uint32_t)(127 - q_exp[bb]) << 23);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] = f16_pair(pair_lo_f32<E>(w[i]) * f, pair_hi_f32<E>(w[i]) * f);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        qraw[bb][s] = make_uint4(w[4 * s], w[4 * s + 1], w[4 * s + 2], w[4 * s + 3]);
+    }
+  }
+
   // Q^T (B of the K MFMA): lane (col, blk), element j of k-step s is channel
   // 32*blk + qtile_k_channel(s, j); nonzero only where the channel's group is
   // the column's group.  qsum: sum of q_h over the column's group, times
@@ -492,7 +547,11 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     qsum[bb] += __shfl_xor(qsum[bb], 32);
     qsum[bb] *= kCodeUnit;
   }
-  const float qscale = a.qscale * kCodeScale;  // scores are sums in units of 2^-24
+  // Scores are sums in units of 2^-24 (times 2^-q_exp for a scaled bf16 head).
+  float qsc[NB];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+    qsc[bb] = a.qscale * kCodeScale * __builtin_bit_cast(float, (uint32_t)(127 + q_exp[bb]) << 23);
 
   floatx4 acc1[NB][8], acc2[NB][8], accl[NB];
   float beta1[NB], beta2[NB];  // sum_r p * b_V over this lane's rows
@@ -577,10 +636,28 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           bkw[p] = noise ? sw[7][p] : bkw[p];
         }
       }
-      const half2_t sk01 = as_h2(skw[0]), sk23 = as_h2(skw[1]);
-      const half2_t bk01 = as_h2(bkw[0]), bk23 = as_h2(bkw[1]);
-      const float skr[4] = {(float)sk01.x, (float)sk01.y, (float)sk23.x, (float)sk23.y};
-      const float bkr[4] = {(float)bk01.x, (float)bk01.y, (float)bk23.x, (float)bk23.y};
+      float skr[4], bkr[4];
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          skr[2 * p] = pair_lo_f32<E>(skw[p]);
+          skr[2 * p + 1] = pair_hi_f32<E>(skw[p]);
+          bkr[2 * p] = pair_lo_f32<E>(bkw[p]);
+          bkr[2 * p + 1] = pair_hi_f32<E>(bkw[p]);
+        }
+        // V scales as fp16 pairs for the weight products (exact in fp16's
+        // normal range).
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          sw[2][p] = f16_pair(pair_lo_f32<E>(sw[2][p]), pair_hi_f32<E>(sw[2][p]));
+          sw[4][p] = f16_pair(pair_lo_f32<E>(sw[4][p]), pair_hi_f32<E>(sw[4][p]));
+        }
+      } else {
+        const half2_t sk01 = as_h2(skw[0]), sk23 = as_h2(skw[1]);
+        const half2_t bk01 = as_h2(bkw[0]), bk23 = as_h2(bkw[1]);
+        skr[0] = (float)sk01.x; skr[1] = (float)sk01.y; skr[2] = (float)sk23.x; skr[3] = (float)sk23.y;
+        bkr[0] = (float)bk01.x; bkr[1] = (float)bk01.y; bkr[2] = (float)bk23.x; bkr[3] = (float)bk23.y;
+      }
       half4_t w1[NB], w2[NB], pbb[NB];
 #pragma unroll
       for (int bb = 0; bb < NB; ++bb) {
@@ -590,7 +667,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
           // Unused columns have Q^T = 0 and qsum = 0, so t = 0 there without
           // a select (their scale words are finite cache values or 0).
           const float t = fmaf(skr[r], sacc[bb][r], bkr[r] * qsum[bb]);
-          sc[r] = sum_group_columns<GC>(t) * qscale;
+          sc[r] = sum_group_columns<GC>(t) * qsc[bb];
         }
         // Rows at or past the column's limit score -inf, so their weight
         // exp2(-inf - m) is 0 with no select (m_run starts at the finite
@@ -631,10 +708,20 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
         const half2_t w2a = p01 * as_h2(sw[4][0]), w2b = p23 * as_h2(sw[4][1]);
         w1[bb] = half4_t{w1a.x, w1a.y, w1b.x, w1b.y};
         w2[bb] = half4_t{w2a.x, w2a.y, w2b.x, w2b.y};
-        beta1[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[3][0]), beta1[bb], false);
-        beta1[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[3][1]), beta1[bb], false);
-        beta2[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[5][0]), beta2[bb], false);
-        beta2[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[5][1]), beta2[bb], false);
+        if constexpr (kBf16) {  // the bias terms in fp32, with the same fp16 weights
+          const float pf[4] = {(float)p01.x, (float)p01.y, (float)p23.x, (float)p23.y};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t b1 = sw[3][r / 2], b2 = sw[5][r / 2];
+            beta1[bb] = fmaf(pf[r], (r & 1) ? pair_hi_f32<E>(b1) : pair_lo_f32<E>(b1), beta1[bb]);
+            beta2[bb] = fmaf(pf[r], (r & 1) ? pair_hi_f32<E>(b2) : pair_lo_f32<E>(b2), beta2[bb]);
+          }
+        } else {
+          beta1[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[3][0]), beta1[bb], false);
+          beta1[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[3][1]), beta1[bb], false);
+          beta2[bb] = __builtin_amdgcn_fdot2(p01, as_h2(sw[5][0]), beta2[bb], false);
+          beta2[bb] = __builtin_amdgcn_fdot2(p23, as_h2(sw[5][1]), beta2[bb], false);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -722,39 +809,58 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   __syncthreads();
   // The in-kernel merge's LDS does not fit beside NB > 1 blocks' staging:
   // those launches always use the merge launch.
-  wg_epilogue<half_t, D, GCW, NW, DUAL, NB == 1>(a, lds_o, lds_m, lds_l, qrow0, nvh, split,
+  wg_epilogue<E, D, GCW, NW, DUAL, NB == 1>(a, lds_o, lds_m, lds_l, qrow0, nvh, split,
                                                  unit);
 }
 
 // Packed cache, head_dim 128, fp16 scales: heads x groups <= 16 columns.
 // One tile per register set: with the prefetched set, two tiles' loads are
 // in flight per wave while one is computed.
-template <int BITS, int GS>
+template <int BITS, int GS, typename E = half_t>
 int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;
   constexpr int U = 1;
+  constexpr int P = kCachePolicyStream;
   constexpr int GCM = 16 / NG < 8 ? 16 / NG : 8;  // widest pass
-  if (a.nchunk > 1 && gc == GCM && waves == 4) {
-    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, GCM, 4, U, 0>), dim3(nblocks), dim3(256), 0,
-                       st, a);
+  // bf16 variants run one wave per SIMD: 4-wave workgroups only.
+  constexpr bool k8 = !std::is_same<E, bf16_t>::value;
+  if (a.nchunk > 1 && gc == GCM && (waves == 4 || !k8)) {
+    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, GCM, 4, U, 0, false, 1, E>), dim3(nblocks),
+                       dim3(256), 0, st, a);
     return check_launch("sdpa_dual_v_q (mfma, chunks)");
   }
+  const bool w8 = k8 && waves == 8;
   switch (gc) {
     case 1:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 8, U>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 4, U>), dim3(nblocks), dim3(256), 0, st, a);
+      if constexpr (k8) {
+        if (w8) {
+          hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 8, U, P, false, 1, E>), dim3(nblocks), dim3(512), 0, st, a);
+          break;
+        }
+      }
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 1, 4, U, P, false, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 2:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 8, U>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 4, U>), dim3(nblocks), dim3(256), 0, st, a);
+      if constexpr (k8) {
+        if (w8) {
+          hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 8, U, P, false, 1, E>), dim3(nblocks), dim3(512), 0, st, a);
+          break;
+        }
+      }
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 4, U, P, false, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 4:
-      if (waves == 8) hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 8, U>), dim3(nblocks), dim3(512), 0, st, a);
-      else hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 4, U>), dim3(nblocks), dim3(256), 0, st, a);
+      if constexpr (k8) {
+        if (w8) {
+          hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 8, U, P, false, 1, E>), dim3(nblocks), dim3(512), 0, st, a);
+          break;
+        }
+      }
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 4, U, P, false, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
       break;
     case 8:
       if constexpr (8 * NG <= 16) {
-        hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 8, 4, U>), dim3(nblocks), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 8, 4, U, P, false, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
         break;
       }
       [[fallthrough]];
@@ -830,16 +936,17 @@ inline int launch_sdpa_mfma_q_wide(const SdpaArgs& a, int bits, int gs, int nb, 
   return launch_sdpa_mfma_q_wide_gs<8, 128>(a, nb, nblocks, st);
 }
 
+template <typename E = half_t>
 inline int launch_sdpa_mfma_q(const SdpaArgs& a, int bits, int gs, int gc, int waves, int nblocks,
                               hipStream_t st) {
   if (bits == 4) {
-    if (gs == 32) return launch_sdpa_mfma_q_gs<4, 32>(a, gc, waves, nblocks, st);
-    if (gs == 64) return launch_sdpa_mfma_q_gs<4, 64>(a, gc, waves, nblocks, st);
-    return launch_sdpa_mfma_q_gs<4, 128>(a, gc, waves, nblocks, st);
+    if (gs == 32) return launch_sdpa_mfma_q_gs<4, 32, E>(a, gc, waves, nblocks, st);
+    if (gs == 64) return launch_sdpa_mfma_q_gs<4, 64, E>(a, gc, waves, nblocks, st);
+    return launch_sdpa_mfma_q_gs<4, 128, E>(a, gc, waves, nblocks, st);
   }
-  if (gs == 32) return launch_sdpa_mfma_q_gs<8, 32>(a, gc, waves, nblocks, st);
-  if (gs == 64) return launch_sdpa_mfma_q_gs<8, 64>(a, gc, waves, nblocks, st);
-  return launch_sdpa_mfma_q_gs<8, 128>(a, gc, waves, nblocks, st);
+  if (gs == 32) return launch_sdpa_mfma_q_gs<8, 32, E>(a, gc, waves, nblocks, st);
+  if (gs == 64) return launch_sdpa_mfma_q_gs<8, 64, E>(a, gc, waves, nblocks, st);
+  return launch_sdpa_mfma_q_gs<8, 128, E>(a, gc, waves, nblocks, st);
 }
 
 }  // namespace motif

@@ -99,21 +99,6 @@ struct QPair {
 // Packed cache, head_dim 128, fp16 scales; heads x groups <= 16 columns.
 // GC heads per workgroup (column n = NG*h + g), NW waves, POL cache policy
 // (cached when several head chunks read the same rows).
-template <typename T>
-__device__ inline float pair_lo_f32(uint32_t w) {
-  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w << 16);
-  return (float)as_h2(w).x;
-}
-template <typename T>
-__device__ inline float pair_hi_f32(uint32_t w) {
-  if constexpr (std::is_same<T, bf16_t>::value) return __builtin_bit_cast(float, w & 0xFFFF0000u);
-  return (float)as_h2(w).y;
-}
-// Two floats as an fp16 pair (round to nearest even).
-__device__ inline uint32_t f16_pair(float lo, float hi) {
-  return h2_bits(half2_t{(_Float16)lo, (_Float16)hi});
-}
-
 template <int BITS, int GS, int GC, int NW, int POL = kCachePolicyStream, typename E = half_t>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 sdpa_qpair_kernel(SdpaArgs a) {

@@ -287,38 +287,48 @@ def test_paired_kernel_agrees_with_per_tile(gpu, Hq, Hkv, cap, kv_len, gs, bits)
     assert np.max(np.abs(ys[0] - ys[1])) <= 2e-3
 
 
-# bf16 activations, scales and biases: the paired-tile kernel (fp16 matrix-
-# core products after an exact per-head power-of-two scaling of q) against
-# the VALU kernel on the same inputs, both within the bf16 bar of the oracle
-# and of each other.  Reference: the kernel tests of sdpa_dual_v_q4 run bf16
+# bf16 activations, scales and biases on the matrix cores (fp16 products after
+# an exact per-head power-of-two scaling of q): the per-tile kernel (qpair 0;
+# the default for 8-bit caches and group size 32), the paired-tile kernel
+# (qpair 2, group sizes 64/128; the default for 4-bit caches) and the VALU
+# kernel on the same inputs, all within the bf16 bar of the oracle and of each
+# other.  Reference: the kernel tests of sdpa_dual_v_q4 run bf16
 # (tests/test_kernels_sdpa_dual_v_q4.py:34).
+_BF16_MODES = {"tile": (("qpair", 0),), "pair": (("qpair", 2),), "valu": (("mfma", 0),)}
+
+
 @pytest.mark.parametrize("Hq,Hkv,cap,kv_len", [
     (32, 8, 64, 1), (32, 8, 64, 17), (32, 8, 128, 100), (8, 8, 1024, 1000),
     (64, 8, 4096, 3001), (16, 4, 512, 511), (40, 8, 1024, 1024), (32, 8, 16128, 16000),
 ])
-@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("gs", [32, 64, 128])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_bf16_paired_kernel_agrees_with_valu(gpu, Hq, Hkv, cap, kv_len, gs, bits):
+def test_bf16_matrix_core_kernels_agree_with_valu(gpu, Hq, Hkv, cap, kv_len, gs, bits):
     from mlx_motif import _native
 
+    modes = ["tile", "valu"] if gs == 32 else ["tile", "pair", "valu"]
     errs, ys = [], []
-    for mfma in (1, 0):
-        _native.set_tuning("mfma", mfma)
+    for mode in modes:
         try:
-            print(f"bf16 mfma={mfma} Hq={Hq} kv_len={kv_len} gs={gs} bits={bits}", flush=True)
+            for key, value in _BF16_MODES[mode]:
+                _native.set_tuning(key, value)
+            print(f"bf16 {mode} Hq={Hq} kv_len={kv_len} gs={gs} bits={bits}", flush=True)
             err, y, _ = _run(gpu, np.random.default_rng(13), 1, Hq, Hkv, cap, kv_len, 128, bits,
                              gs, "bf16", poison=True)
         finally:
+            _native.set_tuning("qpair", 1)
             _native.set_tuning("mfma", 1)
         assert np.isfinite(torch_to_np(y)).all()
         errs.append(err)
         ys.append(torch_to_np(y))
-    assert max(errs) <= TOL["bf16"], errs
-    assert np.max(np.abs(ys[0] - ys[1])) <= TOL["bf16"]
+    assert max(errs) <= TOL["bf16"], dict(zip(modes, errs))
+    for y in ys[1:]:
+        assert np.max(np.abs(ys[0] - y)) <= TOL["bf16"]
 
 
+@pytest.mark.parametrize("mode", ["tile", "pair"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_bf16_q_beyond_fp16_range(gpu, rng, bits):
+def test_bf16_q_beyond_fp16_range(gpu, rng, bits, mode):
     """bf16 queries far outside fp16's range (|q| up to ~1e6) and far below
     it (~1e-6): the per-head power-of-two scaling keeps the fp16 products
     finite and exact in the large heads, and the small heads' scores stay
@@ -335,9 +345,15 @@ def test_bf16_q_beyond_fp16_range(gpu, rng, bits):
     k, v1, v2 = (randn(rng, (B, Hkv, cap, D), "bf16") for _ in range(3))
     kq, v1q, v2q = (_quant(t, gs, bits, "bf16") for t in (k, v1, v2))
     scale = 1.0 / np.sqrt(D)
-    y = sdpa_dual_v_q4(np_to_torch(q, torch.bfloat16, gpu), _to_gpu(kq, "bf16", gpu),
-                       _to_gpu(v1q, "bf16", gpu), _to_gpu(v2q, "bf16", gpu), scale,
-                       group_size=gs, bits=bits, kv_len=kv_len)
+    from mlx_motif import _native
+
+    _native.set_tuning("qpair", 2 if mode == "pair" else 0)
+    try:
+        y = sdpa_dual_v_q4(np_to_torch(q, torch.bfloat16, gpu), _to_gpu(kq, "bf16", gpu),
+                           _to_gpu(v1q, "bf16", gpu), _to_gpu(v2q, "bf16", gpu), scale,
+                           group_size=gs, bits=bits, kv_len=kv_len)
+    finally:
+        _native.set_tuning("qpair", 1)
     ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, scale, gs, bits, kv_len)
     got = torch_to_np(y)
     assert np.isfinite(got).all()
