@@ -146,7 +146,7 @@ def make_fp16_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, hq=HQ, hkv=H
 
 
 def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True, gr=4,
-                      bits=None, append=None):
+                      bits=None, append=None, bf16=False):
     """One GDA decode-attention step per call over distinct layer caches
     (k1, k2, v1, v2 of HKV heads): motif_gda_decode / motif_gda_decode_q
     (fused) or the reference's three calls (two motif_sdpa_dual_v(_q) +
@@ -154,26 +154,28 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
     ``append``: also write the token's four rows at row kv_len - 1, inside
     the step ("fused": motif_gda_decode(_q)_append) or before it ("write":
     the cache write -- four row copies, or motif_quant_write4 -- then the
-    fused step)."""
+    fused step).  ``bf16``: bf16 activations, cache (or scales and biases)
+    and output."""
     from mlx_motif import _native
     from mlx_motif.kernels import quantize
 
+    dt, code = (torch.bfloat16, 1) if bf16 else (torch.float16, 0)
     g = torch.Generator(device=dev)
     g.manual_seed(99)
-    q1 = torch.randn((B, HKV * gr, 1, D), generator=g, device=dev).half()
-    q2 = torch.randn((B, HKV, 1, D), generator=g, device=dev).half()
-    w = torch.rand(2 * D, generator=g, device=dev).half()
+    q1 = torch.randn((B, HKV * gr, 1, D), generator=g, device=dev).to(dt)
+    q2 = torch.randn((B, HKV, 1, D), generator=g, device=dev).to(dt)
+    w = torch.rand(2 * D, generator=g, device=dev).to(dt)
     lam = torch.tensor([0.37], dtype=torch.float32, device=dev)
-    sets = [tuple(torch.randn((B, HKV, cap, D), generator=g, device=dev).half()
+    sets = [tuple(torch.randn((B, HKV, cap, D), generator=g, device=dev).to(dt)
                   for _ in range(4)) for _ in range(nsets)]
     if bits:
         sets = [tuple(quantize(t, GS, bits) for t in st) for st in sets]
         torch.cuda.synchronize()
-    rows = [torch.randn((B, HKV, 1, D), generator=g, device=dev).half() for _ in range(4)]
+    rows = [torch.randn((B, HKV, 1, D), generator=g, device=dev).to(dt) for _ in range(4)]
     rp = [r.data_ptr() for r in rows]
-    y = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
-    o = torch.empty((B, HKV * gr, 1, 2 * D), dtype=torch.float16, device=dev)
-    n = torch.empty((B, HKV, 1, 2 * D), dtype=torch.float16, device=dev)
+    y = torch.empty((B, HKV * gr, 1, 2 * D), dtype=dt, device=dev)
+    o = torch.empty((B, HKV * gr, 1, 2 * D), dtype=dt, device=dev)
+    n = torch.empty((B, HKV, 1, 2 * D), dtype=dt, device=dev)
     nbytes = max(lib.motif_gda_decode_workspace_bytes(B, HKV, gr, kv_len, D),
                  lib.motif_sdpa_workspace_bytes(B, HKV * gr, HKV, 1, kv_len, D))
     ws = torch.zeros(max(nbytes, 16 << 20), dtype=torch.uint8, device=dev)
@@ -189,27 +191,27 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
 
         def call():
             st = torch.cuda.current_stream().cuda_stream
-            tail = (w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B, HKV, gr, D, cap,
-                    kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st)
+            tail = (w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), code, B, HKV, gr, D,
+                    cap, kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st)
             if append == "fused":
                 _native.check(lib.motif_gda_decode_q_append(
                     q1.data_ptr(), q2.data_ptr(), *rp, *p(k1), *p(k2), *p(v1), *p(v2), *tail))
                 return
             if append == "write":
-                _native.check(lib.motif_quant_write4(*rp, data, scl, bia, 0, B, HKV, 1, D, cap,
+                _native.check(lib.motif_quant_write4(*rp, data, scl, bia, code, B, HKV, 1, D, cap,
                                                      kv_len - 1, bits, GS, st))
             if fused:
                 _native.check(lib.motif_gda_decode_q(
                     q1.data_ptr(), q2.data_ptr(), *p(k1), *p(k2), *p(v1), *p(v2), *tail))
                 return
             _native.check(lib.motif_sdpa_dual_v_q(
-                q1.data_ptr(), *p(k1), *p(v1), *p(v2), o.data_ptr(), 0, B, HKV * gr, HKV, D, cap,
-                kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
+                q1.data_ptr(), *p(k1), *p(v1), *p(v2), o.data_ptr(), code, B, HKV * gr, HKV, D,
+                cap, kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
             _native.check(lib.motif_sdpa_dual_v_q(
-                q2.data_ptr(), *p(k2), *p(v1), *p(v2), n.data_ptr(), 0, B, HKV, HKV, D, cap,
-                kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
+                q2.data_ptr(), *p(k2), *p(v1), *p(v2), n.data_ptr(), code, B, HKV, HKV, D,
+                cap, kv_len, bits, GS, scale, ws.data_ptr(), ws.numel(), st))
             _native.check(lib.motif_gda_post_split(
-                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), 0, B, HKV * gr, HKV, gr,
+                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), code, B, HKV * gr, HKV, gr,
                 1, 2 * D, lam.data_ptr(), 0.8, 1e-5, st))
         return call
 
@@ -220,7 +222,7 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
                 _native.check(lib.motif_gda_decode_append(
                     q1.data_ptr(), q2.data_ptr(), *rp, k1.data_ptr(), k2.data_ptr(),
                     v1.data_ptr(), v2.data_ptr(), w.data_ptr(), lam.data_ptr(), 0.8, 1e-5,
-                    y.data_ptr(), 0, B, HKV, gr, D, cap, kv_len, scale, ws.data_ptr(),
+                    y.data_ptr(), code, B, HKV, gr, D, cap, kv_len, scale, ws.data_ptr(),
                     ws.numel(), st))
                 return
             if append == "write":  # the fp cache's write: a slice copy per slot
@@ -229,17 +231,17 @@ def make_decode_calls(torch, lib, dev, nsets, kv_len=KV_LEN, cap=CAP, fused=True
             if fused:
                 _native.check(lib.motif_gda_decode(
                     q1.data_ptr(), q2.data_ptr(), k1.data_ptr(), k2.data_ptr(), v1.data_ptr(),
-                    v2.data_ptr(), w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), 0, B,
+                    v2.data_ptr(), w.data_ptr(), lam.data_ptr(), 0.8, 1e-5, y.data_ptr(), code, B,
                     HKV, gr, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
                 return
             _native.check(lib.motif_sdpa_dual_v(
-                q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), v2.data_ptr(), o.data_ptr(), 0, B,
+                q1.data_ptr(), k1.data_ptr(), v1.data_ptr(), v2.data_ptr(), o.data_ptr(), code, B,
                 HKV * gr, HKV, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
             _native.check(lib.motif_sdpa_dual_v(
-                q2.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr(), n.data_ptr(), 0, B,
+                q2.data_ptr(), k2.data_ptr(), v1.data_ptr(), v2.data_ptr(), n.data_ptr(), code, B,
                 HKV, HKV, D, cap, kv_len, scale, ws.data_ptr(), ws.numel(), st))
             _native.check(lib.motif_gda_post_split(
-                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), 0, B, HKV * gr, HKV, gr,
+                o.data_ptr(), n.data_ptr(), w.data_ptr(), y.data_ptr(), code, B, HKV * gr, HKV, gr,
                 1, 2 * D, lam.data_ptr(), 0.8, 1e-5, st))
         return call
 

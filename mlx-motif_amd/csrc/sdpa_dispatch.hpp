@@ -46,8 +46,8 @@ int launch_sdpa_merge_bf16(const SdpaArgs& a, int D, hipStream_t s);
 int launch_sdpa_merge_f32(const SdpaArgs& a, int D, hipStream_t s);
 
 // Fused GDA decode step (attention + merge/epilogue launches); the f16 and
-// bf16 instances have kernels (head_dim 128; the packed-cache step only
-// f16), the others return MOTIF_ERR_UNSUPPORTED.
+// bf16 instances have kernels (head_dim 128), the others return
+// MOTIF_ERR_UNSUPPORTED.
 int launch_gda_decode_f16(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t s);
 int launch_gda_decode_bf16(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t s);
 int launch_gda_decode_f32(const SdpaArgs& a, int gc, int waves, int nblocks, hipStream_t s);

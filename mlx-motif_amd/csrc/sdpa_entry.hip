@@ -841,7 +841,8 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
                                (uintptr_t)k2_scales | (uintptr_t)k2_biases |
                                (uintptr_t)v1_scales | (uintptr_t)v1_biases |
                                (uintptr_t)v2_scales | (uintptr_t)v2_biases;
-  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && G1 + G2 <= 16 &&
+  const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
+                     G1 + G2 <= 16 &&
                      gc * ng <= 16 && (data_bits & 15u) == 0 &&
                      (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
                      kv_len <= kMfmaMaxRows && aligned(q1, 16) && aligned(q2, 16) &&
@@ -863,7 +864,9 @@ static int gda_decode_q(const char* name, const void* q1, const void* q2,
     }
     rc = check_partials(name, a, true);
     if (rc != MOTIF_OK) return rc;
-    return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit), s);
+    const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+    return dtype == MOTIF_F16 ? launch_gda_decode_q_f16(a, bits, gc, nblocks, s)
+                              : launch_gda_decode_q_bf16(a, bits, gc, nblocks, s);
   }
   if (new_kv) {
     uint32_t* const data[4] = {const_cast<uint32_t*>(k1_data), const_cast<uint32_t*>(k2_data),
@@ -992,7 +995,8 @@ int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const
                                (uintptr_t)k2_scales | (uintptr_t)k2_biases |
                                (uintptr_t)v1_scales | (uintptr_t)v1_biases |
                                (uintptr_t)v2_scales | (uintptr_t)v2_biases;
-  const bool fused = dtype == MOTIF_F16 && D == 128 && tuning().mfma && gr + 1 <= 16 &&
+  const bool fused = (dtype == MOTIF_F16 || dtype == MOTIF_BF16) && D == 128 && tuning().mfma &&
+                     gr + 1 <= 16 &&
                      gc * ng <= 16 && (data_bits & 15u) == 0 &&
                      (scale_bits & (ng == 1 ? 7u : 15u)) == 0 && kv_cap % 4 == 0 &&
                      kv_len <= kMfmaMaxRows && aligned(q_proj, 16) && aligned(k_proj, 16) &&
@@ -1018,8 +1022,9 @@ int motif_gda_decode_q_proj_scaled(const void* q_proj, const void* k_proj, const
   a.rope_pos_scale = position_scale;
   rc = check_partials(name, a, true);
   if (rc != MOTIF_OK) return rc;
-  return launch_gda_decode_q_f16(a, bits, gc, sdpa_grid_blocks(B * Hkv, 1, a.nsplit),
-                                 (hipStream_t)stream);
+  const int nblocks = sdpa_grid_blocks(B * Hkv, 1, a.nsplit);
+  return dtype == MOTIF_F16 ? launch_gda_decode_q_f16(a, bits, gc, nblocks, (hipStream_t)stream)
+                            : launch_gda_decode_q_bf16(a, bits, gc, nblocks, (hipStream_t)stream);
 }
 
 int motif_gda_decode_q_proj(const void* q_proj, const void* k_proj, const void* v_proj,

@@ -150,10 +150,10 @@ int MOTIF_CAT(launch_gda_prefill_proj_, MOTIF_SUFFIX)(const SdpaArgs& a, int wav
 // Same over the packed q4/q8 cache (fp16 scales, head_dim 128).
 int MOTIF_CAT(launch_gda_decode_q_, MOTIF_SUFFIX)(const SdpaArgs& a, int bits, int gc, int nblocks,
                                                  hipStream_t s) {
-  if constexpr (std::is_same<MOTIF_ELEM, half_t>::value) {
-    const int rc = launch_gda_decode_mfma_q(a, bits, a.group_size, gc, nblocks, s);
+  if constexpr (!std::is_same<MOTIF_ELEM, float>::value) {  // fp16 and bf16
+    const int rc = launch_gda_decode_mfma_q<MOTIF_ELEM>(a, bits, a.group_size, gc, nblocks, s);
     if (rc != MOTIF_OK) return rc;
-    return launch_gda_decode_merge_d<half_t, 128>(a, s);
+    return launch_gda_decode_merge_d<MOTIF_ELEM, 128>(a, s);
   }
   set_error("gda_decode_q: no fused variant for this element type");
   return MOTIF_ERR_UNSUPPORTED;

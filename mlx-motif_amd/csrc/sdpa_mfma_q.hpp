@@ -217,8 +217,9 @@ __device__ inline void drop_rows_past(uint32_t (&out)[2], unsigned row0, unsigne
 
 // Packed rows: lane L quantises chunk L % 16 (8 values) of slot L / 16 (k1,
 // k2, v1, v2) of the new token exactly as motif_quant_write4 does, and
-// stores the codes, scale and bias at row kv_len - 1 of KV head bk.
-template <int BITS, int GS>
+// stores the codes, scale and bias at row kv_len - 1 of KV head bk.  E:
+// element type of the new rows, scales and biases.
+template <int BITS, int GS, typename E = half_t>
 __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
   constexpr int D = 128;
   constexpr int LPG = GS / 8;
@@ -233,13 +234,12 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
   if (!a.from_proj) {
     const void* src =
         slot == 0 ? a.new_k1 : slot == 1 ? a.new_k2 : slot == 2 ? a.new_v1 : a.new_v2;
-    load8<half_t>(src, bk * D + (long)chunk * 8, v);
+    load8<E>(src, bk * D + (long)chunk * 8, v);
   } else {
     // From the projections: head 2 * kvh + (slot & 1), row 2 * bk + (slot & 1);
-    // k rows are roped (pair partner in lane L ^ 8) and rounded to fp16 as
+    // k rows are roped (pair partner in lane L ^ 8) and rounded to E as
     // rope_split4 stores them, then quantised.
-    load8<half_t>(slot < 2 ? a.new_k1 : a.new_v1, (2 * bk + (slot & 1)) * D + (long)chunk * 8,
-                  v);
+    load8<E>(slot < 2 ? a.new_k1 : a.new_v1, (2 * bk + (slot & 1)) * D + (long)chunk * 8, v);
     // Lane L computes the angle of pair L (0..63) once; the lanes read the
     // eight they need with __shfl (one slow-path sincosf per lane, not eight).
     const bool first = chunk < 8;
@@ -252,7 +252,7 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
       const float sn = __shfl(sn0, 8 * (chunk & 7) + e);
       float y1, y2;
       rope_rotate(first ? v[e] : other, first ? other : v[e], cs, sn, y1, y2);
-      const float y = (float)(half_t)(first ? y1 : y2);
+      const float y = Elem<E>::to_f32(Elem<E>::from_f32(first ? y1 : y2));
       if (slot < 2) v[e] = y;
     }
   }
@@ -262,8 +262,8 @@ __device__ inline void append_rows_q(const SdpaArgs& a, long bk, int lane) {
   const long crow = bk * a.kv_cap + a.kv_len - 1;
   store_words<BITS>(const_cast<uint32_t*>(data), crow * WPR + (long)chunk * (8 * BITS / 32), w);
   if (chunk % LPG == 0) {
-    Elem<half_t>::store(const_cast<void*>(sc), crow * NG + chunk / LPG, scale);
-    Elem<half_t>::store(const_cast<void*>(bi), crow * NG + chunk / LPG, bias);
+    Elem<E>::store(const_cast<void*>(sc), crow * NG + chunk / LPG, scale);
+    Elem<E>::store(const_cast<void*>(bi), crow * NG + chunk / LPG, bias);
   }
 }
 
@@ -300,7 +300,6 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
   static_assert(GC * NG <= 16, "heads x groups ride the 16 MFMA columns");
   static_assert(!DUAL || NB == 1, "the fused decode step uses one column block");
   constexpr bool kBf16 = std::is_same<E, bf16_t>::value;
-  static_assert(!(DUAL && kBf16), "the fused packed decode step takes fp16 activations");
   // Lazy-rescale slack (see kRescaleSlackF16): here p also multiplies the V
   // scale in fp16, so p * s must stay finite.  An fp16 cache row spans at
   // most 2 * 65504, so s <= 131008 / 15 (q4) or / 255 (q8), and 2^slack * s
@@ -377,7 +376,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     owner = append_owner<NW>(a, split, wave);
 #pragma unroll
     for (int u = 0; u < U; ++u) append_early |= tile_row(u) == append_tile;
-    if (owner && append_early) append_rows_q<BITS, GS>(a, bk, lane);
+    if (owner && append_early) append_rows_q<BITS, GS, E>(a, bk, lane);
   }
 
   // All loads of this wave's tiles k0 .. k0 + U - 1 (rows past max_lim read 0).
@@ -472,11 +471,11 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
             const int p = 32 * (blk & 1) + 8 * s + 2 * i + e;
             const float cs = __shfl(cs0, p);
             const float sn = __shfl(sn0, p);
-            const float mine = (float)__builtin_bit_cast(half_t, (uint16_t)(e ? w[i] >> 16 : w[i] & 0xFFFFu));
-            const float oth = (float)__builtin_bit_cast(half_t, (uint16_t)(e ? o >> 16 : o & 0xFFFFu));
+            const float mine = Elem<E>::to_f32((uint16_t)(e ? w[i] >> 16 : w[i] & 0xFFFFu));
+            const float oth = Elem<E>::to_f32((uint16_t)(e ? o >> 16 : o & 0xFFFFu));
             float y1, y2;
             rope_rotate(first ? mine : oth, first ? oth : mine, cs, sn, y1, y2);
-            r |= (uint32_t)__builtin_bit_cast(uint16_t, (half_t)(first ? y1 : y2)) << (16 * e);
+            r |= (uint32_t)Elem<E>::from_f32(first ? y1 : y2) << (16 * e);
           }
           w[i] = r;
         }
@@ -486,7 +485,7 @@ sdpa_mfma_q_kernel(SdpaArgs a) {
     // The deferred append comes after the q RoPE: its loads would otherwise
     // make every wave's RoPE wait for the first tiles (register reuse
     // across the branch).
-    if (owner && !append_early) append_rows_q<BITS, GS>(a, bk, lane);
+    if (owner && !append_early) append_rows_q<BITS, GS, E>(a, bk, lane);
   }
 
   // bf16 activations: each head's q is scaled by 2^-e, e the smallest >= 0
@@ -872,8 +871,9 @@ int launch_sdpa_mfma_q_gs(const SdpaArgs& a, int gc, int waves, int nblocks, hip
 }
 
 // Fused GDA decode step over the packed cache: gc columns per scale group
-// (G + G2 rounded up to a power of two, gc * 128 / gs <= 16), 4 waves.
-template <int BITS, int GS>
+// (G + G2 rounded up to a power of two, gc * 128 / gs <= 16), 4 waves; E the
+// element type of q, the new rows, the scales and biases and y.
+template <int BITS, int GS, typename E = half_t>
 int launch_gda_decode_mfma_q_gs(const SdpaArgs& a, int gc, int nblocks, hipStream_t st) {
   constexpr int NG = 128 / GS;
   constexpr int P = kCachePolicyStream;
@@ -882,30 +882,31 @@ int launch_gda_decode_mfma_q_gs(const SdpaArgs& a, int gc, int nblocks, hipStrea
     return MOTIF_ERR_UNSUPPORTED;
   }
   if (gc == 2) {
-    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 2, 4, 1, P, true, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
   } else if (gc == 4) {
     if constexpr (4 * NG <= 16)
-      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 4, 4, 1, P, true, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
   } else if (gc == 8) {
     if constexpr (8 * NG <= 16)
-      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 8, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 8, 4, 1, P, true, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
   } else {
     if constexpr (16 * NG <= 16)
-      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 16, 4, 1, P, true>), dim3(nblocks), dim3(256), 0, st, a);
+      hipLaunchKernelGGL((sdpa_mfma_q_kernel<BITS, GS, 16, 4, 1, P, true, 1, E>), dim3(nblocks), dim3(256), 0, st, a);
   }
   return check_launch("gda_decode_q (mfma)");
 }
 
+template <typename E = half_t>
 inline int launch_gda_decode_mfma_q(const SdpaArgs& a, int bits, int gs, int gc, int nblocks,
                                     hipStream_t st) {
   if (bits == 4) {
-    if (gs == 32) return launch_gda_decode_mfma_q_gs<4, 32>(a, gc, nblocks, st);
-    if (gs == 64) return launch_gda_decode_mfma_q_gs<4, 64>(a, gc, nblocks, st);
-    return launch_gda_decode_mfma_q_gs<4, 128>(a, gc, nblocks, st);
+    if (gs == 32) return launch_gda_decode_mfma_q_gs<4, 32, E>(a, gc, nblocks, st);
+    if (gs == 64) return launch_gda_decode_mfma_q_gs<4, 64, E>(a, gc, nblocks, st);
+    return launch_gda_decode_mfma_q_gs<4, 128, E>(a, gc, nblocks, st);
   }
-  if (gs == 32) return launch_gda_decode_mfma_q_gs<8, 32>(a, gc, nblocks, st);
-  if (gs == 64) return launch_gda_decode_mfma_q_gs<8, 64>(a, gc, nblocks, st);
-  return launch_gda_decode_mfma_q_gs<8, 128>(a, gc, nblocks, st);
+  if (gs == 32) return launch_gda_decode_mfma_q_gs<8, 32, E>(a, gc, nblocks, st);
+  if (gs == 64) return launch_gda_decode_mfma_q_gs<8, 64, E>(a, gc, nblocks, st);
+  return launch_gda_decode_mfma_q_gs<8, 128, E>(a, gc, nblocks, st);
 }
 
 // Two column blocks of GC = 16 / groups (at most 8) heads per wave, one

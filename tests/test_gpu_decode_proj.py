@@ -84,16 +84,18 @@ def test_decode_proj_matches_oracle(gpu):
     assert float(err.mean()) <= 0.1 * float(tol.mean()) + 1e-6
 
 
-@pytest.mark.parametrize("bits,gs,gr,cap,offset,origin_first", [
-    (4, 64, 4, 256, 0, False),
-    (4, 64, 4, 3328, 3203, False),
-    (8, 64, 4, 16128, 15999, True),
-    (4, 32, 3, 300, 250, False),     # 4 columns x 4 groups
-    (8, 128, 15, 512, 300, False),   # 16 columns x 1 group
-    (4, 32, 4, 256, 100, False),     # 32 columns: rope_split4 + the step
+@pytest.mark.parametrize("bits,gs,gr,cap,offset,origin_first,tag", [
+    (4, 64, 4, 256, 0, False, "f16"),
+    (4, 64, 4, 3328, 3203, False, "f16"),
+    (8, 64, 4, 16128, 15999, True, "f16"),
+    (4, 32, 3, 300, 250, False, "f16"),     # 4 columns x 4 groups
+    (8, 128, 15, 512, 300, False, "f16"),   # 16 columns x 1 group
+    (4, 32, 4, 256, 100, False, "f16"),     # 32 columns: rope_split4 + the step
+    (4, 64, 4, 640, 600, False, "bf16"),
+    (8, 64, 4, 3328, 3203, True, "bf16"),
 ])
 def test_decode_q_proj_equals_rope_split4_then_step(gpu, bits, gs, gr, cap, offset,
-                                                    origin_first):
+                                                    origin_first, tag):
     """Packed cache: rows quantised after RoPE exactly as rope_split4 +
     the append step writes them, and the same output bit for bit."""
     import torch
@@ -102,10 +104,11 @@ def test_decode_q_proj_equals_rope_split4_then_step(gpu, bits, gs, gr, cap, offs
                                    quantize, rope_split4)
 
     Hkv = 8 if gr <= 4 else 2
-    qp, kp, vp, raw, w, lam = _inputs(gpu, 1, Hkv, gr, cap, torch.float16, offset + bits)
+    dt = torch.float16 if tag == "f16" else torch.bfloat16
+    qp, kp, vp, raw, w, lam = _inputs(gpu, 1, Hkv, gr, cap, dt, offset + bits)
     slots = [quantize(t, gs, bits) for t in raw]
     ref_slots = [tuple(x.clone() for x in t) for t in slots]
-    print(f"decode_q_proj bits={bits} gs={gs} gr={gr} offset={offset}", flush=True)
+    print(f"decode_q_proj bits={bits} gs={gs} gr={gr} offset={offset} {tag}", flush=True)
     y = gda_decode_attention_q4_from_proj(qp, kp, vp, *slots, 0.0884, w, lam, 0.2, gr, offset,
                                           gs, bits, origin_first=origin_first)
     q1, q2, *rows = rope_split4(qp, kp, vp, Hkv, gr, Hkv, 1, offset, origin_first=origin_first)

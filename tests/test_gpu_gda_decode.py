@@ -243,6 +243,22 @@ def test_fused_decode_q_poisoned_padding_and_bf16(gpu, rng):
     assert _run_q(gpu, rng, 1, 4, 4, 256, 150, 128, 8, 64, "bf16") <= 0
 
 
+@pytest.mark.parametrize("bits,gs,gr,kv_len", [
+    (4, 64, 4, 1), (4, 64, 4, 300), (8, 64, 4, 3204), (4, 128, 4, 3204),
+    (4, 32, 3, 300),    # 4 columns x 4 groups
+    (8, 128, 15, 385),  # 16 columns x 1 group
+])
+def test_fused_decode_q_bf16(gpu, rng, bits, gs, gr, kv_len):
+    """bf16 activations, scales and biases on the fused packed step: q
+    scaled per head by a power of two into fp16 for the products, the K
+    scale and bias terms in fp32 (one wave per SIMD)."""
+    cap = (kv_len + 255) // 256 * 256
+    Hkv = 8 if gr <= 4 else 2
+    print(f"gda_decode_q bf16 bits={bits} gs={gs} gr={gr} kv_len={kv_len}", flush=True)
+    excess = _run_q(gpu, rng, 1, Hkv, gr, cap, kv_len, 128, bits, gs, "bf16")
+    assert excess <= 0, f"bits={bits} gs={gs} gr={gr} kv_len={kv_len}: exceeds the bar by {excess:.3e}"
+
+
 # ---------------------------------------------------------- append (write) ---
 def _append_inputs(gpu, B, Hkv, gr, cap, D, dt, seed):
     import torch
@@ -331,7 +347,8 @@ def test_append_matches_oracle_step(gpu, rng):
     (4, 32, 3, 300, 300, "f16"),      # 4 columns x 4 groups
     (8, 128, 15, 512, 385, "f16"),    # 16 columns x 1 group
     (4, 32, 4, 256, 200, "f16"),      # 32 columns: composed (quant_write4 first)
-    (8, 64, 4, 256, 150, "bf16"),     # composed: bf16
+    (8, 64, 4, 256, 150, "bf16"),     # bf16 on the fused kernel
+    (4, 64, 4, 3328, 3204, "bf16"),
 ])
 def test_append_q_quantises_row_then_attends(gpu, bits, gs, gr, cap, kv_len, tag):
     """Packed cache: the token's rows are quantised into row kv_len - 1

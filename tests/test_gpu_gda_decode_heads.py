@@ -265,7 +265,7 @@ def test_packed_columns_and_groups(gpu, rng, Hkv, G1, G2, gs):
     assert excess <= 0, f"{(Hkv, G1, G2, gs)}: exceeds the bar by {excess:.3e}"
 
 
-def test_packed_bf16_composes(gpu, rng):
+def test_packed_bf16(gpu, rng):
     assert _run_q(gpu, rng, 1, 4, 2, 2, 256, 150, 8, 64, "bf16") <= 0
 
 
