@@ -342,9 +342,10 @@ int motif_gda_decode(const void* q1, const void* q2, const void* k1, const void*
 /* Same step over the packed MLX-affine q4/q8 cache (QUANT_SDPA path of
  * model.py:717-748: two sdpa_dual_v_q4 calls + gda_post_split).  Each slot is
  * a (data, scales, biases) triple laid out as for motif_sdpa_dual_v_q.  The
- * fused launch covers fp16 scales at D = 128 when (gr + 1) rounded up to a
- * power of two, times D / group_size, is at most 16; other shapes compose
- * the separate calls on the device.  Contract as motif_sdpa_dual_v_q. */
+ * fused launch covers fp16 and bf16 activations, scales and biases at D = 128
+ * when (gr + 1) rounded up to a power of two, times D / group_size, is at
+ * most 16; other shapes compose the separate calls on the device.  Contract
+ * as motif_sdpa_dual_v_q. */
 int motif_gda_decode_q(const void* q1, const void* q2, const uint32_t* k1_data,
                        const void* k1_scales, const void* k1_biases, const uint32_t* k2_data,
                        const void* k2_scales, const void* k2_biases, const uint32_t* v1_data,
