@@ -3,11 +3,11 @@
 The reference's kernels take any float ``scale`` (attention.py:190-260,
 510-645): q is scaled first, then the running maximum is taken over the
 scaled scores.  The build's tile-softmax kernels (shared-tile prefill/slab,
-packed slab, paired-tile q4 decode, fused prefill chunk) take the maximum
+packed slab, paired-tile decode, fused prefill chunk) take the maximum
 over unscaled scores, which is only right for a positive scale; calls with
 any other scale are routed to the per-tile kernels.  These tests run the
 shapes that take each of those routes with scale -1/sqrt(128) and 0 and
-hold the outputs to the oracle (fp16, max-abs 2e-3).  Scale 0 gives every
+hold the outputs to the oracle (fp16 max-abs 2e-3, bf16 1e-2).  Scale 0 gives every
 visible key the same weight: y is the mean of the visible V rows.
 """
 
@@ -49,33 +49,39 @@ def test_fp16_rows(gpu, rng, scale, S_q, G, kv_len):
     assert np.all(np.isfinite(torch_to_np(y))) and err <= TOL, err
 
 
-def _packed(rng, B, Hkv, cap, D, bits):
-    return [O.quantize(randn(rng, (B, Hkv, cap, D), "f16"), 64, bits) for _ in range(3)]
+def _packed(rng, B, Hkv, cap, D, bits, tag="f16"):
+    return [O.quantize(randn(rng, (B, Hkv, cap, D), tag), 64, bits, out_dtype=tag)
+            for _ in range(3)]
 
 
-def _gpu_trip(trip, gpu):
+def _gpu_trip(trip, gpu, tag="f16"):
     import torch
 
+    dt = torch.float16 if tag == "f16" else torch.bfloat16
     d, s, b = trip
-    return (np_to_torch(d, None, gpu), np_to_torch(s, torch.float16, gpu),
-            np_to_torch(b, torch.float16, gpu))
+    return (np_to_torch(d, None, gpu), np_to_torch(s, dt, gpu), np_to_torch(b, dt, gpu))
 
 
 @pytest.mark.parametrize("scale", SCALES)
 @pytest.mark.parametrize("bits", [4, 8])
-def test_packed_decode(gpu, rng, scale, bits):
-    """q4 decode at group size 64 (the paired-tile route for a positive
-    scale) and q8 (per-tile) over 5000 rows, 32 heads over 8."""
+@pytest.mark.parametrize("tag", ["f16", "bf16"])
+def test_packed_decode(gpu, rng, scale, bits, tag):
+    """q4/q8 decode at group size 64 over 5000 rows, 32 heads over 8:
+    fp16 (per-tile kernel) and bf16 (q4: the paired-tile route for a
+    positive scale; q8: per-tile)."""
+    import torch
+
     from mlx_motif.kernels import sdpa_dual_v_q4
 
     B, Hq, Hkv, D, kv_len, cap = 1, 32, 8, 128, 5000, 5120
-    q = randn(rng, (B, Hq, 1, D), "f16")
-    kq, v1q, v2q = _packed(rng, B, Hkv, cap, D, bits)
-    y = sdpa_dual_v_q4(_t(q, gpu), _gpu_trip(kq, gpu), _gpu_trip(v1q, gpu), _gpu_trip(v2q, gpu),
-                       scale, group_size=64, bits=bits, kv_len=kv_len)
+    dt = torch.float16 if tag == "f16" else torch.bfloat16
+    q = randn(rng, (B, Hq, 1, D), tag)
+    kq, v1q, v2q = _packed(rng, B, Hkv, cap, D, bits, tag)
+    y = sdpa_dual_v_q4(np_to_torch(q, dt, gpu), _gpu_trip(kq, gpu, tag), _gpu_trip(v1q, gpu, tag),
+                       _gpu_trip(v2q, gpu, tag), scale, group_size=64, bits=bits, kv_len=kv_len)
     ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, scale, 64, bits, kv_len)
     err = float(np.max(np.abs(torch_to_np(y) - ref)))
-    assert np.all(np.isfinite(torch_to_np(y))) and err <= TOL, err
+    assert np.all(np.isfinite(torch_to_np(y))) and err <= (TOL if tag == "f16" else 1e-2), err
 
 
 @pytest.mark.parametrize("scale", SCALES)
