@@ -1,5 +1,6 @@
 // Matrix-core formulation of split-KV dual-V decode over the packed
-// MLX-affine cache (q4 / q8, head_dim 128, fp16 scales and biases).
+// MLX-affine cache (q4 / q8, head_dim 128; fp16 or bf16 q, scales, biases
+// and outputs, the products fp16 MFMAs either way).
 //
 // Dequantised value = s * u + b with u the unsigned code, (s, b) per row and
 // group of gs channels.  Both products are split so that the matrix cores
