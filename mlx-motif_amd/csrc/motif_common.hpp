@@ -45,7 +45,7 @@ struct Tuning {
   int qslab_sets = 2;      // producer register sets of the producer / consumer slab kernel (2 or 3)
   int prefill_ncb = 0;     // column blocks per wave of the 8-wave prefill kernel (0 = automatic)
   int prefill_min_heads = 0;  // virtual heads per KV head from which multi-row fp16/bf16 calls take the shared-tile kernel (0: automatic)
-  int part_f16 = 1;       // shared-tile kernels' split partials as fp16 o / l when the row-per-wave merge reads them: 1 on, 0 fp32
+  int part_f16 = 1;       // shared-tile kernels' split partials over fp16 caches as fp16 o / l when the row-per-wave merge reads them: 1 on, 0 fp32
 };
 // The calling thread's snapshot of the process-wide knobs.  Inside a
 // CallScope it is the copy taken when the outermost scope opened, so every

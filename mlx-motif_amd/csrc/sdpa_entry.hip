@@ -187,7 +187,7 @@ static int sdpa_fp_run(const char* name, const void* q, const void* k, const voi
                           counter_reserve);
       if (rc != MOTIF_OK) return rc;
     }
-    a.part_f16 = use_part_f16((long)B * Hq * S_q, pp.nsplit) ? 1 : 0;
+    a.part_f16 = use_part_f16((long)B * Hq * S_q, pp.nsplit, dtype == MOTIF_F16) ? 1 : 0;
     rc = check_partials(name, a, false);
     if (rc != MOTIF_OK) return rc;
     const int nblocks = sdpa_grid_blocks(B * Hkv, pp.nqb, pp.nsplit);
@@ -1128,7 +1128,8 @@ int motif_gda_prefill_proj_scaled(const void* q_proj, const void* k_proj, const 
                                   (size_t)B * (Hq_o + q_groups) * S, pp.nsplit, D, 0);
     if (rc != MOTIF_OK) return rc;
   }
-  a.part_f16 = use_part_f16((long)B * (Hq_o + q_groups) * S, pp.nsplit) ? 1 : 0;
+  a.part_f16 =
+      use_part_f16((long)B * (Hq_o + q_groups) * S, pp.nsplit, dtype == MOTIF_F16) ? 1 : 0;
   int rc = check_partials(name, a, false);
   if (rc != MOTIF_OK) return rc;
   hipStream_t s = (hipStream_t)stream;

@@ -199,9 +199,12 @@ constexpr int kMfmaMaxRows = 1 << 22;
 // wave per row (tuning merge_rows) instead of one wave per row slice.
 constexpr int kMergeRowsMin = 2048;
 // The shared-tile kernels store split partials as fp16 o / l (SdpaArgs::
-// part_f16) when the row-per-wave merge will read them.
-inline bool use_part_f16(long rows, int nsplit) {
-  return nsplit > 1 && rows >= kMergeRowsMin && tuning().merge_rows && tuning().part_f16;
+// part_f16) when the row-per-wave merge will read them, over fp16 caches
+// only: o / l is a convex combination of the V rows, within fp16 range for
+// an fp16 cache but not for a bf16 one (those keep fp32 partials).
+inline bool use_part_f16(long rows, int nsplit, bool f16_cache) {
+  return nsplit > 1 && f16_cache && rows >= kMergeRowsMin && tuning().merge_rows &&
+         tuning().part_f16;
 }
 
 // The tile-softmax kernels (shared-tile prefill and slab kernels, the packed

@@ -181,3 +181,30 @@ def test_fp16_split_partials(gpu, rng, S, cap, kv_len, tag):
     assert float(np.max(np.abs(torch_to_np(y2) - ref))) <= (2e-3 if tag == "f16" else 1e-2)
     d = float(np.max(np.abs(torch_to_np(y) - torch_to_np(y2))))
     assert d <= (1e-3 if tag == "f16" else 8e-3), f"{d:.3e}"
+
+
+def test_bf16_split_partials_beyond_fp16_range(gpu, rng):
+    """Split partials over a bf16 cache stay fp32: o / l is a convex
+    combination of V rows, which a bf16 cache may hold beyond fp16's 65504
+    (here V = 2e5 + N(0, 1e4^2), so every output is near 2e5), where fp16
+    partials would read inf.  2048 partial rows (the row-per-wave merge) over
+    16 splits; the bf16 bar scales with the V magnitude."""
+    import torch
+
+    from mlx_motif.kernels import sdpa_dual_v_rows
+
+    S, cap, kv_len, D, vs = 64, 3328, 3204, 128, 2.5e5
+    q = randn(rng, (1, 32, S, D), "bf16")
+    k = randn(rng, (1, 8, cap, D), "bf16")
+    v1, v2 = (O.round_to(randn(rng, (1, 8, cap, D), "f32", 1e4) + np.float32(2e5),
+                         "bf16").astype(np.float32) for _ in range(2))
+    T = lambda a: np_to_torch(a, torch.bfloat16, gpu)  # noqa: E731
+    print(f"bf16 prefill S={S} kv_len={kv_len} v ~ 2e5", flush=True)
+    y = sdpa_dual_v_rows(T(q), T(k), T(v1), T(v2), 1 / np.sqrt(D), kv_len=kv_len, causal=True)
+    torch.cuda.synchronize()
+    got = torch_to_np(y)
+    ref = O.sdpa_dual_v(q, k, v1, v2, 1 / np.sqrt(D), kv_len, True)
+    assert np.isfinite(got).all()
+    assert float(np.min(np.abs(ref))) > 65504  # every output lies past fp16's range
+    err = float(np.max(np.abs(got - ref)))
+    assert err <= 1e-2 * vs, f"{err:.3e}"
