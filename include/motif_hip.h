@@ -111,6 +111,11 @@ int motif_sdpa_dual_v_noalloc(const void* q, const void* k, const void* v1, cons
  * Contract (attention.py:556-608): bits in {4,8}, D % 32 == 0,
  * D % group_size == 0, (32/bits) % (D/32) == 0, group_size % (D/32) == 0,
  * Hq % Hkv == 0, 0 <= kv_len <= kv_cap.
+ * MOTIF_BF16 at D = 128 runs on fp16 matrix cores, whose softmax weights
+ * carry the V scales in fp16: V scales must stay below 16376 (bits 4) or
+ * 1023 (bits 8), i.e. V groups spanning less than ~2.4e5, or the output is
+ * not finite (an fp16 cache always holds them; bf16 caches beyond them take
+ * motif_set_tuning("mfma", 0)).
  * ------------------------------------------------------------------------ */
 int motif_sdpa_dual_v_q(const void* q,
                         const uint32_t* k_data, const void* k_scales, const void* k_biases,
