@@ -358,3 +358,48 @@ def test_bf16_q_beyond_fp16_range(gpu, rng, bits, mode):
     got = torch_to_np(y)
     assert np.isfinite(got).all()
     assert np.max(np.abs(got - ref)) <= TOL["bf16"], np.max(np.abs(got - ref))
+
+
+@pytest.mark.parametrize("bits,mode,sigma", [
+    (4, "tile", 2e4), (4, "pair", 2e4), (4, "valu", 2e4),
+    (8, "tile", 2.5e4), (8, "pair", 2.5e4), (8, "valu", 2.5e4),
+    (4, "valu", 1e6), (8, "valu", 1e6),
+])
+def test_bf16_large_v_scales(gpu, rng, bits, mode, sigma):
+    """bf16 V far beyond fp16's range.  The matrix-core kernels carry the V
+    scales in fp16 inside the softmax weights p * s (p <= 2^2 for q4, 2^6 for
+    q8), which holds for scales below 16376 (q4) / 1023 (q8): V ~ N(0, sigma^2)
+    with scales up to ~1.3e4 (q4) and ~8e2 (q8) -- past what an fp16 cache can
+    hold for q8 -- must stay finite and within the bf16 bar scaled by sigma.
+    Beyond that limit (sigma 1e6) the VALU kernels (mfma 0) take every scale
+    in fp32."""
+    import torch
+
+    from mlx_motif import _native
+    from mlx_motif.kernels import sdpa_dual_v_q4
+
+    B, Hq, Hkv, D, cap, kv_len, gs = 1, 32, 8, 128, 2048, 2000, 64
+    q = randn(rng, (B, Hq, 1, D), "bf16")
+    k = randn(rng, (B, Hkv, cap, D), "bf16")
+    v1, v2 = (randn(rng, (B, Hkv, cap, D), "bf16", sigma) for _ in range(2))
+    kq, v1q, v2q = (_quant(t, gs, bits, "bf16") for t in (k, v1, v2))
+    smax = max(float(np.max(np.abs(t[1][..., :kv_len, :]))) for t in (v1q, v2q))
+    if mode != "valu":
+        assert smax < (16376 if bits == 4 else 1023), smax  # the kernels' stated range
+    scale = 1.0 / np.sqrt(D)
+    print(f"bf16 q{bits} {mode} sigma={sigma:g} max V scale {smax:.4g}", flush=True)
+    for key, value in _BF16_MODES[mode]:
+        _native.set_tuning(key, value)
+    try:
+        y = sdpa_dual_v_q4(np_to_torch(q, torch.bfloat16, gpu), _to_gpu(kq, "bf16", gpu),
+                           _to_gpu(v1q, "bf16", gpu), _to_gpu(v2q, "bf16", gpu), scale,
+                           group_size=gs, bits=bits, kv_len=kv_len)
+        torch.cuda.synchronize()
+    finally:
+        _native.set_tuning("qpair", 1)
+        _native.set_tuning("mfma", 1)
+    ref = O.sdpa_dual_v_q(q, kq, v1q, v2q, scale, gs, bits, kv_len)
+    got = torch_to_np(y)
+    assert np.isfinite(got).all()
+    err = float(np.max(np.abs(got - ref)))
+    assert err <= TOL["bf16"] * sigma, f"{err:.3e}"
