@@ -527,10 +527,7 @@ int motif_polynorm(const void* x, const void* weight, const void* bias, void* y,
  * shared-tile kernel from 64 virtual heads per KV head, or from 17 over 2048
  * or more rows; n > 0: from n heads),
  * "poly_rows" (workgroups per CU of the persistent PolyNorm kernel for 16-bit
- * rows of 2056..16384 values; 0, the default, sizes it by register use),
- * "part_f16" (1, the default: the shared-tile kernels' split partials over
- * fp16 caches are fp16 o / l when the row-per-wave merge reads them; bf16
- * caches always keep fp32 partials; 0: fp32 partials).
+ * rows of 2056..16384 values; 0, the default, sizes it by register use).
  * Returns MOTIF_OK or MOTIF_ERR_CONTRACT for an unknown key or value.
  * ------------------------------------------------------------------------ */
 int motif_set_tuning(const char* key, int value);
